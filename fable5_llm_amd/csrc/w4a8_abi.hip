@@ -1,0 +1,700 @@
+// C ABI of the W4A8 engine (include/fable5_w4a8.h).
+//
+// Host side of the path: contexts (one HIP stream each), device-resident
+// weights repacked once from the reference's row image, staging for the
+// host-buffer entry points, and the reference's assertion classes mapped to
+// status codes.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/fable5_w4a8.h"
+#include "w4a8_internal.h"
+
+using namespace w4a8;
+
+struct w4a8_ctx {
+  int device = 0;
+  hipStream_t own = nullptr;
+  hipStream_t stream = nullptr;
+  int num_cu = 0;
+  int grid = 0;            // persistent GEMV grid
+  int grid_override = 0;
+  int32_t *d_tables = nullptr;
+  int32_t *d_err = nullptr;
+  uint64_t *d_partials = nullptr;
+  int partials_cap = 0;
+  int32_t *d_result = nullptr;   // head argmax {idx, val}
+  uint8_t *d_stage = nullptr;
+  size_t stage_cap = 0;
+  int32_t h_tables[kTableLen];
+};
+
+struct w4a8_weights {
+  w4a8_ctx *ctx = nullptr;
+  uint8_t *d = nullptr;
+  int64_t nrows = 0;
+  int64_t ntiles = 0;
+  int32_t sh = 0;
+  Layout L{};
+  size_t bytes = 0;
+};
+
+static thread_local std::string g_err;
+
+static int fail(int code, const std::string &msg) {
+  g_err = msg;
+  return code;
+}
+
+#define HIP_TRY(expr)                                                        \
+  do {                                                                       \
+    hipError_t e_ = (expr);                                                  \
+    if (e_ != hipSuccess)                                                    \
+      return fail(W4A8_E_HIP, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+  } while (0)
+
+namespace {
+
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != dev) (void)hipSetDevice(dev);
+  }
+  ~DeviceGuard() {
+    int cur = -1;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev)
+      (void)hipSetDevice(prev);
+  }
+};
+
+int64_t wire_stride(int32_t K) {
+  const int ng = K / kGroup;
+  return (int64_t)(ng + (ng + 31) / 32) * 64;
+}
+
+// K legality and the engine envelope (w4a8_ref.py:104-105; hwmap.py:146-169)
+int check_k_sh(int32_t K, int32_t sh) {
+  if (K <= 0 || K % kGroup)
+    return fail(W4A8_E_SHAPE, "K=" + std::to_string(K) + " must be a multiple of 128");
+  if (K / kGroup > kNgMax)
+    return fail(W4A8_E_ENVELOPE, "ng=" + std::to_string(K / kGroup) +
+                                     " outside the engine envelope 1..96");
+  if (sh < 0 || sh > 63)
+    return fail(W4A8_E_ENVELOPE, "sh=" + std::to_string(sh) + " outside 0..63");
+  return W4A8_OK;
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+void build_tables(int32_t *t) {
+  // fixedpoint.py:42-53: round(2^15 / sqrt(mid)), 256 midpoints over [1,2)
+  // then 256 over [2,4).  sqrt is correctly rounded and nearbyint rounds
+  // half to even like numpy.round.
+  for (int i = 0; i < 256; ++i) {
+    t[kRsqrtOff + i] = (int32_t)std::nearbyint(32768.0 / std::sqrt(1.0 + (i + 0.5) / 256.0));
+    t[kRsqrtOff + 256 + i] =
+        (int32_t)std::nearbyint(32768.0 / std::sqrt(2.0 + (i + 0.5) / 128.0));
+  }
+  // fixedpoint.py:128-142: sigmoid knots over [-16, 16], Q15, max 32767
+  for (int i = 0; i <= 256; ++i) {
+    const double x = -16.0 + 32.0 * i / 256.0;
+    double v = std::nearbyint(32768.0 / (1.0 + std::exp(-x)));
+    t[kSigmoidOff + i] = (int32_t)(v > 32767.0 ? 32767.0 : v);
+  }
+}
+
+int ensure_stage(w4a8_ctx *c, size_t bytes) {
+  if (bytes <= c->stage_cap) return W4A8_OK;
+  if (c->d_stage) HIP_TRY(hipFree(c->d_stage));
+  c->d_stage = nullptr;
+  c->stage_cap = 0;
+  size_t cap = bytes < (1u << 20) ? (1u << 20) : bytes;
+  HIP_TRY(hipMalloc(&c->d_stage, cap));
+  c->stage_cap = cap;
+  return W4A8_OK;
+}
+
+int ensure_partials(w4a8_ctx *c, int n) {
+  if (n <= c->partials_cap) return W4A8_OK;
+  if (c->d_partials) HIP_TRY(hipFree(c->d_partials));
+  c->d_partials = nullptr;
+  c->partials_cap = 0;
+  HIP_TRY(hipMalloc(&c->d_partials, sizeof(uint64_t) * (size_t)n));
+  c->partials_cap = n;
+  return W4A8_OK;
+}
+
+// reads and clears the device error word (stream must be idle)
+int take_err(w4a8_ctx *c) {
+  int32_t h = 0;
+  HIP_TRY(hipMemcpy(&h, c->d_err, sizeof(h), hipMemcpyDeviceToHost));
+  if (h) {
+    HIP_TRY(hipMemset(c->d_err, 0, sizeof(int32_t)));
+    if (h & 1) return fail(W4A8_E_Y32_OVF, "y32 overflow — sh miscomputed");
+  }
+  return W4A8_OK;
+}
+
+int grid_for(w4a8_ctx *c, int64_t tiles) {
+  const int g = c->grid_override > 0 ? c->grid_override : c->grid;
+  return (int)(tiles < g ? tiles : g);
+}
+
+// fills prologue fields and validates them
+int set_prologue(w4a8_ctx *c, GemvParams &P, int32_t K, int32_t prologue,
+                 const void *x, const int16_t *norm_w, int32_t in_f,
+                 int32_t one_plus, int32_t e_x) {
+  if (prologue < PRO_X8 || prologue > PRO_RMSNORM_DYNQ8)
+    return fail(W4A8_E_ARG, "unknown prologue " + std::to_string(prologue));
+  if (!x || !aligned16(x)) return fail(W4A8_E_ARG, "x must be a 16-byte aligned pointer");
+  if (prologue == PRO_RMSNORM_DYNQ8) {
+    if (!norm_w || !aligned16(norm_w))
+      return fail(W4A8_E_ARG, "norm_w must be a 16-byte aligned pointer");
+    if ((K & (K - 1)) != 0)
+      return fail(W4A8_E_RANGE, "rmsnorm_fx: n=" + std::to_string(K) +
+                                    " is not a power of 2");
+    if (K > 8192)
+      return fail(W4A8_E_RANGE, "rmsnorm_fx: n=" + std::to_string(K) + " > 8192");
+  }
+  P.K = K;
+  P.NG = K / kGroup;
+  P.nblk = (P.NG + kGroupsPerBlock - 1) / kGroupsPerBlock;
+  P.tile_bytes = layout_for(K).tile_bytes;
+  P.pro = prologue;
+  P.x = x;
+  P.norm_w = norm_w;
+  P.in_f = in_f;
+  P.one_plus = one_plus ? 1 : 0;
+  P.e_x_given = e_x;
+  P.tables = c->d_tables;
+  P.err = c->d_err;
+  return W4A8_OK;
+}
+
+int check_epilogue(int32_t epi) {
+  if (epi < EPI_Y32 || epi > EPI_SHIFT_I64)
+    return fail(W4A8_E_ARG, "unknown epilogue " + std::to_string(epi));
+  return W4A8_OK;
+}
+
+size_t out_elem(int32_t epi) {
+  switch (epi) {
+    case EPI_MOVY_I16:
+    case EPI_SILU32: return 2;
+    case EPI_SHIFT_I64: return 8;
+    default: return 4;
+  }
+}
+
+int site_launch(w4a8_ctx *c, int32_t nmat, const w4a8_weights *const *w,
+                const int32_t *epi, const int32_t *p0, void *const *out,
+                int32_t prologue, const void *x, const int16_t *norm_w,
+                int32_t in_f, int32_t one_plus, int32_t e_x, int8_t *x8_out,
+                int32_t *e_x_out, int16_t *xn_out) {
+  if (nmat < 1 || nmat > kMaxJobs)
+    return fail(W4A8_E_ARG, "site holds 1.." + std::to_string(kMaxJobs) + " matrices");
+  GemvParams P{};
+  const int32_t K = w[0]->L.K;
+  int rc = set_prologue(c, P, K, prologue, x, norm_w, in_f, one_plus, e_x);
+  if (rc) return rc;
+  int64_t tiles = 0;
+  for (int i = 0; i < nmat; ++i) {
+    if (!w[i] || !out[i]) return fail(W4A8_E_ARG, "null weights/output");
+    if (w[i]->L.K != K) return fail(W4A8_E_SHAPE, "matrices of one site must share K");
+    if ((rc = check_epilogue(epi[i]))) return rc;
+    P.job[i].w = w[i]->d;
+    P.job[i].out = out[i];
+    P.job[i].nrows = (int32_t)w[i]->nrows;
+    P.job[i].tile0 = (int32_t)tiles;
+    P.job[i].sh = w[i]->sh;
+    P.job[i].epi = epi[i];
+    P.job[i].p0 = p0[i];
+    tiles += w[i]->ntiles;
+  }
+  P.njobs = nmat;
+  P.total_tiles = (int32_t)tiles;
+  P.x8_out = x8_out;
+  P.e_x_out = e_x_out;
+  P.xn_out = xn_out;
+  P.partials = nullptr;
+  DeviceGuard g(c->device);
+  HIP_TRY(launch_gemv(P, grid_for(c, tiles), c->stream));
+  return W4A8_OK;
+}
+
+int head_launch(w4a8_ctx *c, const w4a8_weights *w, int32_t prologue,
+                const void *x, const int16_t *norm_w, int32_t in_f,
+                int32_t one_plus, int32_t e_x, int32_t *d_result) {
+  if (w->nrows > (1 << 18))
+    return fail(W4A8_E_RANGE, "vocab " + std::to_string(w->nrows) +
+                                  " exceeds the 18-bit AMAX32 index (2^18)");
+  GemvParams P{};
+  int rc = set_prologue(c, P, w->L.K, prologue, x, norm_w, in_f, one_plus, e_x);
+  if (rc) return rc;
+  P.job[0].w = w->d;
+  P.job[0].out = nullptr;
+  P.job[0].nrows = (int32_t)w->nrows;
+  P.job[0].tile0 = 0;
+  P.job[0].sh = w->sh;
+  P.job[0].epi = EPI_ARGMAX;
+  P.job[0].p0 = 0;
+  P.njobs = 1;
+  P.total_tiles = (int32_t)w->ntiles;
+  const int grid = grid_for(c, w->ntiles);
+  if ((rc = ensure_partials(c, grid))) return rc;
+  P.partials = c->d_partials;
+  DeviceGuard g(c->device);
+  HIP_TRY(launch_gemv(P, grid, c->stream));
+  HIP_TRY(launch_argmax_final(c->d_partials, grid, d_result, c->stream));
+  return W4A8_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *w4a8_version(void) { return "fable5-w4a8 0.1 gfx950"; }
+
+const char *w4a8_last_error(void) { return g_err.c_str(); }
+
+int w4a8_ctx_create(int32_t device, w4a8_ctx **out) {
+  if (!out) return fail(W4A8_E_ARG, "null out");
+  *out = nullptr;
+  int ndev = 0;
+  HIP_TRY(hipGetDeviceCount(&ndev));
+  if (device < 0 || device >= ndev)
+    return fail(W4A8_E_ARG, "no HIP device " + std::to_string(device));
+  DeviceGuard g(device);
+  w4a8_ctx *c = new w4a8_ctx();
+  c->device = device;
+  int rc = W4A8_OK;
+  do {
+    hipError_t e;
+    if ((e = hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking)) != hipSuccess) {
+      rc = fail(W4A8_E_HIP, std::string("hipStreamCreate: ") + hipGetErrorString(e));
+      break;
+    }
+    c->stream = c->own;
+    if ((e = hipDeviceGetAttribute(&c->num_cu, hipDeviceAttributeMultiprocessorCount,
+                                   device)) != hipSuccess) {
+      rc = fail(W4A8_E_HIP, hipGetErrorString(e));
+      break;
+    }
+    c->grid = c->num_cu * gemv_max_blocks_per_cu();
+    build_tables(c->h_tables);
+    if ((e = hipMalloc(&c->d_tables, sizeof(int32_t) * kTableLen)) != hipSuccess ||
+        (e = hipMemcpy(c->d_tables, c->h_tables, sizeof(int32_t) * kTableLen,
+                       hipMemcpyHostToDevice)) != hipSuccess ||
+        (e = hipMalloc(&c->d_err, 64)) != hipSuccess ||
+        (e = hipMemset(c->d_err, 0, 64)) != hipSuccess ||
+        (e = hipMalloc(&c->d_result, 64)) != hipSuccess) {
+      rc = fail(W4A8_E_HIP, hipGetErrorString(e));
+      break;
+    }
+  } while (0);
+  if (rc) {
+    w4a8_ctx_destroy(c);
+    return rc;
+  }
+  *out = c;
+  return W4A8_OK;
+}
+
+int w4a8_ctx_destroy(w4a8_ctx *c) {
+  if (!c) return W4A8_OK;
+  DeviceGuard g(c->device);
+  if (c->own) (void)hipStreamSynchronize(c->own);
+  if (c->stream && c->stream != c->own) (void)hipStreamSynchronize(c->stream);
+  (void)hipFree(c->d_tables);
+  (void)hipFree(c->d_err);
+  (void)hipFree(c->d_partials);
+  (void)hipFree(c->d_result);
+  (void)hipFree(c->d_stage);
+  if (c->own) (void)hipStreamDestroy(c->own);
+  delete c;
+  return W4A8_OK;
+}
+
+int w4a8_ctx_set_stream(w4a8_ctx *c, void *s) {
+  if (!c) return fail(W4A8_E_ARG, "null ctx");
+  c->stream = s ? (hipStream_t)s : c->own;
+  return W4A8_OK;
+}
+
+int w4a8_ctx_sync(w4a8_ctx *c) {
+  if (!c) return fail(W4A8_E_ARG, "null ctx");
+  DeviceGuard g(c->device);
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return take_err(c);
+}
+
+int w4a8_ctx_info(const w4a8_ctx *c, int32_t *num_cu, int32_t *grid) {
+  if (!c) return fail(W4A8_E_ARG, "null ctx");
+  if (num_cu) *num_cu = c->num_cu;
+  if (grid) *grid = c->grid_override > 0 ? c->grid_override : c->grid;
+  return W4A8_OK;
+}
+
+int w4a8_ctx_set_grid(w4a8_ctx *c, int32_t grid) {
+  if (!c || grid < 0) return fail(W4A8_E_ARG, "bad ctx/grid");
+  c->grid_override = grid;
+  return W4A8_OK;
+}
+
+int w4a8_tables(w4a8_ctx *c, int32_t *rsqrt512, int32_t *sigmoid257) {
+  if (!c) return fail(W4A8_E_ARG, "null ctx");
+  // read back what the device actually holds
+  int32_t t[kTableLen];
+  DeviceGuard g(c->device);
+  HIP_TRY(hipMemcpy(t, c->d_tables, sizeof(t), hipMemcpyDeviceToHost));
+  if (rsqrt512) memcpy(rsqrt512, t + kRsqrtOff, 512 * sizeof(int32_t));
+  if (sigmoid257) memcpy(sigmoid257, t + kSigmoidOff, 257 * sizeof(int32_t));
+  return W4A8_OK;
+}
+
+// ------------------------------------------------------------------ weights
+static int upload_common(w4a8_ctx *c, const uint8_t *img, bool host, int64_t nrows,
+                         int32_t K, int32_t sh, w4a8_weights **out) {
+  if (!c || !img || !out) return fail(W4A8_E_ARG, "null argument");
+  *out = nullptr;
+  int rc = check_k_sh(K, sh);
+  if (rc) return rc;
+  if (nrows < 1 || nrows > (int64_t)1 << 30)
+    return fail(W4A8_E_SHAPE, "nrows=" + std::to_string(nrows) + " out of range");
+  DeviceGuard g(c->device);
+  w4a8_weights *w = new w4a8_weights();
+  w->ctx = c;
+  w->nrows = nrows;
+  w->ntiles = (nrows + kTileRows - 1) / kTileRows;
+  w->sh = sh;
+  w->L = layout_for(K);
+  w->bytes = (size_t)(w->ntiles * w->L.tile_bytes);
+  const int64_t stride = wire_stride(K);
+  hipError_t e = hipMalloc(&w->d, w->bytes);
+  if (e != hipSuccess) {
+    delete w;
+    return fail(W4A8_E_HIP, std::string("hipMalloc weights: ") + hipGetErrorString(e));
+  }
+  const uint8_t *src = img;
+  uint8_t *tmp = nullptr;
+  if (host || !aligned16(img)) {
+    e = hipMalloc(&tmp, (size_t)(nrows * stride));
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(tmp, img, (size_t)(nrows * stride),
+                         host ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice,
+                         c->stream);
+    src = tmp;
+  }
+  if (e == hipSuccess) e = launch_repack(src, nrows, w->L, stride, w->d, c->stream);
+  if (e == hipSuccess && (host || tmp)) e = hipStreamSynchronize(c->stream);
+  if (tmp) (void)hipFree(tmp);
+  if (e != hipSuccess) {
+    (void)hipFree(w->d);
+    delete w;
+    return fail(W4A8_E_HIP, std::string("weights upload: ") + hipGetErrorString(e));
+  }
+  *out = w;
+  return W4A8_OK;
+}
+
+int w4a8_weights_upload(w4a8_ctx *c, const uint8_t *img, int64_t nrows, int32_t K,
+                        int32_t sh, w4a8_weights **out) {
+  return upload_common(c, img, true, nrows, K, sh, out);
+}
+
+int w4a8_weights_upload_async(w4a8_ctx *c, const uint8_t *d_img, int64_t nrows,
+                              int32_t K, int32_t sh, w4a8_weights **out) {
+  return upload_common(c, d_img, false, nrows, K, sh, out);
+}
+
+int w4a8_weights_download(w4a8_ctx *c, const w4a8_weights *w, uint8_t *img) {
+  if (!c || !w || !img) return fail(W4A8_E_ARG, "null argument");
+  DeviceGuard g(c->device);
+  const int64_t stride = wire_stride(w->L.K);
+  const size_t n = (size_t)(w->nrows * stride);
+  int rc = ensure_stage(c, n);
+  if (rc) return rc;
+  HIP_TRY(launch_unpack(w->d, w->nrows, w->L, stride, c->d_stage, c->stream));
+  HIP_TRY(hipMemcpyAsync(img, c->d_stage, n, hipMemcpyDeviceToHost, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return W4A8_OK;
+}
+
+int w4a8_weights_info(const w4a8_weights *w, int64_t *nrows, int32_t *K, int32_t *sh,
+                      int64_t *bytes) {
+  if (!w) return fail(W4A8_E_ARG, "null weights");
+  if (nrows) *nrows = w->nrows;
+  if (K) *K = w->L.K;
+  if (sh) *sh = w->sh;
+  if (bytes) *bytes = (int64_t)w->bytes;
+  return W4A8_OK;
+}
+
+int w4a8_weights_free(w4a8_weights *w) {
+  if (!w) return W4A8_OK;
+  DeviceGuard g(w->ctx->device);
+  (void)hipStreamSynchronize(w->ctx->stream);
+  (void)hipFree(w->d);
+  delete w;
+  return W4A8_OK;
+}
+
+// --------------------------------------------------------- elementwise ops
+int w4a8_rshift_round(w4a8_ctx *c, const int64_t *v, int64_t n, int32_t s, int64_t *out) {
+  if (!c || (n > 0 && (!v || !out)) || n < 0) return fail(W4A8_E_ARG, "bad argument");
+  if (s < -63 || s > 63) return fail(W4A8_E_RANGE, "shift outside -63..63");
+  if (n == 0) return W4A8_OK;
+  DeviceGuard g(c->device);
+  int rc = ensure_stage(c, (size_t)n * 16);
+  if (rc) return rc;
+  int64_t *d_in = (int64_t *)c->d_stage, *d_out = d_in + n;
+  HIP_TRY(hipMemcpyAsync(d_in, v, n * 8, hipMemcpyHostToDevice, c->stream));
+  HIP_TRY(launch_rshift_round(d_in, n, s, d_out, c->stream));
+  HIP_TRY(hipMemcpyAsync(out, d_out, n * 8, hipMemcpyDeviceToHost, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return W4A8_OK;
+}
+
+static int vec_prologue(w4a8_ctx *c, int32_t pro, const int16_t *x16,
+                        const int16_t *w_q14, int32_t n, int32_t in_f,
+                        int32_t one_plus, int8_t *x8, int32_t *e, int16_t *xn) {
+  if (!c || !x16) return fail(W4A8_E_ARG, "null argument");
+  if (n < 1 || n > kKMax || n % 8)
+    return fail(W4A8_E_RANGE, "vector length " + std::to_string(n) +
+                                  " must be a multiple of 8 in 8..12288");
+  DeviceGuard g(c->device);
+  const size_t nb = (size_t)n * 2;
+  int rc = ensure_stage(c, 4 * nb + 64);
+  if (rc) return rc;
+  uint8_t *base = c->d_stage;
+  int16_t *d_x = (int16_t *)base;
+  int16_t *d_w = (int16_t *)(base + nb);
+  int16_t *d_xn = (int16_t *)(base + 2 * nb);
+  int8_t *d_x8 = (int8_t *)(base + 3 * nb);
+  int32_t *d_e = (int32_t *)(base + 4 * nb);
+  HIP_TRY(hipMemcpyAsync(d_x, x16, nb, hipMemcpyHostToDevice, c->stream));
+  if (pro == PRO_RMSNORM_DYNQ8)
+    HIP_TRY(hipMemcpyAsync(d_w, w_q14, nb, hipMemcpyHostToDevice, c->stream));
+  GemvParams P{};
+  if (pro == PRO_RMSNORM_DYNQ8) {
+    if ((n & (n - 1)) != 0)
+      return fail(W4A8_E_RANGE, "rmsnorm_fx: n=" + std::to_string(n) + " is not a power of 2");
+    if (n > 8192) return fail(W4A8_E_RANGE, "rmsnorm_fx: n > 8192");
+  }
+  P.K = n;
+  P.NG = 0;
+  P.pro = pro;
+  P.x = d_x;
+  P.norm_w = d_w;
+  P.in_f = in_f;
+  P.one_plus = one_plus ? 1 : 0;
+  P.tables = c->d_tables;
+  P.err = c->d_err;
+  P.x8_out = d_x8;
+  P.e_x_out = d_e;
+  P.xn_out = d_xn;
+  HIP_TRY(launch_vec_prologue(P, c->stream));
+  if (x8) HIP_TRY(hipMemcpyAsync(x8, d_x8, n, hipMemcpyDeviceToHost, c->stream));
+  if (e) HIP_TRY(hipMemcpyAsync(e, d_e, 4, hipMemcpyDeviceToHost, c->stream));
+  if (xn) HIP_TRY(hipMemcpyAsync(xn, d_xn, nb, hipMemcpyDeviceToHost, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return W4A8_OK;
+}
+
+int w4a8_dynq8(w4a8_ctx *c, const int16_t *x16, int32_t n, int8_t *x8, int32_t *e) {
+  return vec_prologue(c, PRO_DYNQ8, x16, nullptr, n, 0, 0, x8, e, nullptr);
+}
+
+int w4a8_rmsnorm(w4a8_ctx *c, const int16_t *x16, const int16_t *w_q14, int32_t n,
+                 int32_t in_f, int32_t one_plus, int16_t *out) {
+  if (!w_q14 || !out) return fail(W4A8_E_ARG, "null argument");
+  return vec_prologue(c, PRO_RMSNORM_DYNQ8, x16, w_q14, n, in_f, one_plus, nullptr,
+                      nullptr, out);
+}
+
+int w4a8_movy(w4a8_ctx *c, const int32_t *y32, int64_t n, int32_t shift, int32_t mode,
+              void *out) {
+  if (!c || n < 0 || (n > 0 && (!y32 || !out))) return fail(W4A8_E_ARG, "bad argument");
+  if (mode != W4A8_MOVY_INT16 && mode != W4A8_MOVY_PAIRS32)
+    return fail(W4A8_E_ARG, "unknown MOVY mode");
+  if (n == 0) return W4A8_OK;
+  DeviceGuard g(c->device);
+  const size_t ob = mode == W4A8_MOVY_INT16 ? 2 : 4;
+  int rc = ensure_stage(c, (size_t)n * (4 + ob) + 16);
+  if (rc) return rc;
+  int32_t *d_y = (int32_t *)c->d_stage;
+  void *d_o = c->d_stage + (((size_t)n * 4 + 15) & ~(size_t)15);
+  HIP_TRY(hipMemcpyAsync(d_y, y32, n * 4, hipMemcpyHostToDevice, c->stream));
+  HIP_TRY(launch_movy(d_y, n, shift, mode, d_o, c->stream));
+  HIP_TRY(hipMemcpyAsync(out, d_o, n * ob, hipMemcpyDeviceToHost, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return W4A8_OK;
+}
+
+int w4a8_alu(w4a8_ctx *c, int32_t op, const int32_t *y32, const int16_t *b, int64_t n,
+             int32_t p0, void *out) {
+  if (!c || n < 0 || (n > 0 && (!y32 || !out))) return fail(W4A8_E_ARG, "bad argument");
+  if (op != W4A8_ALU_SHIFT32 && op != W4A8_ALU_SILU32 && op != W4A8_ALU_EMUL32 &&
+      op != W4A8_ALU_SHIFT32W)
+    return fail(W4A8_E_ARG, "unsupported ALU op " + std::to_string(op));
+  if (op == W4A8_ALU_EMUL32 && !b) return fail(W4A8_E_ARG, "EMUL32 needs b");
+  if (n > 16383)
+    return fail(W4A8_E_RANGE, "ALU count " + std::to_string(n) +
+                                  " does not fit ARG0[17:4] (max 16383)");
+  if (n == 0) return W4A8_OK;
+  DeviceGuard g(c->device);
+  const size_t ob = op == W4A8_ALU_SHIFT32W ? 4 : 2;
+  const size_t a4 = ((size_t)n * 4 + 15) & ~(size_t)15, a2 = ((size_t)n * 2 + 15) & ~(size_t)15;
+  int rc = ensure_stage(c, a4 + a2 + n * ob + 16);
+  if (rc) return rc;
+  int32_t *d_y = (int32_t *)c->d_stage;
+  int16_t *d_b = (int16_t *)(c->d_stage + a4);
+  void *d_o = c->d_stage + a4 + a2;
+  HIP_TRY(hipMemcpyAsync(d_y, y32, n * 4, hipMemcpyHostToDevice, c->stream));
+  if (b) HIP_TRY(hipMemcpyAsync(d_b, b, n * 2, hipMemcpyHostToDevice, c->stream));
+  HIP_TRY(launch_alu(op, d_y, d_b, n, p0, c->d_tables, d_o, c->stream));
+  HIP_TRY(hipMemcpyAsync(out, d_o, n * ob, hipMemcpyDeviceToHost, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return W4A8_OK;
+}
+
+// ------------------------------------------------------------- matvec (host)
+int w4a8_matvec_fused(w4a8_ctx *c, const w4a8_weights *w, int32_t prologue,
+                      const void *x, const int16_t *norm_w, int32_t in_f,
+                      int32_t one_plus, int32_t epilogue, int32_t p0, void *out,
+                      int8_t *x8_out, int32_t *e_x_io, int16_t *xn_out) {
+  if (!c || !w || !x || !out) return fail(W4A8_E_ARG, "null argument");
+  int rc = check_epilogue(epilogue);
+  if (rc) return rc;
+  if (prologue == PRO_X8 && !e_x_io && epilogue != EPI_Y32)
+    return fail(W4A8_E_ARG, "PRO_X8 with a shifting epilogue needs e_x");
+  DeviceGuard g(c->device);
+  const int32_t K = w->L.K;
+  const size_t xb = prologue == PRO_X8 ? (size_t)K : (size_t)K * 2;
+  const size_t A = 256;
+  auto up = [&](size_t v) { return (v + A - 1) & ~(A - 1); };
+  const size_t ob = out_elem(epilogue) * (size_t)w->nrows;
+  const size_t o_x = 0, o_w = up(xb), o_out = o_w + up((size_t)K * 2),
+               o_x8 = o_out + up(ob), o_e = o_x8 + up(K), o_xn = o_e + A,
+               total = o_xn + up((size_t)K * 2);
+  if ((rc = ensure_stage(c, total))) return rc;
+  uint8_t *s = c->d_stage;
+  HIP_TRY(hipMemcpyAsync(s + o_x, x, xb, hipMemcpyHostToDevice, c->stream));
+  if (prologue == PRO_RMSNORM_DYNQ8) {
+    if (!norm_w) return fail(W4A8_E_ARG, "PRO_RMSNORM_DYNQ8 needs norm_w");
+    HIP_TRY(hipMemcpyAsync(s + o_w, norm_w, (size_t)K * 2, hipMemcpyHostToDevice,
+                           c->stream));
+  }
+  const int32_t ex_in = (prologue == PRO_X8 && e_x_io) ? *e_x_io : 0;
+  const int32_t ep = epilogue;
+  void *d_out = s + o_out;
+  rc = site_launch(c, 1, &w, &ep, &p0, &d_out, prologue, s + o_x,
+                   (const int16_t *)(s + o_w), in_f, one_plus, ex_in,
+                   (int8_t *)(s + o_x8), (int32_t *)(s + o_e), (int16_t *)(s + o_xn));
+  if (rc) return rc;
+  HIP_TRY(hipMemcpyAsync(out, d_out, ob, hipMemcpyDeviceToHost, c->stream));
+  if (x8_out) HIP_TRY(hipMemcpyAsync(x8_out, s + o_x8, K, hipMemcpyDeviceToHost, c->stream));
+  if (e_x_io) HIP_TRY(hipMemcpyAsync(e_x_io, s + o_e, 4, hipMemcpyDeviceToHost, c->stream));
+  if (xn_out && prologue == PRO_RMSNORM_DYNQ8)
+    HIP_TRY(hipMemcpyAsync(xn_out, s + o_xn, (size_t)K * 2, hipMemcpyDeviceToHost,
+                           c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return take_err(c);
+}
+
+int w4a8_matvec_y32(w4a8_ctx *c, const w4a8_weights *w, const int8_t *x8, int32_t *y32) {
+  int32_t ex = 0;
+  return w4a8_matvec_fused(c, w, PRO_X8, x8, nullptr, 0, 0, EPI_Y32, 0, y32, nullptr,
+                           &ex, nullptr);
+}
+
+int w4a8_head_argmax(w4a8_ctx *c, const w4a8_weights *w, int32_t prologue, const void *x,
+                     const int16_t *norm_w, int32_t in_f, int32_t one_plus,
+                     int32_t *idx, int32_t *val) {
+  if (!c || !w || !x) return fail(W4A8_E_ARG, "null argument");
+  DeviceGuard g(c->device);
+  const int32_t K = w->L.K;
+  const size_t xb = prologue == PRO_X8 ? (size_t)K : (size_t)K * 2;
+  const size_t o_w = (xb + 255) & ~(size_t)255;
+  int rc = ensure_stage(c, o_w + (size_t)K * 2 + 256);
+  if (rc) return rc;
+  uint8_t *s = c->d_stage;
+  HIP_TRY(hipMemcpyAsync(s, x, xb, hipMemcpyHostToDevice, c->stream));
+  if (prologue == PRO_RMSNORM_DYNQ8 && norm_w)
+    HIP_TRY(hipMemcpyAsync(s + o_w, norm_w, (size_t)K * 2, hipMemcpyHostToDevice,
+                           c->stream));
+  rc = head_launch(c, w, prologue, s, (const int16_t *)(s + o_w), in_f, one_plus, 0,
+                   c->d_result);
+  if (rc) return rc;
+  int32_t h[2];
+  HIP_TRY(hipMemcpyAsync(h, c->d_result, 8, hipMemcpyDeviceToHost, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  if ((rc = take_err(c))) return rc;
+  if (idx) *idx = h[0];
+  if (val) *val = h[1];
+  return W4A8_OK;
+}
+
+int w4a8_matmul_y32(w4a8_ctx *c, const w4a8_weights *w, const int8_t *x8, int32_t B,
+                    int32_t *y32) {
+  if (!c || !w || !x8 || !y32) return fail(W4A8_E_ARG, "null argument");
+  if (B < 1 || B > 64) return fail(W4A8_E_RANGE, "batch must be 1..64");
+  DeviceGuard g(c->device);
+  const int32_t K = w->L.K;
+  const size_t xb = (size_t)B * K, yb = (size_t)B * w->nrows * 4;
+  const size_t o_y = (xb + 255) & ~(size_t)255;
+  int rc = ensure_stage(c, o_y + yb);
+  if (rc) return rc;
+  HIP_TRY(hipMemcpyAsync(c->d_stage, x8, xb, hipMemcpyHostToDevice, c->stream));
+  rc = w4a8_matmul_y32_async(c, w, (const int8_t *)c->d_stage, B,
+                             (int32_t *)(c->d_stage + o_y));
+  if (rc) return rc;
+  HIP_TRY(hipMemcpyAsync(y32, c->d_stage + o_y, yb, hipMemcpyDeviceToHost, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return take_err(c);
+}
+
+// ----------------------------------------------------------- async variants
+int w4a8_matvec_fused_async(w4a8_ctx *c, const w4a8_weights *w, int32_t prologue,
+                            const void *d_x, const int16_t *d_norm_w, int32_t in_f,
+                            int32_t one_plus, int32_t e_x, int32_t epilogue, int32_t p0,
+                            void *d_out, int8_t *d_x8_out, int32_t *d_e_x_out,
+                            int16_t *d_xn_out) {
+  if (!c || !w) return fail(W4A8_E_ARG, "null argument");
+  return site_launch(c, 1, &w, &epilogue, &p0, &d_out, prologue, d_x, d_norm_w, in_f,
+                     one_plus, e_x, d_x8_out, d_e_x_out, d_xn_out);
+}
+
+int w4a8_site_async(w4a8_ctx *c, int32_t nmat, const w4a8_weights *const *w,
+                    const int32_t *epilogue, const int32_t *p0, void *const *d_out,
+                    int32_t prologue, const void *d_x, const int16_t *d_norm_w,
+                    int32_t in_f, int32_t one_plus, int32_t e_x, int8_t *d_x8_out,
+                    int32_t *d_e_x_out, int16_t *d_xn_out) {
+  if (!c || !w || !epilogue || !p0 || !d_out) return fail(W4A8_E_ARG, "null argument");
+  return site_launch(c, nmat, w, epilogue, p0, d_out, prologue, d_x, d_norm_w, in_f,
+                     one_plus, e_x, d_x8_out, d_e_x_out, d_xn_out);
+}
+
+int w4a8_head_argmax_async(w4a8_ctx *c, const w4a8_weights *w, int32_t prologue,
+                           const void *d_x, const int16_t *d_norm_w, int32_t in_f,
+                           int32_t one_plus, int32_t e_x, int32_t *d_result) {
+  if (!c || !w || !d_result) return fail(W4A8_E_ARG, "null argument");
+  return head_launch(c, w, prologue, d_x, d_norm_w, in_f, one_plus, e_x, d_result);
+}
+
+int w4a8_matmul_y32_async(w4a8_ctx *c, const w4a8_weights *w, const int8_t *d_x8,
+                          int32_t B, int32_t *d_y32) {
+  if (!c || !w || !d_x8 || !d_y32) return fail(W4A8_E_ARG, "null argument");
+  if (B < 1 || B > 64) return fail(W4A8_E_RANGE, "batch must be 1..64");
+  if (!aligned16(d_x8)) return fail(W4A8_E_ARG, "x8 must be 16-byte aligned");
+  DeviceGuard g(c->device);
+  HIP_TRY(launch_matmul(w->d, (int32_t)w->nrows, w->L, w->sh, d_x8, B, d_y32, c->d_err,
+                        c->stream));
+  return W4A8_OK;
+}
+
+}  // extern "C"

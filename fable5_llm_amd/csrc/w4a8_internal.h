@@ -1,0 +1,122 @@
+// Internal declarations shared by the kernels (w4a8_kernels.hip) and the
+// C ABI (w4a8_abi.hip).  Not installed; the public surface is
+// include/fable5_w4a8.h.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace w4a8 {
+
+// ---------------------------------------------------------------------------
+// Device weight layout ("tile layout").
+//
+// Rows are grouped into tiles of 16.  A tile is a sequence of scale blocks;
+// block b covers groups 8b..8b+7 (a group is 128 weights of one row, the
+// unit that shares one uint16 scale mantissa) and is laid out as
+//
+//   [scales: 16 rows x 16 B = m[r][8b..8b+7] as uint16 LE, zero padded]
+//   [group 8b  : 16 rows x 64 B]
+//   [group 8b+1: 16 rows x 64 B] ...
+//
+// Inside a group chunk, bytes [64r + 16q, 64r + 16q + 16) hold weights
+// k = 128g + 32q + [0, 32) of row r, so lane (4r + q) of a wavefront reads
+// one contiguous 16-byte piece and a whole wavefront reads the 1 KiB chunk
+// with one coalesced load.  Each 32-bit word of a piece covers k0..k0+7:
+// byte i carries ((w[k0+i] + 8) & 15) in its low nibble (offset form) and
+// (w[k0+4+i] & 15) in its high nibble (two's complement), so
+//   (word & 0x0F0F0F0F) are 4 unsigned weights + 8 against x8[k0..k0+3]
+//   (word & 0xF0F0F0F0) are 4 signed weights * 16  against x8[k0+4..k0+7]
+// and sdot4 consumes both without any further unpacking.  The +8 offset is
+// removed exactly with a per-(group, quarter) correction 8 * sum x8[lo k].
+//
+// Bytes per row = K/2 + 16*ceil(NG/8): identical to the row image's
+// K/2 + 64*ceil(NG/32) whenever NG % 32 == 0 (K = 4096, 8192, 12288).
+// ---------------------------------------------------------------------------
+constexpr int kTileRows = 16;
+constexpr int kGroup = 128;
+constexpr int kGroupsPerBlock = 8;
+constexpr int kScaleChunk = kTileRows * 16;                     // 256
+constexpr int kGroupChunk = kTileRows * 64;                     // 1024
+constexpr int kBlockBytes = kScaleChunk + kGroupsPerBlock * kGroupChunk;  // 8448
+constexpr int kKMax = 12288;     // ng <= 96, the engine envelope
+constexpr int kNgMax = kKMax / kGroup;
+constexpr int kMaxJobs = 6;
+constexpr int kWG = 256;         // threads per workgroup (4 wavefronts)
+constexpr int kWaves = kWG / 64;
+
+enum Prologue { PRO_X8 = 0, PRO_DYNQ8 = 1, PRO_RMSNORM_DYNQ8 = 2 };
+enum Epilogue {
+  EPI_Y32 = 0, EPI_MOVY_I16 = 1, EPI_MOVY_P32 = 2, EPI_SILU32 = 3,
+  EPI_SHIFT_I64 = 4, EPI_ARGMAX = 5
+};
+
+struct Layout {
+  int32_t K, NG, nblk;
+  int64_t tile_bytes;
+};
+
+inline Layout layout_for(int32_t K) {
+  Layout L;
+  L.K = K;
+  L.NG = K / kGroup;
+  L.nblk = (L.NG + kGroupsPerBlock - 1) / kGroupsPerBlock;
+  L.tile_bytes = (int64_t)L.nblk * kScaleChunk + (int64_t)L.NG * kGroupChunk;
+  return L;
+}
+
+// Table offsets inside the device table buffer (int32 entries).
+constexpr int kRsqrtOff = 0;      // 512 Q1.15 seeds
+constexpr int kSigmoidOff = 512;  // 257 Q15 knots
+constexpr int kTableLen = 512 + 257;
+
+struct GemvJob {
+  const uint8_t *w;   // tile layout
+  void *out;
+  int32_t nrows;
+  int32_t tile0;      // first global tile index of this job
+  int32_t sh;
+  int32_t epi;
+  int32_t p0;         // epilogue shift = p0 - e_x
+  int32_t pad_;
+};
+
+struct GemvParams {
+  GemvJob job[kMaxJobs];
+  int32_t njobs;
+  int32_t total_tiles;
+  int32_t K, NG, nblk;
+  int32_t pro;
+  int64_t tile_bytes;
+  const void *x;            // int8[K] or int16[K]
+  const int16_t *norm_w;    // int16[K] Q14 (RMSNorm)
+  int32_t in_f, one_plus, e_x_given, pad_;
+  int8_t *x8_out;           // optional (written by workgroup 0)
+  int32_t *e_x_out;         // optional
+  int16_t *xn_out;          // optional RMSNorm output
+  const int32_t *tables;    // kTableLen entries
+  int32_t *err;             // bit 0: y32 overflow
+  uint64_t *partials;       // EPI_ARGMAX: one key per workgroup
+};
+
+// launchers (all asynchronous on `s`)
+hipError_t launch_fill_i32(int32_t *p, int32_t v, int64_t n, hipStream_t s);
+hipError_t launch_repack(const uint8_t *img, int64_t nrows, const Layout &L,
+                         int64_t stride, uint8_t *dst, hipStream_t s);
+hipError_t launch_unpack(const uint8_t *src, int64_t nrows, const Layout &L,
+                         int64_t stride, uint8_t *img, hipStream_t s);
+hipError_t launch_gemv(const GemvParams &p, int grid, hipStream_t s);
+hipError_t launch_argmax_final(const uint64_t *partials, int n,
+                               int32_t *result, hipStream_t s);
+hipError_t launch_rshift_round(const int64_t *v, int64_t n, int s,
+                               int64_t *out, hipStream_t st);
+hipError_t launch_movy(const int32_t *y, int64_t n, int shift, int mode,
+                       void *out, hipStream_t s);
+hipError_t launch_alu(int op, const int32_t *y, const int16_t *b, int64_t n,
+                      int p0, const int32_t *tables, void *out, hipStream_t s);
+hipError_t launch_vec_prologue(const GemvParams &p, hipStream_t s);
+hipError_t launch_matmul(const uint8_t *w, int32_t nrows, const Layout &L,
+                         int32_t sh, const int8_t *x8, int32_t B,
+                         int32_t *y32, int32_t *err, hipStream_t s);
+int gemv_max_blocks_per_cu();
+
+}  // namespace w4a8

@@ -1,0 +1,249 @@
+"""Handle-level API over the C ABI: a Context owns one HIP stream on one
+device; Weights are device-resident matrices repacked once from the
+reference's row image (w4a8_ref.pack_ddr_rows layout).
+
+Host-array methods (numpy in, numpy out) are synchronous; *_async methods
+take torch tensors already on the device and enqueue on the context stream.
+"""
+import ctypes
+
+import numpy as np
+
+from . import _native as N
+
+_c = ctypes.c_void_p
+
+
+def _ptr(a):
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def _dptr(t):
+    """device pointer of a torch tensor (or None)"""
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def wire_stride(K):
+    ng = K // 128
+    return (ng + (ng + 31) // 32) * 64
+
+
+class Weights:
+    """A W4A8 matrix resident in HBM in the engine's tile layout."""
+
+    def __init__(self, ctx, handle, nrows, K, sh):
+        self.ctx, self.h, self.nrows, self.K, self.sh = ctx, handle, nrows, K, sh
+        dev = ctypes.c_int64()
+        N.check(N.lib().w4a8_weights_info(handle, None, None, None,
+                                           ctypes.byref(dev)))
+        self.device_bytes = int(dev.value)
+
+    @property
+    def wire_bytes(self):
+        return self.nrows * wire_stride(self.K)
+
+    def download(self):
+        """The row image back from the device (bytes)."""
+        out = np.empty(self.wire_bytes, dtype=np.uint8)
+        N.check(N.lib().w4a8_weights_download(self.ctx.h, self.h, _ptr(out)))
+        return out.tobytes()
+
+    def free(self):
+        if self.h:
+            N.lib().w4a8_weights_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            if self.h and self.ctx.h:
+                self.free()
+        except Exception:
+            pass
+
+
+class Context:
+    def __init__(self, device=0):
+        h = ctypes.c_void_p()
+        N.check(N.lib().w4a8_ctx_create(device, ctypes.byref(h)), "ctx_create")
+        self.h = h
+        self.device = device
+        cu, grid = ctypes.c_int32(), ctypes.c_int32()
+        N.check(N.lib().w4a8_ctx_info(self.h, ctypes.byref(cu), ctypes.byref(grid)))
+        self.num_cu, self.grid = int(cu.value), int(grid.value)
+
+    def close(self):
+        if self.h:
+            N.lib().w4a8_ctx_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    # ------------------------------------------------------------ control
+    def set_stream(self, stream=None):
+        """Run on a torch.cuda.Stream (or raw hipStream_t int); None = own."""
+        s = None if stream is None else getattr(stream, "cuda_stream", stream)
+        N.check(N.lib().w4a8_ctx_set_stream(self.h, ctypes.c_void_p(s)))
+
+    def set_grid(self, grid):
+        N.check(N.lib().w4a8_ctx_set_grid(self.h, int(grid)))
+
+    def sync(self):
+        N.check(N.lib().w4a8_ctx_sync(self.h), "sync")
+
+    def tables(self):
+        r = np.empty(512, dtype=np.int32)
+        s = np.empty(257, dtype=np.int32)
+        N.check(N.lib().w4a8_tables(self.h, _ptr(r), _ptr(s)))
+        return r, s
+
+    # ------------------------------------------------------------ weights
+    def upload(self, img, nrows, K, sh):
+        """img: row image (bytes / uint8 array on the host, or a uint8 torch
+        tensor on the device)."""
+        h = ctypes.c_void_p()
+        if hasattr(img, "data_ptr"):
+            assert img.numel() == nrows * wire_stride(K), "image size"
+            N.check(N.lib().w4a8_weights_upload_async(
+                self.h, _dptr(img), nrows, K, sh, ctypes.byref(h)), "upload")
+        else:
+            a = np.frombuffer(img, dtype=np.uint8) if isinstance(img, (bytes, bytearray)) \
+                else np.ascontiguousarray(img, dtype=np.uint8).reshape(-1)
+            assert a.size == nrows * wire_stride(K), \
+                f"image is {a.size}B, expected {nrows}*{wire_stride(K)}"
+            N.check(N.lib().w4a8_weights_upload(self.h, _ptr(a), nrows, K, sh,
+                                                 ctypes.byref(h)), "upload")
+        return Weights(self, h, nrows, K, sh)
+
+    # -------------------------------------------------- elementwise (host)
+    def rshift_round(self, v, s):
+        a = np.ascontiguousarray(np.asarray(v, dtype=np.int64).reshape(-1))
+        out = np.empty_like(a)
+        N.check(N.lib().w4a8_rshift_round(self.h, _ptr(a), a.size, int(s), _ptr(out)))
+        return out.reshape(np.shape(v))
+
+    def dynq8(self, x16):
+        x = np.ascontiguousarray(np.asarray(x16, dtype=np.int16).reshape(-1))
+        n = x.size
+        pad = (-n) % 8
+        if pad:   # zeros never change max|x|, so padding is exact
+            x = np.concatenate([x, np.zeros(pad, np.int16)])
+        x8 = np.empty(x.size, dtype=np.int8)
+        e = ctypes.c_int32()
+        N.check(N.lib().w4a8_dynq8(self.h, _ptr(x), x.size, _ptr(x8), ctypes.byref(e)),
+                "dyn_quant_i8")
+        return x8[:n], int(e.value)
+
+    def rmsnorm(self, x16, w_q14, in_f, one_plus):
+        x = np.ascontiguousarray(np.asarray(x16, dtype=np.int16).reshape(-1))
+        w = np.ascontiguousarray(np.asarray(w_q14, dtype=np.int16).reshape(-1))
+        assert w.size == x.size, "weight length"
+        out = np.empty(x.size, dtype=np.int16)
+        N.check(N.lib().w4a8_rmsnorm(self.h, _ptr(x), _ptr(w), x.size, int(in_f),
+                                     1 if one_plus else 0, _ptr(out)), "rmsnorm_fx")
+        return out
+
+    def movy(self, y32, shift, mode):
+        y = np.ascontiguousarray(np.asarray(y32, dtype=np.int32).reshape(-1))
+        out = np.empty(y.size, dtype=np.int16 if mode == N.MOVY_INT16 else np.int32)
+        N.check(N.lib().w4a8_movy(self.h, _ptr(y), y.size, int(shift), int(mode),
+                                  _ptr(out)), "movy")
+        return out
+
+    def alu(self, op, y32, p0, b=None):
+        y = np.ascontiguousarray(np.asarray(y32, dtype=np.int32).reshape(-1))
+        bb = None if b is None else np.ascontiguousarray(np.asarray(b, dtype=np.int16))
+        out = np.empty(y.size, dtype=np.int32 if op == N.ALU_SHIFT32W else np.int16)
+        N.check(N.lib().w4a8_alu(self.h, int(op), _ptr(y),
+                                 None if bb is None else _ptr(bb), y.size, int(p0),
+                                 _ptr(out)), f"alu op {op}")
+        return out
+
+    # ------------------------------------------------------- matvec (host)
+    def matvec_y32(self, w, x8):
+        x = np.ascontiguousarray(np.asarray(x8, dtype=np.int8))
+        assert x.size == w.K, "x8 length"
+        y = np.empty(w.nrows, dtype=np.int32)
+        N.check(N.lib().w4a8_matvec_y32(self.h, w.h, _ptr(x), _ptr(y)), "matvec_y32")
+        return y
+
+    def matvec_fused(self, w, x, prologue=N.PRO_X8, epilogue=N.EPI_Y32, p0=0,
+                     e_x=0, norm_w=None, in_f=0, one_plus=False):
+        """Returns (out, x8, e_x, xn) -- xn only for the RMSNorm prologue."""
+        xdt = np.int8 if prologue == N.PRO_X8 else np.int16
+        xa = np.ascontiguousarray(np.asarray(x, dtype=xdt))
+        assert xa.size == w.K, "x length"
+        nw = None
+        if prologue == N.PRO_RMSNORM_DYNQ8:
+            nw = np.ascontiguousarray(np.asarray(norm_w, dtype=np.int16))
+            assert nw.size == w.K
+        odt = {N.EPI_Y32: np.int32, N.EPI_MOVY_I16: np.int16, N.EPI_MOVY_P32: np.int32,
+               N.EPI_SILU32: np.int16, N.EPI_SHIFT_I64: np.int64}[epilogue]
+        out = np.empty(w.nrows, dtype=odt)
+        x8 = np.empty(w.K, dtype=np.int8)
+        xn = np.empty(w.K, dtype=np.int16)
+        ex = ctypes.c_int32(int(e_x))
+        N.check(N.lib().w4a8_matvec_fused(
+            self.h, w.h, int(prologue), _ptr(xa), None if nw is None else _ptr(nw),
+            int(in_f), 1 if one_plus else 0, int(epilogue), int(p0), _ptr(out),
+            _ptr(x8), ctypes.byref(ex), _ptr(xn)), "matvec")
+        return out, x8, int(ex.value), (xn if prologue == N.PRO_RMSNORM_DYNQ8 else None)
+
+    def head_argmax(self, w, x, prologue=N.PRO_X8, norm_w=None, in_f=0,
+                    one_plus=False):
+        xdt = np.int8 if prologue == N.PRO_X8 else np.int16
+        xa = np.ascontiguousarray(np.asarray(x, dtype=xdt))
+        assert xa.size == w.K
+        nw = None if norm_w is None else np.ascontiguousarray(np.asarray(norm_w, np.int16))
+        idx, val = ctypes.c_int32(), ctypes.c_int32()
+        N.check(N.lib().w4a8_head_argmax(
+            self.h, w.h, int(prologue), _ptr(xa), None if nw is None else _ptr(nw),
+            int(in_f), 1 if one_plus else 0, ctypes.byref(idx), ctypes.byref(val)),
+            "head_argmax")
+        return int(idx.value), int(val.value)
+
+    def matmul_y32(self, w, x8):
+        x = np.ascontiguousarray(np.asarray(x8, dtype=np.int8))
+        assert x.ndim == 2 and x.shape[1] == w.K
+        y = np.empty((x.shape[0], w.nrows), dtype=np.int32)
+        N.check(N.lib().w4a8_matmul_y32(self.h, w.h, _ptr(x), x.shape[0], _ptr(y)),
+                "matmul_y32")
+        return y
+
+    # ------------------------------------------------------ device (async)
+    def site_async(self, weights, epilogues, p0s, outs, x, prologue=N.PRO_DYNQ8,
+                   e_x=0, norm_w=None, in_f=0, one_plus=False, x8_out=None,
+                   e_x_out=None, xn_out=None):
+        n = len(weights)
+        wa = (ctypes.c_void_p * n)(*[w.h.value for w in weights])
+        oa = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
+        ea = np.ascontiguousarray(epilogues, dtype=np.int32)
+        pa = np.ascontiguousarray(p0s, dtype=np.int32)
+        N.check(N.lib().w4a8_site_async(
+            self.h, n, wa, _ptr(ea), _ptr(pa), oa, int(prologue), _dptr(x),
+            _dptr(norm_w), int(in_f), 1 if one_plus else 0, int(e_x), _dptr(x8_out),
+            _dptr(e_x_out), _dptr(xn_out)), "site")
+
+    def head_argmax_async(self, w, x, result, prologue=N.PRO_DYNQ8, e_x=0,
+                          norm_w=None, in_f=0, one_plus=False):
+        N.check(N.lib().w4a8_head_argmax_async(
+            self.h, w.h, int(prologue), _dptr(x), _dptr(norm_w), int(in_f),
+            1 if one_plus else 0, int(e_x), _dptr(result)), "head_argmax")
+
+    def matmul_async(self, w, x8, y32):
+        N.check(N.lib().w4a8_matmul_y32_async(self.h, w.h, _dptr(x8), x8.shape[0],
+                                              _dptr(y32)), "matmul")
+
+
+_DEFAULT = None
+
+
+def default_context():
+    """Process-wide context on device 0, for the reference-named functions."""
+    global _DEFAULT
+    if _DEFAULT is None or _DEFAULT.h is None:
+        _DEFAULT = Context(0)
+    return _DEFAULT

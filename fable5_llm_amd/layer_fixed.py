@@ -1,0 +1,147 @@
+"""Drop-in for the matvec-path entry points of ref/layer_fixed.py and the
+MOVY / ALU / AMAX32 movers, computed on the MI355X engine.
+
+  matvec_fx(qw, x16, out_f)            layer_fixed.py:1201-1221
+  matvec_to(qw, x16, in_f, out_f)      layer_fixed.py:1224-1236 (one fused launch)
+  rmsnorm_fx(x16, w_q14, in_f, one_plus) layer_fixed.py:1242-1278
+  mlp_fx(xn16, qm, rs_f)               layer_fixed.py:1597-1604
+  movy(y32, shift, mode)               seq_model.py:1027-1050
+  alu_shift32/shift32w/silu32/emul32   gen_layer_script.py:1397-1423
+  Amax32 / head_argmax                 gen_layer_script.py:1424-1433,
+                                       gen_model_script.py:627-643
+
+A quantised matrix `qw` is the reference's dict {"w4", "m", "e", "sh"} (or
+an already-uploaded engine.Weights via qw["dev"]).
+"""
+import numpy as np
+
+from . import _native as N
+from .engine import default_context
+from .w4a8_ref import G, pack_ddr_rows
+
+RS_F_9B = 7      # layer_fixed.py:103 (9B operating point)
+MOVY_PAIRS32 = N.MOVY_PAIRS32
+MOVY_INT16 = N.MOVY_INT16
+
+
+def clip16(x):
+    return np.clip(np.asarray(x, dtype=np.int64), -32768, 32767)
+
+
+def _weights(qw):
+    """Upload (once per dict) the matrix of a quantised dict."""
+    w = qw.get("dev") if isinstance(qw, dict) else None
+    if w is not None and w.h is not None:
+        return w
+    g = int(qw.get("g", G))
+    assert g == G, "g=64 images are not executable by the 9B engine (g=128 only)"
+    w4 = np.asarray(qw["w4"])
+    img, _ = pack_ddr_rows(w4, qw["m"])
+    w = default_context().upload(img, w4.shape[0], w4.shape[1], int(qw["sh"]))
+    qw["dev"] = w
+    return w
+
+
+def shift_for(qw, e_x, in_f, out_f):
+    """MOVY shift (gen_layer_script.py:1753-1754)."""
+    return (15 - qw["e"] - qw["sh"]) - e_x + in_f - out_f
+
+
+def matvec_fx(qw, x16, out_f=None):
+    """DYNQ8 then matvec: returns (y32, e_x)."""
+    w = _weights(qw)
+    y, _x8, e_x, _ = default_context().matvec_fused(
+        w, np.asarray(x16, dtype=np.int16), prologue=N.PRO_DYNQ8,
+        epilogue=N.EPI_Y32)
+    return y, e_x
+
+
+def matvec_to(qw, x16, in_f, out_f):
+    """x16 (in_f frac) -> int64 y with out_f frac bits:
+    rshift_round(y32, (15-e-sh) - e_x + in_f - out_f), one device launch."""
+    w = _weights(qw)
+    p0 = (15 - int(qw["e"]) - int(qw["sh"])) + int(in_f) - int(out_f)
+    y, _x8, _e, _ = default_context().matvec_fused(
+        w, np.asarray(x16, dtype=np.int16), prologue=N.PRO_DYNQ8,
+        epilogue=N.EPI_SHIFT_I64, p0=p0)
+    return y
+
+
+def rmsnorm_fx(x16, w_q14, in_f, one_plus):
+    x = np.asarray(x16)
+    n = x.size
+    nbits = n.bit_length() - 1
+    assert n > 0 and (1 << nbits) == n, f"rmsnorm_fx: n={n} not a power of 2"
+    return default_context().rmsnorm(x, w_q14, in_f, one_plus).astype(np.int64)
+
+
+def movy(y32, shift, mode):
+    return default_context().movy(y32, shift, mode).astype(np.int64)
+
+
+def alu_shift32(y32, p0):
+    return default_context().alu(N.ALU_SHIFT32, y32, p0).astype(np.int64)
+
+
+def alu_shift32w(y32, p0):
+    return default_context().alu(N.ALU_SHIFT32W, y32, p0).astype(np.int64)
+
+
+def alu_silu32(y32, p0):
+    return default_context().alu(N.ALU_SILU32, y32, p0).astype(np.int64)
+
+
+def alu_emul32(y32, b16, p0):
+    return default_context().alu(N.ALU_EMUL32, y32, p0, b=b16).astype(np.int64)
+
+
+def mlp_fx(xn16, qm, rs_f=RS_F_9B):
+    """SwiGLU block: gate -> SILU32 (out_f 12), up -> SHIFT32W (out_f rs_f),
+    EMUL32 product, DYNQ8 -> down -> int16.  gate/up share one DYNQ8 site
+    and run fused in one launch; the product and down run on the device."""
+    ctx = default_context()
+    wg, wu, wd = _weights(qm["gate"]), _weights(qm["up"]), _weights(qm["down"])
+    x = np.asarray(xn16, dtype=np.int16)
+    # gate: clip(silu(clip(rs(y, p), +-2^20))) in Q12 (layer_fixed.py:1598-1601)
+    p_g = (15 - qm["gate"]["e"] - qm["gate"]["sh"]) + rs_f - 12
+    sg, _x8, e_x, _ = ctx.matvec_fused(wg, x, prologue=N.PRO_DYNQ8,
+                                       epilogue=N.EPI_SILU32, p0=p_g)
+    # up stays 32-bit (SHIFT32W), then EMUL32 by the gate (mlp_block,
+    # gen_layer_script.py:2176-2186).  layer_fixed.py:1602 multiplies the
+    # unclipped int64 value instead; the two agree whenever the shifted up
+    # value fits int32, i.e. for every right shift of a y32.
+    p_u = (15 - qm["up"]["e"] - qm["up"]["sh"]) + rs_f - rs_f
+    u, _, _, _ = ctx.matvec_fused(wu, x, prologue=N.PRO_DYNQ8,
+                                  epilogue=N.EPI_MOVY_P32, p0=p_u)
+    prod = ctx.alu(N.ALU_EMUL32, u, 12, b=sg)
+    p_d = (15 - qm["down"]["e"] - qm["down"]["sh"]) + rs_f - rs_f
+    y, _, _, _ = ctx.matvec_fused(wd, prod, prologue=N.PRO_DYNQ8,
+                                  epilogue=N.EPI_MOVY_I16, p0=p_d)
+    return y.astype(np.int64)
+
+
+class Amax32:
+    """AMAX32 running argmax over int32 chunks, fed on the host the way
+    the head loop feeds 2048-row chunks; the fused device path is
+    head_argmax()."""
+
+    def __init__(self):
+        self.val, self.idx, self.g, self.first = 0, 0, 0, True
+
+    def feed(self, y32, fresh=False):
+        if fresh:
+            self.g, self.first = 0, True
+        y = np.asarray(y32, dtype=np.int64)
+        if y.size:
+            i = int(np.argmax(y))          # first max inside the chunk
+            if self.first or int(y[i]) > self.val:
+                self.val, self.idx = int(y[i]), self.g + i
+            self.first = False
+            self.g += y.size
+        return self
+
+
+def head_argmax(qw, x, prologue=N.PRO_X8, norm_w=None, in_f=0, one_plus=False):
+    """LM head in one pass: (argmax row, its int32 y32), lowest index on ties."""
+    return default_context().head_argmax(_weights(qw), x, prologue=prologue,
+                                         norm_w=norm_w, in_f=in_f, one_plus=one_plus)

@@ -1,0 +1,174 @@
+/* fable5_w4a8.h -- C ABI of the MI355X W4A8 matvec engine.
+ *
+ * Replaces the FPGA matvec datapath of coreyhahn/fable5_llm
+ * (rtl/matvec_engine.sv, rtl/matvec_chan.sv, rtl/ddr_rd_streamer.sv and the
+ * DYNQ8 / MOVX / MOVY movers of rtl/seq_movers.sv + rtl/vec_alu.sv) and the
+ * Python law functions of ref/w4a8_ref.py and ref/fixedpoint.py that define
+ * it.  Every result is bit-exact with that integer law.
+ *
+ * Conventions
+ *   - every entry point returns int: W4A8_OK (0) or a negative W4A8_E_*;
+ *     w4a8_last_error() gives the message of the calling thread's last error
+ *   - host-buffer entry points are synchronous; *_async entry points take
+ *     DEVICE pointers and enqueue on the context's stream (see
+ *     w4a8_ctx_set_stream); a device-side y32 overflow raised by async work
+ *     is reported by the next w4a8_ctx_sync()
+ *   - one context per host thread; contexts are not internally locked
+ *   - weights are uploaded once as the reference's row image
+ *     (ref/w4a8_ref.py:349-370 pack_ddr_rows) and repacked on the device;
+ *     group size g = 128 (the 9B engine's only format, matvec_engine.sv:17-34)
+ */
+#ifndef FABLE5_W4A8_H
+#define FABLE5_W4A8_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes (mirror the reference's assertion classes) ---------- */
+#define W4A8_OK           0
+#define W4A8_E_SHAPE    (-1) /* K % 128, image size, m shape: w4a8_ref.py:104-105, 147-150, 439-440 */
+#define W4A8_E_ENVELOPE (-2) /* ng outside 1..96 or sh outside 0..63: hwmap.py:146-169, matvec_engine.sv:716-719 */
+#define W4A8_E_ACC_OVF  (-3) /* |acc| >= 2^31: w4a8_ref.py:285 (unreachable for int4 x int8 codes) */
+#define W4A8_E_Y32_OVF  (-4) /* |y32| >= 2^31: w4a8_ref.py:288 "y32 overflow — sh miscomputed" */
+#define W4A8_E_HIP      (-5) /* HIP runtime failure */
+#define W4A8_E_ARG      (-6) /* null / misaligned pointer, bad handle, bad enum */
+#define W4A8_E_RANGE    (-7) /* value outside the law's domain: rmsnorm n not a power of 2
+                                (layer_fixed.py:1270-1272), vocab > 2^18 (gen_model_script.py:564-565),
+                                ALU count > 16383 (gen_layer_script.py:1377-1386) */
+
+/* ---- prologue: how the int8 activation vector is produced ------------- */
+#define W4A8_PRO_X8             0 /* x is int8[K] already quantised, e_x supplied by caller */
+#define W4A8_PRO_DYNQ8          1 /* x is int16[K]: DYNQ8, fixedpoint.py:24-33 */
+#define W4A8_PRO_RMSNORM_DYNQ8  2 /* x is int16[K]: RMSNorm (layer_fixed.py:1242-1278) then DYNQ8 */
+
+/* ---- epilogue: what is written per output row ------------------------- */
+#define W4A8_EPI_Y32        0 /* int32 y32 (w4a8_ref.py:254-289) */
+#define W4A8_EPI_MOVY_I16   1 /* int16 clip16(rs_s(y32, shift)): MOVY int16 / SHIFT32 (seq_model.py:1027-1050) */
+#define W4A8_EPI_MOVY_P32   2 /* int32 clip32(rs_s(y32, shift)): MOVY pairs32 / SHIFT32W */
+#define W4A8_EPI_SILU32     3 /* int16 SILU32 (gen_layer_script.py:1409-1413) */
+#define W4A8_EPI_SHIFT_I64  4 /* int64 rs_s(y32, shift), no clip: layer_fixed.matvec_to (1224-1236) */
+/* shift = p0 - e_x (the MOVY IND_SUB XRF[0] encoding, seq_format.py:771-782).
+   MOVY-style shifts are capped as the RTL caps them: right by <= 63, left by
+   <= 40 (seq_movers.sv:770-777). */
+
+/* ---- ALU ops (rtl/vec_alu.sv op numbers) ------------------------------- */
+#define W4A8_ALU_SHIFT32   1
+#define W4A8_ALU_SILU32    6
+#define W4A8_ALU_EMUL32    8
+#define W4A8_ALU_SHIFT32W  9
+
+/* MOVY modes (seq_model.py MOVY_INT16 / pairs) */
+#define W4A8_MOVY_PAIRS32  0
+#define W4A8_MOVY_INT16    1
+
+typedef struct w4a8_ctx w4a8_ctx;
+typedef struct w4a8_weights w4a8_weights;
+typedef struct w4a8_plan w4a8_plan;
+
+const char *w4a8_version(void);
+const char *w4a8_last_error(void);
+
+/* ---- context (replaces the board lock + channel CSR block,
+ *      sw/board_lock.py, matvec_chan.sv:12-49) -------------------------- */
+int w4a8_ctx_create(int32_t device, w4a8_ctx **out);
+int w4a8_ctx_destroy(w4a8_ctx *ctx);
+/* run on a caller-owned hipStream_t (e.g. torch's current stream); NULL
+   restores the context's own stream */
+int w4a8_ctx_set_stream(w4a8_ctx *ctx, void *hip_stream);
+/* wait for the stream; returns W4A8_E_Y32_OVF if async work overflowed */
+int w4a8_ctx_sync(w4a8_ctx *ctx);
+/* number of compute units and the default persistent grid of the device */
+int w4a8_ctx_info(const w4a8_ctx *ctx, int32_t *num_cu, int32_t *grid);
+/* override the GEMV grid size (0 = default); for tuning sweeps */
+int w4a8_ctx_set_grid(w4a8_ctx *ctx, int32_t grid);
+/* the rsqrt seed LUT (512 Q1.15) and sigmoid knots (257 Q15) the device
+   uses: fixedpoint.py:42-53 and 128-142 (ROMs roms/rsqrt_rom.hex,
+   roms/sigmoid_rom.hex) */
+int w4a8_tables(w4a8_ctx *ctx, int32_t *rsqrt512, int32_t *sigmoid257);
+
+/* ---- weights (replaces the DDR weight image + WBASE/WBEATS/SHAPE CSRs,
+ *      w4a8_ref.py:349-370, matvec_chan.sv:12-49) ----------------------- */
+/* img: host row image of nrows rows, stride (K/128 + ceil(K/4096))*64 */
+int w4a8_weights_upload(w4a8_ctx *ctx, const uint8_t *img, int64_t nrows,
+                        int32_t K, int32_t sh, w4a8_weights **out);
+/* same, image already in device memory */
+int w4a8_weights_upload_async(w4a8_ctx *ctx, const uint8_t *d_img,
+                              int64_t nrows, int32_t K, int32_t sh,
+                              w4a8_weights **out);
+/* inverse repack to the row image (host buffer of nrows*stride bytes):
+   w4a8_ref.py:429-446 unpack_ddr_rows view */
+int w4a8_weights_download(w4a8_ctx *ctx, const w4a8_weights *w, uint8_t *img);
+int w4a8_weights_info(const w4a8_weights *w, int64_t *nrows, int32_t *K,
+                      int32_t *sh, int64_t *device_bytes);
+int w4a8_weights_free(w4a8_weights *w);
+
+/* ---- elementwise law (host buffers, synchronous) ---------------------- */
+/* w4a8_ref.py:90-99 rshift_round */
+int w4a8_rshift_round(w4a8_ctx *ctx, const int64_t *v, int64_t n, int32_t s,
+                      int64_t *out);
+/* fixedpoint.py:24-33 dyn_quant_i8 */
+int w4a8_dynq8(w4a8_ctx *ctx, const int16_t *x16, int32_t n, int8_t *x8,
+               int32_t *e);
+/* layer_fixed.py:1242-1278 rmsnorm_fx */
+int w4a8_rmsnorm(w4a8_ctx *ctx, const int16_t *x16, const int16_t *w_q14,
+                 int32_t n, int32_t in_f, int32_t one_plus, int16_t *out);
+/* seq_model.py:1027-1050 MOVY: out is int16[n] (INT16) or int32[n] (PAIRS32) */
+int w4a8_movy(w4a8_ctx *ctx, const int32_t *y32, int64_t n, int32_t shift,
+              int32_t mode, void *out);
+/* gen_layer_script.py:1397-1423 ALU ops on int32 pairs: SHIFT32, SILU32,
+   EMUL32 (b = int16[n]) -> int16 out; SHIFT32W -> int32 out */
+int w4a8_alu(w4a8_ctx *ctx, int32_t op, const int32_t *y32, const int16_t *b,
+             int64_t n, int32_t p0, void *out);
+
+/* ---- matvec (host buffers, synchronous) ------------------------------- */
+/* w4a8_ref.py:254-289 matvec_y32 */
+int w4a8_matvec_y32(w4a8_ctx *ctx, const w4a8_weights *w, const int8_t *x8,
+                    int32_t *y32);
+/* prologue -> matvec -> epilogue in one launch.  x: int8[K] (PRO_X8, e_x
+   taken from *e_x_io) or int16[K]; norm_w: int16[K] Q14 for
+   PRO_RMSNORM_DYNQ8 (one_plus selects vecnorm mode 0 = (1+w) / 1 = w);
+   out: per epilogue; x8_out (int8[K]), e_x_io, xn_out (int16[K], RMSNorm
+   output) are optional */
+int w4a8_matvec_fused(w4a8_ctx *ctx, const w4a8_weights *w, int32_t prologue,
+                      const void *x, const int16_t *norm_w, int32_t in_f,
+                      int32_t one_plus, int32_t epilogue, int32_t p0, void *out,
+                      int8_t *x8_out, int32_t *e_x_io, int16_t *xn_out);
+/* LM head: matvec + running argmax (AMAX32, strictly greater => lowest
+   index wins ties; gen_layer_script.py:1424-1433, gen_model_script.py:627-643) */
+int w4a8_head_argmax(w4a8_ctx *ctx, const w4a8_weights *w, int32_t prologue,
+                     const void *x, const int16_t *norm_w, int32_t in_f,
+                     int32_t one_plus, int32_t *idx, int32_t *val);
+/* batched: y32[b][n] = matvec_y32(w, x8[b][:]) for b < B (int8 MFMA) */
+int w4a8_matmul_y32(w4a8_ctx *ctx, const w4a8_weights *w, const int8_t *x8,
+                    int32_t B, int32_t *y32);
+
+/* ---- device-pointer variants (async on the context stream) ------------ */
+int w4a8_matvec_fused_async(w4a8_ctx *ctx, const w4a8_weights *w,
+                            int32_t prologue, const void *d_x,
+                            const int16_t *d_norm_w, int32_t in_f,
+                            int32_t one_plus, int32_t e_x, int32_t epilogue,
+                            int32_t p0, void *d_out, int8_t *d_x8_out,
+                            int32_t *d_e_x_out, int16_t *d_xn_out);
+/* several matrices sharing one input vector in one launch: the MOVX
+   broadcast + MVGO x4 analogue (seq_movers.sv:939-1029) */
+int w4a8_site_async(w4a8_ctx *ctx, int32_t nmat,
+                    const w4a8_weights *const *w, const int32_t *epilogue,
+                    const int32_t *p0, void *const *d_out, int32_t prologue,
+                    const void *d_x, const int16_t *d_norm_w, int32_t in_f,
+                    int32_t one_plus, int32_t e_x, int8_t *d_x8_out,
+                    int32_t *d_e_x_out, int16_t *d_xn_out);
+/* d_result: int32[2] = {idx, val} */
+int w4a8_head_argmax_async(w4a8_ctx *ctx, const w4a8_weights *w,
+                           int32_t prologue, const void *d_x,
+                           const int16_t *d_norm_w, int32_t in_f,
+                           int32_t one_plus, int32_t e_x, int32_t *d_result);
+int w4a8_matmul_y32_async(w4a8_ctx *ctx, const w4a8_weights *w,
+                          const int8_t *d_x8, int32_t B, int32_t *d_y32);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FABLE5_W4A8_H */

@@ -1,0 +1,45 @@
+"""Seeded synthetic inputs shared by the tests (no reference code)."""
+import numpy as np
+
+from oracle import law
+
+
+def rand_w4_m(rng, N, K, mlo=256, mhi=16385):
+    """int4 weights uniform in [-8, 7] and uint16 scale mantissas in
+    [mlo, mhi) (the log-uniform 2^-10..2^-4 fp16 scales of the benchmark
+    configurations map to e = -3, m in [256, 16384])."""
+    w4 = rng.integers(-8, 8, (N, K)).astype(np.int8)
+    m = rng.integers(mlo, mhi, (N, K // 128)).astype(np.uint16)
+    return w4, m
+
+
+def log_uniform_m(rng, shape):
+    """m = round(s * 2^18) for s = 2^U(-10, -4) (scale encoding a7, e = -3)."""
+    s = np.exp2(rng.uniform(-10.0, -4.0, shape))
+    return np.clip(np.round(s * (1 << 18)), 1, 65535).astype(np.uint16)
+
+
+def rand_image(rng, N, K, m=None):
+    """Row image straight from random bytes (fast for very large N): every
+    byte is two uniform int4 codes.  Returns (image uint8 array, m)."""
+    stride = law.row_stride(K)
+    img = np.zeros((N, stride), dtype=np.uint8)
+    img[:, :K // 2] = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    if m is None:
+        m = log_uniform_m(rng, (N, K // 128))
+    img[:, K // 2:K // 2 + 2 * (K // 128)] = m.astype('<u2').view(np.uint8).reshape(N, -1)
+    return img.reshape(-1), m
+
+
+def activation_x16(rng, K, frac=7):
+    """fp32 x ~ N(0,1) with 1 % outliers at +-20 -> int16 at `frac` fraction
+    bits (rint = round half to even)."""
+    x = rng.normal(0.0, 1.0, K)
+    idx = rng.choice(K, max(1, K // 100), replace=False)
+    x[idx] = 20.0 * rng.choice([-1.0, 1.0], idx.size)
+    return np.clip(np.rint(x * (1 << frac)), -32768, 32767).astype(np.int16)
+
+
+def norm_weight_q14(rng, K):
+    w = rng.normal(1.0, 0.1, K)
+    return np.clip(np.rint(w * (1 << 14)), -32768, 32767).astype(np.int16)
