@@ -190,14 +190,15 @@ size_t out_elem(int32_t epi) {
   }
 }
 
-int site_launch(w4a8_ctx *c, int32_t nmat, const w4a8_weights *const *w,
-                const int32_t *epi, const int32_t *p0, void *const *out,
-                int32_t prologue, const void *x, const int16_t *norm_w,
-                int32_t in_f, int32_t one_plus, int32_t e_x, int8_t *x8_out,
-                int32_t *e_x_out, int16_t *xn_out) {
+int site_params(w4a8_ctx *c, GemvParams &P, int32_t nmat,
+                const w4a8_weights *const *w, const int32_t *epi, const int32_t *p0,
+                void *const *out, int32_t prologue, const void *x,
+                const int16_t *norm_w, int32_t in_f, int32_t one_plus, int32_t e_x,
+                int8_t *x8_out, int32_t *e_x_out, int16_t *xn_out) {
   if (nmat < 1 || nmat > kMaxJobs)
     return fail(W4A8_E_ARG, "site holds 1.." + std::to_string(kMaxJobs) + " matrices");
-  GemvParams P{};
+  P = GemvParams{};
+  if (!w[0]) return fail(W4A8_E_ARG, "null weights");
   const int32_t K = w[0]->L.K;
   int rc = set_prologue(c, P, K, prologue, x, norm_w, in_f, one_plus, e_x);
   if (rc) return rc;
@@ -221,18 +222,31 @@ int site_launch(w4a8_ctx *c, int32_t nmat, const w4a8_weights *const *w,
   P.e_x_out = e_x_out;
   P.xn_out = xn_out;
   P.partials = nullptr;
-  DeviceGuard g(c->device);
-  HIP_TRY(launch_gemv(P, grid_for(c, tiles), c->stream));
   return W4A8_OK;
 }
 
-int head_launch(w4a8_ctx *c, const w4a8_weights *w, int32_t prologue,
+int site_launch(w4a8_ctx *c, int32_t nmat, const w4a8_weights *const *w,
+                const int32_t *epi, const int32_t *p0, void *const *out,
+                int32_t prologue, const void *x, const int16_t *norm_w,
+                int32_t in_f, int32_t one_plus, int32_t e_x, int8_t *x8_out,
+                int32_t *e_x_out, int16_t *xn_out) {
+  GemvParams P;
+  int rc = site_params(c, P, nmat, w, epi, p0, out, prologue, x, norm_w, in_f,
+                       one_plus, e_x, x8_out, e_x_out, xn_out);
+  if (rc) return rc;
+  DeviceGuard g(c->device);
+  HIP_TRY(launch_gemv(P, grid_for(c, P.total_tiles), c->stream));
+  return W4A8_OK;
+}
+
+int head_params(w4a8_ctx *c, GemvParams &P, const w4a8_weights *w, int32_t prologue,
                 const void *x, const int16_t *norm_w, int32_t in_f,
-                int32_t one_plus, int32_t e_x, int32_t *d_result) {
+                int32_t one_plus, int32_t e_x) {
+  if (!w) return fail(W4A8_E_ARG, "null weights");
   if (w->nrows > (1 << 18))
     return fail(W4A8_E_RANGE, "vocab " + std::to_string(w->nrows) +
                                   " exceeds the 18-bit AMAX32 index (2^18)");
-  GemvParams P{};
+  P = GemvParams{};
   int rc = set_prologue(c, P, w->L.K, prologue, x, norm_w, in_f, one_plus, e_x);
   if (rc) return rc;
   P.job[0].w = w->d;
@@ -244,6 +258,15 @@ int head_launch(w4a8_ctx *c, const w4a8_weights *w, int32_t prologue,
   P.job[0].p0 = 0;
   P.njobs = 1;
   P.total_tiles = (int32_t)w->ntiles;
+  return W4A8_OK;
+}
+
+int head_launch(w4a8_ctx *c, const w4a8_weights *w, int32_t prologue,
+                const void *x, const int16_t *norm_w, int32_t in_f,
+                int32_t one_plus, int32_t e_x, int32_t *d_result) {
+  GemvParams P;
+  int rc = head_params(c, P, w, prologue, x, norm_w, in_f, one_plus, e_x);
+  if (rc) return rc;
   const int grid = grid_for(c, w->ntiles);
   if ((rc = ensure_partials(c, grid))) return rc;
   P.partials = c->d_partials;
@@ -694,6 +717,165 @@ int w4a8_matmul_y32_async(w4a8_ctx *c, const w4a8_weights *w, const int8_t *d_x8
   DeviceGuard g(c->device);
   HIP_TRY(launch_matmul(w->d, (int32_t)w->nrows, w->L, w->sh, d_x8, B, d_y32, c->d_err,
                         c->stream));
+  return W4A8_OK;
+}
+
+// ------------------------------------------------------------------ plans
+struct w4a8_plan {
+  w4a8_ctx *ctx = nullptr;
+  int32_t mode = W4A8_PLAN_GRAPH;
+  struct Step {
+    GemvParams P;
+    int grid;
+    bool head;
+    int32_t *result;
+  };
+  std::vector<Step> steps;
+  uint64_t *d_partials = nullptr;   // head partial keys (own buffer: graphs pin it)
+  int partials_cap = 0;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  hipStream_t exec_stream = nullptr;
+};
+
+static void plan_drop_graph(w4a8_plan *p) {
+  if (p->exec) (void)hipGraphExecDestroy(p->exec);
+  if (p->graph) (void)hipGraphDestroy(p->graph);
+  p->exec = nullptr;
+  p->graph = nullptr;
+}
+
+static int plan_enqueue(w4a8_plan *p, hipStream_t s) {
+  for (auto &st : p->steps) {
+    HIP_TRY(launch_gemv(st.P, st.grid, s));
+    if (st.head) HIP_TRY(launch_argmax_final(st.P.partials, st.grid, st.result, s));
+  }
+  return W4A8_OK;
+}
+
+int w4a8_plan_create(w4a8_ctx *c, w4a8_plan **out) {
+  if (!c || !out) return fail(W4A8_E_ARG, "null argument");
+  *out = new w4a8_plan();
+  (*out)->ctx = c;
+  return W4A8_OK;
+}
+
+int w4a8_plan_add_site(w4a8_plan *p, int32_t nmat, const w4a8_weights *const *w,
+                       const int32_t *epilogue, const int32_t *p0, void *const *d_out,
+                       int32_t prologue, const void *d_x, const int16_t *d_norm_w,
+                       int32_t in_f, int32_t one_plus, int32_t e_x, int8_t *d_x8_out,
+                       int32_t *d_e_x_out, int16_t *d_xn_out) {
+  if (!p || !w || !epilogue || !p0 || !d_out) return fail(W4A8_E_ARG, "null argument");
+  w4a8_plan::Step st{};
+  int rc = site_params(p->ctx, st.P, nmat, w, epilogue, p0, d_out, prologue, d_x,
+                       d_norm_w, in_f, one_plus, e_x, d_x8_out, d_e_x_out, d_xn_out);
+  if (rc) return rc;
+  st.grid = grid_for(p->ctx, st.P.total_tiles);
+  st.head = false;
+  st.result = nullptr;
+  p->steps.push_back(st);
+  plan_drop_graph(p);
+  return W4A8_OK;
+}
+
+int w4a8_plan_add_head(w4a8_plan *p, const w4a8_weights *w, int32_t prologue,
+                       const void *d_x, const int16_t *d_norm_w, int32_t in_f,
+                       int32_t one_plus, int32_t e_x, int32_t *d_result) {
+  if (!p || !d_result) return fail(W4A8_E_ARG, "null argument");
+  w4a8_plan::Step st{};
+  int rc = head_params(p->ctx, st.P, w, prologue, d_x, d_norm_w, in_f, one_plus, e_x);
+  if (rc) return rc;
+  st.grid = grid_for(p->ctx, st.P.total_tiles);
+  st.head = true;
+  st.result = d_result;
+  // every head of the plan gets its own slice of the partials buffer
+  int used = 0;
+  for (auto &o : p->steps) if (o.head) used += o.grid;
+  if (used + st.grid > p->partials_cap) {
+    DeviceGuard g(p->ctx->device);
+    const int cap = (used + st.grid) * 2;
+    uint64_t *np_ = nullptr;
+    HIP_TRY(hipMalloc(&np_, sizeof(uint64_t) * (size_t)cap));
+    if (p->d_partials) {
+      (void)hipDeviceSynchronize();
+      (void)hipFree(p->d_partials);
+    }
+    p->d_partials = np_;
+    p->partials_cap = cap;
+    int off = 0;
+    for (auto &o : p->steps)
+      if (o.head) { o.P.partials = p->d_partials + off; off += o.grid; }
+  }
+  st.P.partials = p->d_partials + used;
+  p->steps.push_back(st);
+  plan_drop_graph(p);
+  return W4A8_OK;
+}
+
+int w4a8_plan_set_mode(w4a8_plan *p, int32_t mode) {
+  if (!p || mode != W4A8_PLAN_GRAPH) return fail(W4A8_E_ARG, "unknown plan mode");
+  p->mode = mode;
+  return W4A8_OK;
+}
+
+int w4a8_plan_run(w4a8_plan *p) {
+  if (!p) return fail(W4A8_E_ARG, "null plan");
+  if (p->steps.empty()) return W4A8_OK;
+  w4a8_ctx *c = p->ctx;
+  DeviceGuard g(c->device);
+  if (p->exec && p->exec_stream != c->stream) plan_drop_graph(p);
+  if (!p->exec) {
+    HIP_TRY(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    int rc = plan_enqueue(p, c->stream);
+    hipGraph_t gr = nullptr;
+    hipError_t e = hipStreamEndCapture(c->stream, &gr);
+    if (rc) {
+      if (gr) (void)hipGraphDestroy(gr);
+      return rc;
+    }
+    if (e != hipSuccess)
+      return fail(W4A8_E_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(e));
+    p->graph = gr;
+    HIP_TRY(hipGraphInstantiate(&p->exec, p->graph, nullptr, nullptr, 0));
+    p->exec_stream = c->stream;
+  }
+  HIP_TRY(hipGraphLaunch(p->exec, c->stream));
+  return W4A8_OK;
+}
+
+int w4a8_plan_profile(w4a8_plan *p, int32_t n, float *ms) {
+  if (!p || (n > 0 && !ms)) return fail(W4A8_E_ARG, "null argument");
+  if (n != (int32_t)p->steps.size())
+    return fail(W4A8_E_ARG, "plan has " + std::to_string(p->steps.size()) + " steps");
+  w4a8_ctx *c = p->ctx;
+  DeviceGuard g(c->device);
+  std::vector<hipEvent_t> ev(2 * p->steps.size(), nullptr);
+  int rc = W4A8_OK;
+  for (auto &e : ev)
+    if (hipEventCreate(&e) != hipSuccess) rc = fail(W4A8_E_HIP, "hipEventCreate");
+  for (size_t i = 0; !rc && i < p->steps.size(); ++i) {
+    auto &st = p->steps[i];
+    hipError_t e = launch_gemv_timed(st.P, st.grid, c->stream, ev[2 * i], ev[2 * i + 1]);
+    if (e == hipSuccess && st.head)
+      e = launch_argmax_final(st.P.partials, st.grid, st.result, c->stream);
+    if (e != hipSuccess) rc = fail(W4A8_E_HIP, hipGetErrorString(e));
+  }
+  if (!rc && hipStreamSynchronize(c->stream) != hipSuccess) rc = fail(W4A8_E_HIP, "sync");
+  for (size_t i = 0; !rc && i < p->steps.size(); ++i)
+    if (hipEventElapsedTime(&ms[i], ev[2 * i], ev[2 * i + 1]) != hipSuccess)
+      rc = fail(W4A8_E_HIP, "hipEventElapsedTime");
+  for (auto &e : ev)
+    if (e) (void)hipEventDestroy(e);
+  return rc;
+}
+
+int w4a8_plan_destroy(w4a8_plan *p) {
+  if (!p) return W4A8_OK;
+  DeviceGuard g(p->ctx->device);
+  (void)hipStreamSynchronize(p->ctx->stream);
+  plan_drop_graph(p);
+  if (p->d_partials) (void)hipFree(p->d_partials);
+  delete p;
   return W4A8_OK;
 }
 

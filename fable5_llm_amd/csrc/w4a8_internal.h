@@ -105,6 +105,9 @@ hipError_t launch_repack(const uint8_t *img, int64_t nrows, const Layout &L,
 hipError_t launch_unpack(const uint8_t *src, int64_t nrows, const Layout &L,
                          int64_t stride, uint8_t *img, hipStream_t s);
 hipError_t launch_gemv(const GemvParams &p, int grid, hipStream_t s);
+// same launch bracketed by events recorded by the dispatch itself
+hipError_t launch_gemv_timed(const GemvParams &p, int grid, hipStream_t s,
+                             hipEvent_t start, hipEvent_t stop);
 hipError_t launch_argmax_final(const uint64_t *partials, int n,
                                int32_t *result, hipStream_t s);
 hipError_t launch_rshift_round(const int64_t *v, int64_t n, int s,

@@ -84,8 +84,13 @@ class Context:
 
     # ------------------------------------------------------------ control
     def set_stream(self, stream=None):
-        """Run on a torch.cuda.Stream (or raw hipStream_t int); None = own."""
-        s = None if stream is None else getattr(stream, "cuda_stream", stream)
+        """Run on a torch.cuda.Stream (or raw hipStream_t int); None = the
+        context's own stream.  The null/legacy stream (handle 0) cannot be
+        selected: pass a created stream."""
+        s = None if stream is None else int(getattr(stream, "cuda_stream", stream))
+        if stream is not None and s == 0:
+            raise ValueError("the null stream cannot be selected; use a "
+                             "torch.cuda.Stream() created for the engine")
         N.check(N.lib().w4a8_ctx_set_stream(self.h, ctypes.c_void_p(s)))
 
     def set_grid(self, grid):
@@ -247,3 +252,60 @@ def default_context():
     if _DEFAULT is None or _DEFAULT.h is None:
         _DEFAULT = Context(0)
     return _DEFAULT
+
+
+class Plan:
+    """A fixed sequence of sites (matrices sharing one input vector) and LM
+    heads, replayed as one HIP graph with the site order kept.  Holds
+    references to every device tensor it was given."""
+
+    def __init__(self, ctx):
+        self.ctx = ctx
+        h = ctypes.c_void_p()
+        N.check(N.lib().w4a8_plan_create(ctx.h, ctypes.byref(h)), "plan_create")
+        self.h = h
+        self._keep = []
+        self.bytes = 0        # algorithmic weight bytes per replay
+        self.nsites = 0
+        self.nmats = 0
+
+    def add_site(self, weights, epilogues, p0s, outs, x, prologue=N.PRO_DYNQ8,
+                 e_x=0, norm_w=None, in_f=0, one_plus=False, x8_out=None,
+                 e_x_out=None, xn_out=None):
+        n = len(weights)
+        wa = (ctypes.c_void_p * n)(*[w.h.value for w in weights])
+        oa = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
+        ea = np.ascontiguousarray(epilogues, dtype=np.int32)
+        pa = np.ascontiguousarray(p0s, dtype=np.int32)
+        N.check(N.lib().w4a8_plan_add_site(
+            self.h, n, wa, _ptr(ea), _ptr(pa), oa, int(prologue), _dptr(x),
+            _dptr(norm_w), int(in_f), 1 if one_plus else 0, int(e_x),
+            _dptr(x8_out), _dptr(e_x_out), _dptr(xn_out)), "plan_add_site")
+        self._keep += [weights, outs, x, norm_w, x8_out, e_x_out, xn_out]
+        self.bytes += sum(w.wire_bytes for w in weights)
+        self.nsites += 1
+        self.nmats += n
+
+    def add_head(self, w, x, result, prologue=N.PRO_DYNQ8, e_x=0, norm_w=None,
+                 in_f=0, one_plus=False):
+        N.check(N.lib().w4a8_plan_add_head(
+            self.h, w.h, int(prologue), _dptr(x), _dptr(norm_w), int(in_f),
+            1 if one_plus else 0, int(e_x), _dptr(result)), "plan_add_head")
+        self._keep += [w, x, result, norm_w]
+        self.bytes += w.wire_bytes
+        self.nsites += 1
+        self.nmats += 1
+
+    def run(self):
+        N.check(N.lib().w4a8_plan_run(self.h), "plan_run")
+
+    def profile(self):
+        """Per-step GEMV kernel times in ms (one eager, instrumented pass)."""
+        ms = np.zeros(self.nsites, dtype=np.float32)
+        N.check(N.lib().w4a8_plan_profile(self.h, self.nsites, _ptr(ms)), "plan_profile")
+        return ms
+
+    def close(self):
+        if self.h:
+            N.lib().w4a8_plan_destroy(self.h)
+            self.h = None

@@ -1,0 +1,229 @@
+"""The Qwen3.5-9B-shaped decode weight stream: 249 W4A8 matrices at hidden
+4096 / FFN 12288 / vocab 248,320 in sequencer order, grouped into the 129
+DYNQ8 sites that feed them.
+
+Schedule (per layer, layer_types = (DN, DN, DN, ATTN) x 8 as in
+ref/qwen3_5_9b_config.json):
+  DN   ln1 RMSNorm site: in_qkv 8192, in_z 4096, in_b 32, in_a 32
+       (gen_layer_script.py:1945-1952)
+       gated-heads site (in_f 11): out 4096            (:2046-2049)
+  ATTN ln1 RMSNorm site: q_proj 8192, k_proj 1024, v_proj 1024 (:2068-2073)
+       gated-heads site (in_f 8+15-k_a, k_a = 10): o_proj 4096 (:2153-2159)
+  both ln2 RMSNorm site: gate 12288 (SILU32, out_f 12), up 12288 (SHIFT32W)
+       SwiGLU-product site (FFN 12288): down 4096       (:2166-2190)
+  head: final RMSNorm (mode 1, (1+w) folded at Q3.12) -> DYNQ8 -> 248,320-row
+        head -> AMAX32 argmax on raw y32 (gen_model_script.py:627-643)
+Fixed-point formats: RS_F = 7, QKV_F = 8, DN_NORM_F = 11
+(layer_fixed.py:103-147, 404).  Every matrix shares scale exponent e = -3
+(log-uniform 2^-10..2^-4 scales) and sh = 7 (K 4096) / 9 (K 12288).
+"""
+from dataclasses import dataclass, field
+from typing import List
+
+from . import _native as N
+
+H, FFN, VOCAB = 4096, 12288, 248320
+RS_F, QKV_F, DN_NORM_F = 7, 8, 11
+K_A = 10                     # o_proj block-floating shift k_a (measured 8..12)
+E_SCALE = -3
+LAYER_TYPES = ["linear_attention"] * 3 + ["full_attention"]
+LAYER_TYPES = LAYER_TYPES * 8
+
+
+def sh_for_k(K):
+    bound = (K // 128) * 65535 * (128 * 8 * 127)
+    return max(0, bound.bit_length() - 31)
+
+
+@dataclass
+class Mat:
+    name: str
+    nrows: int
+    K: int
+    out_f: int
+    epi: int
+
+    @property
+    def bytes(self):
+        ng = self.K // 128
+        return self.nrows * (ng + (ng + 31) // 32) * 64
+
+    def p0(self, in_f):
+        """MOVY p0: shift = p0 - e_x (gen_layer_script.py:1753-1754)."""
+        return (15 - E_SCALE - sh_for_k(self.K)) + in_f - self.out_f
+
+
+@dataclass
+class Site:
+    name: str
+    K: int
+    in_f: int
+    prologue: int
+    mats: List[Mat] = field(default_factory=list)
+    one_plus: bool = True
+    head: bool = False
+
+
+def schedule():
+    """The 129 sites of one decode step, in order."""
+    I16, P32, SILU = N.EPI_MOVY_I16, N.EPI_MOVY_P32, N.EPI_SILU32
+    rms, dq = N.PRO_RMSNORM_DYNQ8, N.PRO_DYNQ8
+    sites = []
+    for li, lt in enumerate(LAYER_TYPES):
+        if lt == "linear_attention":
+            sites.append(Site(f"L{li}.ln1", H, RS_F, rms, [
+                Mat(f"L{li}.in_qkv", 8192, H, RS_F, I16),
+                Mat(f"L{li}.in_z", 4096, H, QKV_F, I16),
+                Mat(f"L{li}.in_b", 32, H, 12, I16),
+                Mat(f"L{li}.in_a", 32, H, 12, I16)]))
+            sites.append(Site(f"L{li}.dn_heads", H, DN_NORM_F, dq, [
+                Mat(f"L{li}.out", 4096, H, RS_F, I16)]))
+        else:
+            sites.append(Site(f"L{li}.ln1", H, RS_F, rms, [
+                Mat(f"L{li}.q_proj", 8192, H, QKV_F, I16),
+                Mat(f"L{li}.k_proj", 1024, H, QKV_F, I16),
+                Mat(f"L{li}.v_proj", 1024, H, QKV_F, I16)]))
+            sites.append(Site(f"L{li}.attn_heads", H, QKV_F + 15 - K_A, dq, [
+                Mat(f"L{li}.o_proj", 4096, H, RS_F, I16)]))
+        sites.append(Site(f"L{li}.ln2", H, RS_F, rms, [
+            Mat(f"L{li}.gate", FFN, H, 12, SILU),
+            Mat(f"L{li}.up", FFN, H, RS_F, P32)]))
+        sites.append(Site(f"L{li}.swiglu", FFN, RS_F, dq, [
+            Mat(f"L{li}.down", H, FFN, RS_F, I16)]))
+    sites.append(Site("final_norm", H, RS_F, rms,
+                      [Mat("lm_head", VOCAB, H, 0, -1)], one_plus=False, head=True))
+    return sites
+
+
+def totals(sites=None):
+    sites = sites or schedule()
+    mats = [m for s in sites for m in s.mats]
+    return dict(sites=len(sites), matrices=len(mats),
+                bytes=sum(m.bytes for m in mats),
+                rmsnorm_sites=sum(1 for s in sites if s.prologue == N.PRO_RMSNORM_DYNQ8),
+                weights=sum(m.nrows * m.K for m in mats))
+
+
+def chunks_4chan(nrows, chunk=2048):
+    """MVGO count of one matrix on the reference's 4 DDR channels
+    (contiguous quarters split into <= 2048-row chunks,
+    seq_format.py:1177-1200)."""
+    q, r = divmod(nrows, 4)
+    parts = [q + (1 if i < r else 0) for i in range(4)]
+    return sum(-(-p // chunk) for p in parts if p)
+
+
+def chunks_head(nrows, chunk=2048):
+    """Interleaved 2048-row head chunks (seq_format.py:1237-1245)."""
+    return -(-nrows // chunk)
+
+
+# ---------------------------------------------------------------------------
+# device-resident synthetic stream
+# ---------------------------------------------------------------------------
+def synth_image(gen, nrows, K):
+    """Row image of random W4A8 weights on the device: every weight byte is
+    two uniform int4 codes; scales s = 2^U(-10, -4) encoded at e = -3 as
+    m = round(s * 2^18) (w4a8_ref.py:170-176)."""
+    import torch
+    ng = K // 128
+    stride = (ng + (ng + 31) // 32) * 64
+    img = torch.zeros((nrows, stride), dtype=torch.uint8, device=gen.device)
+    img[:, :K // 2] = torch.randint(0, 256, (nrows, K // 2), dtype=torch.uint8,
+                                    device=gen.device, generator=gen)
+    u = torch.rand((nrows, ng), dtype=torch.float64, device=gen.device, generator=gen)
+    m = torch.clamp(torch.round(torch.exp2(-10.0 + 6.0 * u) * (1 << 18)), 1, 65535)
+    m = m.to(torch.int32)
+    img[:, K // 2:K // 2 + 2 * ng] = torch.stack(
+        [m & 0xFF, m >> 8], dim=-1).reshape(nrows, 2 * ng).to(torch.uint8)
+    return img.reshape(-1)
+
+
+def synth_x16(gen, K, frac):
+    """fp32 x ~ N(0,1) with 1 % outliers at +-20, as int16 with `frac`
+    fraction bits (round half to even)."""
+    import torch
+    x = torch.randn(K, dtype=torch.float64, device=gen.device, generator=gen)
+    n_out = max(1, K // 100)
+    idx = torch.randperm(K, device=gen.device, generator=gen)[:n_out]
+    sign = torch.randint(0, 2, (n_out,), device=gen.device, generator=gen) * 2 - 1
+    x[idx] = 20.0 * sign.to(torch.float64)
+    return torch.clamp(torch.round(x * (1 << frac)), -32768, 32767).to(torch.int16)
+
+
+def synth_norm_w(gen, K, one_plus):
+    """RMSNorm weight w ~ N(1, 0.1): zero-centred Q14 for mode 0 (one_plus),
+    the folded (1+w) at Q3.12 for the final norm's mode 1
+    (gen_model_script.py:502-510)."""
+    import torch
+    w = 1.0 + 0.1 * torch.randn(K, dtype=torch.float64, device=gen.device,
+                                generator=gen)
+    q = torch.round((w - 1.0) * (1 << 14)) if one_plus else torch.round(w * (1 << 12))
+    return torch.clamp(q, -32768, 32767).to(torch.int16)
+
+
+class Stream9B:
+    """All 249 matrices resident on one device with their inputs and
+    outputs, wired into one Plan (site order kept)."""
+
+    def __init__(self, ctx, seed=0, sites=None):
+        import torch
+        from .engine import Plan
+        self.ctx = ctx
+        self.sites = sites or schedule()
+        dev = torch.device("cuda", ctx.device)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+        self.e_x = torch.zeros(len(self.sites), dtype=torch.int32, device=dev)
+        self.inputs, self.weights, self.outs, self.x8 = [], [], [], []
+        self.plan = Plan(ctx)
+        for si, s in enumerate(self.sites):
+            x = synth_x16(gen, s.K, s.in_f)
+            nw = synth_norm_w(gen, s.K, s.one_plus) if s.prologue == N.PRO_RMSNORM_DYNQ8 else None
+            x8 = torch.empty(s.K, dtype=torch.int8, device=dev)
+            ws, outs, imgs = [], [], []
+            for m in s.mats:
+                imgs.append(synth_image(gen, m.nrows, m.K))
+            # the images were written on torch's stream; the engine may run
+            # on its own: order the repack after them, and keep them alive
+            # until it has run
+            torch.cuda.current_stream(dev).synchronize()
+            for m, img in zip(s.mats, imgs):
+                ws.append(ctx.upload(img, m.nrows, m.K, sh_for_k(m.K)))
+            for m in s.mats:
+                if s.head:
+                    outs.append(torch.zeros(2, dtype=torch.int32, device=dev))
+                else:
+                    dt = torch.int32 if m.epi == N.EPI_MOVY_P32 else torch.int16
+                    outs.append(torch.zeros(m.nrows, dtype=dt, device=dev))
+            ctx.sync()
+            del imgs
+            if s.head:
+                self.plan.add_head(ws[0], x, outs[0], prologue=s.prologue, norm_w=nw,
+                                   in_f=s.in_f, one_plus=s.one_plus)
+                # the head's DYNQ8 input is not exported by the fused launch
+                x8 = None
+            else:
+                self.plan.add_site(ws, [m.epi for m in s.mats],
+                                   [m.p0(s.in_f) for m in s.mats], outs, x,
+                                   prologue=s.prologue, norm_w=nw, in_f=s.in_f,
+                                   one_plus=s.one_plus, x8_out=x8,
+                                   e_x_out=self.e_x[si:si + 1])
+            self.inputs.append((x, nw))
+            self.weights.append(ws)
+            self.outs.append(outs)
+            self.x8.append(x8)
+        torch.cuda.synchronize(dev)
+        self.bytes = self.plan.bytes
+
+    def run(self):
+        self.plan.run()
+
+    def profile(self):
+        return self.plan.profile()
+
+    def close(self):
+        self.plan.close()
+        for ws in self.weights:
+            for w in ws:
+                w.free()

@@ -168,6 +168,31 @@ int w4a8_head_argmax_async(w4a8_ctx *ctx, const w4a8_weights *w,
 int w4a8_matmul_y32_async(w4a8_ctx *ctx, const w4a8_weights *w,
                           const int8_t *d_x8, int32_t B, int32_t *d_y32);
 
+/* ---- plans: a fixed sequence of sites (and the LM head) replayed as one
+ *      unit -- the record stream of one decode step (MOVX/MVGO/FENCE/MOVY
+ *      per site, seq_format.py:2077-2231) with the site order kept: site
+ *      s+1 starts after site s has completed.  All pointers are device
+ *      pointers captured at add time. ------------------------------------ */
+#define W4A8_PLAN_GRAPH       0 /* one launch per site, replayed as a HIP graph */
+int w4a8_plan_create(w4a8_ctx *ctx, w4a8_plan **out);
+int w4a8_plan_add_site(w4a8_plan *plan, int32_t nmat,
+                       const w4a8_weights *const *w, const int32_t *epilogue,
+                       const int32_t *p0, void *const *d_out, int32_t prologue,
+                       const void *d_x, const int16_t *d_norm_w, int32_t in_f,
+                       int32_t one_plus, int32_t e_x, int8_t *d_x8_out,
+                       int32_t *d_e_x_out, int16_t *d_xn_out);
+int w4a8_plan_add_head(w4a8_plan *plan, const w4a8_weights *w,
+                       int32_t prologue, const void *d_x,
+                       const int16_t *d_norm_w, int32_t in_f, int32_t one_plus,
+                       int32_t e_x, int32_t *d_result);
+int w4a8_plan_set_mode(w4a8_plan *plan, int32_t mode);
+/* enqueue one replay of the whole plan on the context stream */
+int w4a8_plan_run(w4a8_plan *plan);
+/* run every step once, each GEMV launch bracketed by dispatch-recorded
+   events; ms[i] = kernel time of step i (n = number of steps).  Synchronous. */
+int w4a8_plan_profile(w4a8_plan *plan, int32_t n, float *ms);
+int w4a8_plan_destroy(w4a8_plan *plan);
+
 #ifdef __cplusplus
 }
 #endif
