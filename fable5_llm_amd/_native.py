@@ -72,6 +72,16 @@ def lib():
     """Load the HIP engine; raises if it has not been built."""
     global _LIB
     if _LIB is None:
+        # One HIP runtime per process.  PyTorch-ROCm ships its own
+        # libamdhip64 (soname libamdhip64.so.7) and loads it by the
+        # unversioned name; loaded first, it also satisfies this library's
+        # libamdhip64.so.7 dependency, so torch tensors, streams and this
+        # engine share one runtime.  Loaded the other way round, torch
+        # would bring up a second runtime that sees no device.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         if not os.path.exists(LIB_PATH):
             raise ImportError(
                 f"{LIB_PATH} is missing: the W4A8 engine is a HIP library "

@@ -44,3 +44,18 @@ def test_status_codes_match_header():
                  re.findall(r"#define W4A8_(E_[A-Z0-9_]+)\s+\((-\d+)\)", text))
     for k, v in codes.items():
         assert getattr(_native, k) == v, k
+
+
+def test_single_hip_runtime_in_process():
+    """Loading the engine maps exactly one HIP and one HSA runtime (torch's,
+    when torch is installed), so torch tensors/streams are valid handles."""
+    import subprocess
+    import sys
+    code = ("import sys; sys.path.insert(0, %r)\n"
+            "from fable5_llm_amd import _native; _native.lib()\n"
+            "m = open('/proc/self/maps').read().splitlines()\n"
+            "print(len(set(l.split()[-1] for l in m if 'libamdhip64' in l)),"
+            " len(set(l.split()[-1] for l in m if 'libhsa-runtime64' in l)))" % ROOT)
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True,
+                         text=True, timeout=120).stdout.split()
+    assert out == ["1", "1"], out
