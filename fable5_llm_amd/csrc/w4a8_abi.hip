@@ -135,6 +135,8 @@ int take_err(w4a8_ctx *c) {
   if (h) {
     HIP_TRY(hipMemset(c->d_err, 0, sizeof(int32_t)));
     if (h & 1) return fail(W4A8_E_Y32_OVF, "y32 overflow — sh miscomputed");
+    if (h & 2)
+      return fail(W4A8_E_HIP, "a persistent plan's site-completion wait timed out");
   }
   return W4A8_OK;
 }
@@ -736,13 +738,75 @@ struct w4a8_plan {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   hipStream_t exec_stream = nullptr;
+  // persistent mode
+  GemvParams *d_sites = nullptr;
+  uint32_t *d_done = nullptr;
+  uint64_t *d_pkeys = nullptr;
+  int G = 0;
+  int head_site = -1;
+  int32_t *head_result = nullptr;
 };
+
+static void plan_drop_persistent(w4a8_plan *p) {
+  if (p->d_sites) (void)hipFree(p->d_sites);
+  if (p->d_done) (void)hipFree(p->d_done);
+  if (p->d_pkeys) (void)hipFree(p->d_pkeys);
+  p->d_sites = nullptr;
+  p->d_done = nullptr;
+  p->d_pkeys = nullptr;
+  p->G = 0;
+}
+
+static int plan_build_persistent(w4a8_plan *p) {
+  w4a8_ctx *c = p->ctx;
+  const int n = (int)p->steps.size();
+  p->head_site = -1;
+  for (int i = 0; i < n; ++i)
+    if (p->steps[i].head) {
+      if (i != n - 1 || p->head_site >= 0)
+        return fail(W4A8_E_ARG, "a persistent plan takes one LM head, as its last step");
+      p->head_site = i;
+      p->head_result = p->steps[i].result;
+    }
+  p->G = c->num_cu * stream_max_blocks_per_cu();
+  std::vector<GemvParams> sites(n);
+  int64_t off = 0;
+  for (int i = 0; i < n; ++i) {
+    sites[i] = p->steps[i].P;
+    sites[i].tile_rot = (int32_t)((p->G - off % p->G) % p->G);
+    off += sites[i].total_tiles;
+  }
+  HIP_TRY(hipMalloc(&p->d_sites, sizeof(GemvParams) * (size_t)n));
+  HIP_TRY(hipMalloc(&p->d_done, sizeof(uint32_t) * (size_t)n));
+  HIP_TRY(hipMalloc(&p->d_pkeys, sizeof(uint64_t) * (size_t)p->G));
+  HIP_TRY(hipMemcpy(p->d_sites, sites.data(), sizeof(GemvParams) * (size_t)n,
+                    hipMemcpyHostToDevice));
+  return W4A8_OK;
+}
+
+static int plan_launch_persistent(w4a8_plan *p, hipStream_t s, hipEvent_t e0,
+                                  hipEvent_t e1) {
+  StreamParams sp{};
+  sp.sites = p->d_sites;
+  sp.nsites = (int32_t)p->steps.size();
+  sp.head_site = p->head_site;
+  sp.done = p->d_done;
+  sp.err = p->ctx->d_err;
+  sp.partials = p->d_pkeys;
+  HIP_TRY(launch_fill_i32((int32_t *)p->d_done, 0, sp.nsites, s));
+  if (e0) HIP_TRY(hipEventRecord(e0, s));
+  HIP_TRY(launch_stream(sp, p->G, s));
+  if (e1) HIP_TRY(hipEventRecord(e1, s));
+  if (p->head_site >= 0) HIP_TRY(launch_argmax_final(p->d_pkeys, p->G, p->head_result, s));
+  return W4A8_OK;
+}
 
 static void plan_drop_graph(w4a8_plan *p) {
   if (p->exec) (void)hipGraphExecDestroy(p->exec);
   if (p->graph) (void)hipGraphDestroy(p->graph);
   p->exec = nullptr;
   p->graph = nullptr;
+  plan_drop_persistent(p);
 }
 
 static int plan_enqueue(w4a8_plan *p, hipStream_t s) {
@@ -813,7 +877,9 @@ int w4a8_plan_add_head(w4a8_plan *p, const w4a8_weights *w, int32_t prologue,
 }
 
 int w4a8_plan_set_mode(w4a8_plan *p, int32_t mode) {
-  if (!p || mode != W4A8_PLAN_GRAPH) return fail(W4A8_E_ARG, "unknown plan mode");
+  if (!p || (mode != W4A8_PLAN_GRAPH && mode != W4A8_PLAN_PERSISTENT))
+    return fail(W4A8_E_ARG, "unknown plan mode");
+  if (mode != p->mode) plan_drop_graph(p);
   p->mode = mode;
   return W4A8_OK;
 }
@@ -823,6 +889,16 @@ int w4a8_plan_run(w4a8_plan *p) {
   if (p->steps.empty()) return W4A8_OK;
   w4a8_ctx *c = p->ctx;
   DeviceGuard g(c->device);
+  if (p->mode == W4A8_PLAN_PERSISTENT) {
+    if (!p->d_sites) {
+      int rc = plan_build_persistent(p);
+      if (rc) {
+        plan_drop_persistent(p);
+        return rc;
+      }
+    }
+    return plan_launch_persistent(p, c->stream, nullptr, nullptr);
+  }
   if (p->exec && p->exec_stream != c->stream) plan_drop_graph(p);
   if (!p->exec) {
     HIP_TRY(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
@@ -849,6 +925,26 @@ int w4a8_plan_profile(w4a8_plan *p, int32_t n, float *ms) {
     return fail(W4A8_E_ARG, "plan has " + std::to_string(p->steps.size()) + " steps");
   w4a8_ctx *c = p->ctx;
   DeviceGuard g(c->device);
+  if (p->mode == W4A8_PLAN_PERSISTENT) {
+    // one launch runs every step: ms[0] = its kernel time, the rest 0
+    if (!p->d_sites) {
+      int rc = plan_build_persistent(p);
+      if (rc) return rc;
+    }
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    HIP_TRY(hipEventCreate(&e0));
+    HIP_TRY(hipEventCreate(&e1));
+    int rc = plan_launch_persistent(p, c->stream, e0, e1);
+    if (!rc && hipStreamSynchronize(c->stream) != hipSuccess) rc = fail(W4A8_E_HIP, "sync");
+    if (!rc) {
+      for (int i = 0; i < n; ++i) ms[i] = 0.f;
+      if (hipEventElapsedTime(&ms[0], e0, e1) != hipSuccess)
+        rc = fail(W4A8_E_HIP, "hipEventElapsedTime");
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return rc;
+  }
   std::vector<hipEvent_t> ev(2 * p->steps.size(), nullptr);
   int rc = W4A8_OK;
   for (auto &e : ev)

@@ -89,7 +89,8 @@ struct GemvParams {
   int64_t tile_bytes;
   const void *x;            // int8[K] or int16[K]
   const int16_t *norm_w;    // int16[K] Q14 (RMSNorm)
-  int32_t in_f, one_plus, e_x_given, pad_;
+  int32_t in_f, one_plus, e_x_given;
+  int32_t tile_rot;         // persistent stream: first tile of WG r is (r + tile_rot) % G
   int8_t *x8_out;           // optional (written by workgroup 0)
   int32_t *e_x_out;         // optional
   int16_t *xn_out;          // optional RMSNorm output
@@ -108,6 +109,19 @@ hipError_t launch_gemv(const GemvParams &p, int grid, hipStream_t s);
 // same launch bracketed by events recorded by the dispatch itself
 hipError_t launch_gemv_timed(const GemvParams &p, int grid, hipStream_t s,
                              hipEvent_t start, hipEvent_t stop);
+// Persistent decode-step kernel: every site of a plan in one cooperative
+// launch, site order kept by per-site completion counters.
+struct StreamParams {
+  const GemvParams *sites;  // device array, nsites entries
+  int32_t nsites;
+  int32_t head_site;        // index of the LM-head site, or -1
+  uint32_t *done;           // nsites counters, zero at launch
+  int32_t *err;             // bit 1: a completion wait gave up
+  uint64_t *partials;       // head: one key per workgroup
+};
+hipError_t launch_stream(const StreamParams &sp, int grid, hipStream_t s);
+int stream_max_blocks_per_cu();
+
 hipError_t launch_argmax_final(const uint64_t *partials, int n,
                                int32_t *result, hipStream_t s);
 hipError_t launch_rshift_round(const int64_t *v, int64_t n, int s,

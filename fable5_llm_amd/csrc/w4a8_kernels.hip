@@ -125,6 +125,11 @@ __device__ __forceinline__ void piece_set(int4 &p, int j, int16_t v) {
   else       *w = (int32_t)(((uint32_t)*w & 0xFFFF0000u) | (uint32_t)(uint16_t)v);
 }
 
+// rshift_round of |v| * 2^-s with the sign of v restored (s uniform, >= 0)
+__device__ __forceinline__ uint64_t round_shift_mag(uint64_t mag, int s) {
+  return s == 0 ? mag : ((mag + ((uint64_t)1 << (s - 1))) >> s);
+}
+
 __device__ int run_prologue(const GemvParams &P, int8_t *xs, int64_t *sm) {
   const int tid = threadIdx.x;
   const int K = P.K;
@@ -147,22 +152,25 @@ __device__ int run_prologue(const GemvParams &P, int8_t *xs, int64_t *sm) {
     pc[c] = base < K ? *(const int4 *)(x16 + base) : make_int4(0, 0, 0, 0);
   }
   if (P.pro == PRO_RMSNORM_DYNQ8) {
-    // layer_fixed.py:1262-1278
-    int64_t ss = 0;
+    // layer_fixed.py:1262-1278, in sign-magnitude form: rshift_round rounds
+    // the magnitude, so |x * r| and |y * sc| carry the rounding and the
+    // sign is restored afterwards
+    uint64_t ss = 0;
 #pragma unroll
     for (int c = 0; c < kPieces; ++c)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int64_t v = piece_get(pc[c], j);
-        ss += v * v;
+        const int32_t v = piece_get(pc[c], j);
+        ss += (uint64_t)(uint32_t)(v * v);
       }
-    ss = block_sum_i64(ss, sm);
+    ss = (uint64_t)block_sum_i64((int64_t)ss, sm);
     if (ss == 0) ss = 1;
     const int nbits = 31 - __clz(K);
     int64_t r;
     int e;
-    rsqrt_q((uint64_t)ss, 2 * P.in_f + nbits, P.tables + kRsqrtOff, &r, &e);
-    const int64_t one = P.one_plus ? ((int64_t)1 << 14) : 0;
+    rsqrt_q(ss, 2 * P.in_f + nbits, P.tables + kRsqrtOff, &r, &e);
+    const int s1 = 30 - e;
+    const int32_t one = P.one_plus ? (1 << 14) : 0;
 #pragma unroll
     for (int c = 0; c < kPieces; ++c) {
       const int base = c * kWG * 8 + tid * 8;
@@ -170,10 +178,19 @@ __device__ int run_prologue(const GemvParams &P, int8_t *xs, int64_t *sm) {
         const int4 wv = *(const int4 *)(P.norm_w + base);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          int64_t y = rshr64((int64_t)piece_get(pc[c], j) * r, 30 - e);
-          y = clamp64(y, -((int64_t)1 << 32), ((int64_t)1 << 32) - 1);
-          const int64_t sc = (int64_t)piece_get(wv, j) + one;
-          piece_set(pc[c], j, (int16_t)clamp64(rshr64(y * sc, 14), -32768, 32767));
+          const int32_t xv = piece_get(pc[c], j);
+          const uint64_t mag = (uint64_t)(uint32_t)abs(xv) * (uint64_t)r;
+          uint64_t ym = s1 >= 0 ? round_shift_mag(mag, s1) : (mag << (-s1));
+          // clip to [-2^32, 2^32 - 1]
+          const uint64_t cap = xv < 0 ? ((uint64_t)1 << 32) : (((uint64_t)1 << 32) - 1);
+          ym = ym > cap ? cap : ym;
+          const int32_t sc = (int32_t)piece_get(wv, j) + one;
+          const uint64_t m2 = ym * (uint64_t)(uint32_t)abs(sc);
+          const uint64_t q = round_shift_mag(m2, 14);
+          const bool neg = (xv < 0) != (sc < 0);
+          const int32_t o = neg ? (q > 32768u ? -32768 : -(int32_t)q)
+                                : (q > 32767u ? 32767 : (int32_t)q);
+          piece_set(pc[c], j, (int16_t)o);
         }
         if (writer && P.xn_out) *(int4 *)(P.xn_out + base) = pc[c];
       }
@@ -187,6 +204,7 @@ __device__ int run_prologue(const GemvParams &P, int8_t *xs, int64_t *sm) {
   mx = block_max_i32(mx, sm);
   int e = 0;
   while (((mx + ((1 << e) >> 1)) >> e) > 127) ++e;
+  const int32_t half = (1 << e) >> 1;
 #pragma unroll
   for (int c = 0; c < kPieces; ++c) {
     const int base = c * kWG * 8 + tid * 8;
@@ -194,9 +212,9 @@ __device__ int run_prologue(const GemvParams &P, int8_t *xs, int64_t *sm) {
       uint32_t lo = 0, hi = 0;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        int64_t q = rshr64(piece_get(pc[c], j), e);
-        q = clamp64(q, -127, 127);
-        const uint32_t b = (uint32_t)(uint8_t)(int8_t)q;
+        const int32_t v = piece_get(pc[c], j);
+        const int32_t qm = min((abs(v) + half) >> e, 127);
+        const uint32_t b = (uint32_t)(uint8_t)(int8_t)(v < 0 ? -qm : qm);
         if (j < 4) lo |= b << (8 * j);
         else       hi |= b << (8 * (j - 4));
       }
@@ -301,6 +319,70 @@ __device__ __forceinline__ uint64_t argmax_key(int32_t v, uint32_t row) {
   return ((uint64_t)((uint32_t)v ^ 0x80000000u) << 32) | (uint64_t)(0xFFFFFFFFu - row);
 }
 
+// reduce a tile's 16 * p over the 4 k-quarter lanes and the 4 wavefronts,
+// then round, check and write the 16 rows (one wavefront, rotating per tile)
+__device__ __forceinline__ void tile_finish(const GemvJob &J, int t, int64_t p, int it,
+                                            int wave, int lane, int e_x,
+                                            const int32_t *sig, int32_t *err,
+                                            int64_t (*red)[kWaves][kTileRows],
+                                            uint64_t &best) {
+  p += __shfl_xor(p, 1);
+  p += __shfl_xor(p, 2);
+  const int par = it & 1;
+  if ((lane & 3) == 0) red[par][wave][lane >> 2] = p;
+  __syncthreads();
+  if (wave == (it & (kWaves - 1)) && lane < kTileRows) {
+    int64_t tot = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) tot += red[par][w][lane];
+    const int row = t * kTileRows + lane;
+    if (row < J.nrows) {
+      const int64_t y = rshr64(tot >> 4, J.sh);   // tot is 16 * p exactly
+      if (y > 2147483647LL || y < -2147483647LL) atomicOr(err, 1);
+      const int shift = J.p0 - e_x;
+      switch (J.epi) {
+        case EPI_Y32:
+          ((int32_t *)J.out)[row] = (int32_t)y;
+          break;
+        case EPI_MOVY_I16:
+          ((int16_t *)J.out)[row] = (int16_t)clamp64(movy_shift(y, shift), -32768, 32767);
+          break;
+        case EPI_MOVY_P32:
+          ((int32_t *)J.out)[row] =
+              (int32_t)clamp64(movy_shift(y, shift), -2147483648LL, 2147483647LL);
+          break;
+        case EPI_SILU32:
+          ((int16_t *)J.out)[row] = (int16_t)silu32(y, shift, sig);
+          break;
+        case EPI_SHIFT_I64:
+          ((int64_t *)J.out)[row] = movy_shift(y, shift);
+          break;
+        default: {   // EPI_ARGMAX: raw y32 (shift 0), seq_format.py:2225-2226
+          const uint64_t k = argmax_key((int32_t)y, (uint32_t)row);
+          best = k > best ? k : best;
+        }
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ void write_partial(uint64_t best, uint64_t *partials,
+                                              uint64_t *keys, int wave, int lane) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint64_t other = __shfl_xor(best, o);
+    best = other > best ? other : best;
+  }
+  __syncthreads();
+  if (lane == 0) keys[wave] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint64_t k = keys[0];
+    for (int w = 1; w < kWaves; ++w) k = keys[w] > k ? keys[w] : k;
+    partials[blockIdx.x] = k;
+  }
+}
+
 __global__ __launch_bounds__(kWG) void gemv_kernel(GemvParams P) {
   __shared__ __align__(16) int8_t xs[kKMax];
   __shared__ int32_t xlo[kKMax / 32];
@@ -342,62 +424,130 @@ __global__ __launch_bounds__(kWG) void gemv_kernel(GemvParams P) {
       p = dot_block(cur, groups_in(NG, b), b * kGroupsPerBlock, q, xs, xlo, p);
       if (more) cur = nxt;
     }
-    p += __shfl_xor(p, 1);
-    p += __shfl_xor(p, 2);
-    const int par = it & 1;
-    if ((lane & 3) == 0) red[par][wave][lane >> 2] = p;
-    __syncthreads();
-    if (wave == (it & (kWaves - 1)) && lane < kTileRows) {
-      int64_t tot = 0;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) tot += red[par][w][lane];
-      const int row = t * kTileRows + lane;
-      if (row < J.nrows) {
-        const int64_t y = rshr64(tot >> 4, J.sh);   // tot is 16 * p exactly
-        if (y > 2147483647LL || y < -2147483647LL) atomicOr(P.err, 1);
-        const int shift = J.p0 - e_x;
-        switch (J.epi) {
-          case EPI_Y32:
-            ((int32_t *)J.out)[row] = (int32_t)y;
-            break;
-          case EPI_MOVY_I16:
-            ((int16_t *)J.out)[row] =
-                (int16_t)clamp64(movy_shift(y, shift), -32768, 32767);
-            break;
-          case EPI_MOVY_P32:
-            ((int32_t *)J.out)[row] = (int32_t)clamp64(
-                movy_shift(y, shift), -2147483648LL, 2147483647LL);
-            break;
-          case EPI_SILU32:
-            ((int16_t *)J.out)[row] = (int16_t)silu32(y, shift, sig);
-            break;
-          case EPI_SHIFT_I64:
-            ((int64_t *)J.out)[row] = movy_shift(y, shift);
-            break;
-          default: {   // EPI_ARGMAX: raw y32 (shift 0), seq_format.py:2225-2226
-            const uint64_t k = argmax_key((int32_t)y, (uint32_t)row);
-            best = k > best ? k : best;
-          }
-        }
+    tile_finish(J, t, p, it, wave, lane, e_x, sig, P.err, red, best);
+  }
+  if (P.partials) write_partial(best, P.partials, keys, wave, lane);
+}
+
+// ---------------------------------------------------------------------------
+// persistent decode-step kernel
+//
+// One cooperative launch runs every site of a plan.  Workgroup r processes
+// tiles (r + tile_rot) mod G, + G, ... of each site; the 4 wavefronts split
+// a tile's scale blocks as in gemv_kernel.  Site s+1 starts (prologue and
+// compute) only after all G workgroups have finished site s, which they
+// signal on done[s]: the dependency a decode step has between consecutive
+// DYNQ8 sites.  Weights do not depend on any activation, so each wavefront
+// keeps its next (site, tile, block) in flight across that wait.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kSpinLimit = 1u << 21;   // ~0.1 s: a wait that never ends
+                                            // flags err bit 1 and moves on
+
+__device__ __forceinline__ int first_tile(const GemvParams &P, int rank, int G) {
+  return (rank + P.tile_rot) % G;
+}
+
+// next (site, tile, block) of this wavefront after (s, tg, b); site -1 = none
+__device__ __forceinline__ void next_item(const StreamParams &S, int s, int tg, int b,
+                                          int rank, int wave, int G, int &ns, int &ntg,
+                                          int &nb) {
+  const GemvParams &P = S.sites[s];
+  if (b + kWaves < P.nblk) {
+    ns = s; ntg = tg; nb = b + kWaves;
+    return;
+  }
+  if (tg + G < P.total_tiles) {
+    ns = s; ntg = tg + G; nb = wave;
+    return;
+  }
+  for (int s2 = s + 1; s2 < S.nsites; ++s2) {
+    const GemvParams &Q = S.sites[s2];
+    const int t0 = first_tile(Q, rank, G);
+    if (t0 < Q.total_tiles && wave < Q.nblk) {
+      ns = s2; ntg = t0; nb = wave;
+      return;
+    }
+  }
+  ns = -1; ntg = 0; nb = 0;
+}
+
+__device__ __forceinline__ void site_arrive(uint32_t *cnt) {
+  // every wavefront's output stores become visible device-wide before the
+  // workgroup's arrival is counted
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __syncthreads();
+  if (threadIdx.x == 0)
+    __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void site_wait(const uint32_t *cnt, uint32_t target,
+                                          int32_t *err) {
+  if (threadIdx.x == 0) {
+    uint32_t n = 0;
+    while (__hip_atomic_load(cnt, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < target) {
+      __builtin_amdgcn_s_sleep(1);
+      if (++n > kSpinLimit) {
+        atomicOr(err, 2);
+        break;
       }
     }
   }
-  if (P.partials) {
-    // workgroup max of the keys -> one partial per workgroup
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const uint64_t other = __shfl_xor(best, o);
-      best = other > best ? other : best;
-    }
-    __syncthreads();
-    if (lane == 0) keys[wave] = best;
-    __syncthreads();
-    if (tid == 0) {
-      uint64_t k = keys[0];
-      for (int w = 1; w < kWaves; ++w) k = keys[w] > k ? keys[w] : k;
-      P.partials[blockIdx.x] = k;
+  __syncthreads();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+
+__global__ __launch_bounds__(kWG) void stream_kernel(StreamParams S) {
+  __shared__ __align__(16) int8_t xs[kKMax];
+  __shared__ int32_t xlo[kKMax / 32];
+  __shared__ int64_t red[2][kWaves][kTileRows];
+  __shared__ int64_t sm[kWaves];
+  __shared__ uint64_t keys[kWaves];
+
+  const int tid = threadIdx.x, lane = tid & 63, q = lane & 3;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rank = blockIdx.x, G = gridDim.x;
+
+  // the wavefront's pending item and its registers
+  int cs = -1, ctg = 0, cb = 0;
+  for (int s2 = 0; s2 < S.nsites && cs < 0; ++s2) {
+    const GemvParams &Q = S.sites[s2];
+    const int t0 = first_tile(Q, rank, G);
+    if (t0 < Q.total_tiles && wave < Q.nblk) {
+      cs = s2; ctg = t0; cb = wave;
     }
   }
+  BlockRegs cur;
+  if (cs >= 0)
+    load_block(cur, block_addr(S.sites[cs], ctg, cb), groups_in(S.sites[cs].NG, cb), lane);
+
+  uint64_t best = 0;
+  int it = 0;
+  for (int s = 0; s < S.nsites; ++s) {
+    const GemvParams &P = S.sites[s];
+    if (s > 0) site_wait(S.done + (s - 1), (uint32_t)G, S.err);
+    const int e_x = run_prologue(P, xs, sm);
+    __syncthreads();
+    build_corrections(xs, xlo, P.NG);
+    __syncthreads();
+    const int32_t *sig = P.tables + kSigmoidOff;
+    for (int tg = first_tile(P, rank, G); tg < P.total_tiles; tg += G, ++it) {
+      const GemvJob &J = P.job[job_of(P, tg)];
+      const int t = tg - J.tile0;
+      int64_t p = 0;
+      for (int b = wave; b < P.nblk; b += kWaves) {
+        int ns, ntg, nb;
+        next_item(S, s, tg, b, rank, wave, G, ns, ntg, nb);
+        BlockRegs nxt;
+        if (ns >= 0)
+          load_block(nxt, block_addr(S.sites[ns], ntg, nb), groups_in(S.sites[ns].NG, nb), lane);
+        p = dot_block(cur, groups_in(P.NG, b), b * kGroupsPerBlock, q, xs, xlo, p);
+        if (ns >= 0) cur = nxt;
+      }
+      tile_finish(J, t, p, it, wave, lane, e_x, sig, S.err, red, best);
+    }
+    site_arrive(S.done + s);
+  }
+  if (S.head_site >= 0) write_partial(best, S.partials, keys, wave, lane);
 }
 
 __global__ __launch_bounds__(kWG) void argmax_final_kernel(
@@ -667,6 +817,20 @@ hipError_t launch_alu(int op, const int32_t *y, const int16_t *b, int64_t n, int
   hipLaunchKernelGGL(alu_kernel, dim3(blocks_for(n, 256, 4096)), dim3(256), 0, s,
                      op, y, b, n, p0, tables, out);
   return hipGetLastError();
+}
+
+hipError_t launch_stream(const StreamParams &sp, int grid, hipStream_t s) {
+  void *args[] = {(void *)&sp};
+  return hipLaunchCooperativeKernel((const void *)stream_kernel, dim3(grid), dim3(kWG),
+                                    args, 0, s);
+}
+
+int stream_max_blocks_per_cu() {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, stream_kernel, kWG, 0) !=
+          hipSuccess || n < 1)
+    n = 1;
+  return n;
 }
 
 int gemv_max_blocks_per_cu() {

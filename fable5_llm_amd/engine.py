@@ -296,6 +296,9 @@ class Plan:
         self.nsites += 1
         self.nmats += 1
 
+    def set_mode(self, mode):
+        N.check(N.lib().w4a8_plan_set_mode(self.h, int(mode)), "plan_set_mode")
+
     def run(self):
         N.check(N.lib().w4a8_plan_run(self.h), "plan_run")
 

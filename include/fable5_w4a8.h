@@ -174,6 +174,10 @@ int w4a8_matmul_y32_async(w4a8_ctx *ctx, const w4a8_weights *w,
  *      s+1 starts after site s has completed.  All pointers are device
  *      pointers captured at add time. ------------------------------------ */
 #define W4A8_PLAN_GRAPH       0 /* one launch per site, replayed as a HIP graph */
+#define W4A8_PLAN_PERSISTENT  1 /* one cooperative launch for every site; the
+                                   site order is kept by per-site completion
+                                   counters, and each wavefront keeps its next
+                                   weight block in flight across the wait */
 int w4a8_plan_create(w4a8_ctx *ctx, w4a8_plan **out);
 int w4a8_plan_add_site(w4a8_plan *plan, int32_t nmat,
                        const w4a8_weights *const *w, const int32_t *epilogue,
@@ -189,7 +193,9 @@ int w4a8_plan_set_mode(w4a8_plan *plan, int32_t mode);
 /* enqueue one replay of the whole plan on the context stream */
 int w4a8_plan_run(w4a8_plan *plan);
 /* run every step once, each GEMV launch bracketed by dispatch-recorded
-   events; ms[i] = kernel time of step i (n = number of steps).  Synchronous. */
+   events; ms[i] = kernel time of step i (n = number of steps).  In
+   persistent mode ms[0] is the time of the single launch and the rest are
+   0.  Synchronous. */
 int w4a8_plan_profile(w4a8_plan *plan, int32_t n, float *ms);
 int w4a8_plan_destroy(w4a8_plan *plan);
 
