@@ -120,7 +120,7 @@ def main():
 
     prof = st.profile()          # per-launch GEMV kernel time, ms
     kern_ms = float(prof.sum())
-    nlaunch = int((prof > 0).sum())
+    nlaunch = 1 if args.mode == "persistent" else int(prof.size)
     achieved = st.bytes / (kern_ms * 1e-3) / 1e9
 
     line = {

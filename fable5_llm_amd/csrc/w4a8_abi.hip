@@ -785,7 +785,7 @@ static int plan_build_persistent(w4a8_plan *p) {
 }
 
 static int plan_launch_persistent(w4a8_plan *p, hipStream_t s, hipEvent_t e0,
-                                  hipEvent_t e1) {
+                                  hipEvent_t e1, uint64_t *trace = nullptr) {
   StreamParams sp{};
   sp.sites = p->d_sites;
   sp.nsites = (int32_t)p->steps.size();
@@ -793,6 +793,7 @@ static int plan_launch_persistent(w4a8_plan *p, hipStream_t s, hipEvent_t e0,
   sp.done = p->d_done;
   sp.err = p->ctx->d_err;
   sp.partials = p->d_pkeys;
+  sp.trace = trace;
   HIP_TRY(launch_fill_i32((int32_t *)p->d_done, 0, sp.nsites, s));
   if (e0) HIP_TRY(hipEventRecord(e0, s));
   HIP_TRY(launch_stream(sp, p->G, s));
@@ -926,23 +927,35 @@ int w4a8_plan_profile(w4a8_plan *p, int32_t n, float *ms) {
   w4a8_ctx *c = p->ctx;
   DeviceGuard g(c->device);
   if (p->mode == W4A8_PLAN_PERSISTENT) {
-    // one launch runs every step: ms[0] = its kernel time, the rest 0
+    // one launch runs every step: its per-site times come from the
+    // wall-clock stamps workgroup 0 takes as it starts each site, scaled so
+    // that they sum to the launch's event-measured time
     if (!p->d_sites) {
       int rc = plan_build_persistent(p);
       if (rc) return rc;
     }
+    uint64_t *d_trace = nullptr;
+    HIP_TRY(hipMalloc(&d_trace, sizeof(uint64_t) * (size_t)(n + 1)));
     hipEvent_t e0 = nullptr, e1 = nullptr;
-    HIP_TRY(hipEventCreate(&e0));
-    HIP_TRY(hipEventCreate(&e1));
-    int rc = plan_launch_persistent(p, c->stream, e0, e1);
+    int rc = W4A8_OK;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
+      rc = fail(W4A8_E_HIP, "hipEventCreate");
+    if (!rc) rc = plan_launch_persistent(p, c->stream, e0, e1, d_trace);
     if (!rc && hipStreamSynchronize(c->stream) != hipSuccess) rc = fail(W4A8_E_HIP, "sync");
+    std::vector<uint64_t> tr(n + 1);
+    float total = 0.f;
+    if (!rc && (hipEventElapsedTime(&total, e0, e1) != hipSuccess ||
+                hipMemcpy(tr.data(), d_trace, sizeof(uint64_t) * (n + 1),
+                          hipMemcpyDeviceToHost) != hipSuccess))
+      rc = fail(W4A8_E_HIP, "profile readback");
     if (!rc) {
-      for (int i = 0; i < n; ++i) ms[i] = 0.f;
-      if (hipEventElapsedTime(&ms[0], e0, e1) != hipSuccess)
-        rc = fail(W4A8_E_HIP, "hipEventElapsedTime");
+      const double span = (double)(tr[n] - tr[0]);
+      for (int i = 0; i < n; ++i)
+        ms[i] = span > 0 ? (float)(total * (double)(tr[i + 1] - tr[i]) / span) : 0.f;
     }
-    (void)hipEventDestroy(e0);
-    (void)hipEventDestroy(e1);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipFree(d_trace);
     return rc;
   }
   std::vector<hipEvent_t> ev(2 * p->steps.size(), nullptr);

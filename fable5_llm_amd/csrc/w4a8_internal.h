@@ -118,6 +118,8 @@ struct StreamParams {
   uint32_t *done;           // nsites counters, zero at launch
   int32_t *err;             // bit 1: a completion wait gave up
   uint64_t *partials;       // head: one key per workgroup
+  uint64_t *trace;          // optional: nsites + 1 wall-clock stamps taken by
+                            // workgroup 0 as it starts each site, and at its end
 };
 hipError_t launch_stream(const StreamParams &sp, int grid, hipStream_t s);
 int stream_max_blocks_per_cu();

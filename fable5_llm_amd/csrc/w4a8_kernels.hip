@@ -472,9 +472,9 @@ __device__ __forceinline__ void next_item(const StreamParams &S, int s, int tg, 
 }
 
 __device__ __forceinline__ void site_arrive(uint32_t *cnt) {
-  // every wavefront's output stores become visible device-wide before the
-  // workgroup's arrival is counted
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  // the barrier's workgroup-scope release completes every wavefront's
+  // stores to L2; thread 0's agent-scope release then writes L2 back before
+  // the workgroup is counted
   __syncthreads();
   if (threadIdx.x == 0)
     __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
@@ -484,16 +484,17 @@ __device__ __forceinline__ void site_wait(const uint32_t *cnt, uint32_t target,
                                           int32_t *err) {
   if (threadIdx.x == 0) {
     uint32_t n = 0;
-    while (__hip_atomic_load(cnt, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < target) {
-      __builtin_amdgcn_s_sleep(1);
+    // relaxed polls (no cache invalidation per poll), one acquire at the end
+    while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+      __builtin_amdgcn_s_sleep(2);
       if (++n > kSpinLimit) {
         atomicOr(err, 2);
         break;
       }
     }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 }
 
 __global__ __launch_bounds__(kWG) void stream_kernel(StreamParams S) {
@@ -525,6 +526,7 @@ __global__ __launch_bounds__(kWG) void stream_kernel(StreamParams S) {
   for (int s = 0; s < S.nsites; ++s) {
     const GemvParams &P = S.sites[s];
     if (s > 0) site_wait(S.done + (s - 1), (uint32_t)G, S.err);
+    if (S.trace && rank == 0 && tid == 0) S.trace[s] = wall_clock64();
     const int e_x = run_prologue(P, xs, sm);
     __syncthreads();
     build_corrections(xs, xlo, P.NG);
@@ -547,6 +549,7 @@ __global__ __launch_bounds__(kWG) void stream_kernel(StreamParams S) {
     }
     site_arrive(S.done + s);
   }
+  if (S.trace && rank == 0 && tid == 0) S.trace[S.nsites] = wall_clock64();
   if (S.head_site >= 0) write_partial(best, S.partials, keys, wave, lane);
 }
 

@@ -194,8 +194,9 @@ int w4a8_plan_set_mode(w4a8_plan *plan, int32_t mode);
 int w4a8_plan_run(w4a8_plan *plan);
 /* run every step once, each GEMV launch bracketed by dispatch-recorded
    events; ms[i] = kernel time of step i (n = number of steps).  In
-   persistent mode ms[0] is the time of the single launch and the rest are
-   0.  Synchronous. */
+   persistent mode the single launch's event-measured time is split over the
+   steps by wall-clock stamps taken as workgroup 0 starts each site.
+   Synchronous. */
 int w4a8_plan_profile(w4a8_plan *plan, int32_t n, float *ms);
 int w4a8_plan_destroy(w4a8_plan *plan);
 

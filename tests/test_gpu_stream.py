@@ -30,8 +30,6 @@ def test_full_stream_bit_exact(engine, mode):
         after = [o for outs in st.outs for o in outs]
         assert all(bool((a == b).all()) for a, b in zip(before, after))
         prof = st.profile()
-        assert prof.shape == (129,) and prof[0] > 0
-        if mode == N.PLAN_GRAPH:
-            assert np.all(prof > 0)
+        assert prof.shape == (129,) and np.all(prof > 0)
     finally:
         st.close()
