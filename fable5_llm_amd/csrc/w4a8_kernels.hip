@@ -75,36 +75,63 @@ __device__ void rsqrt_q(uint64_t v, int P, const int32_t *lut, int64_t *r_out,
 // ---------------------------------------------------------------------------
 // workgroup reductions (4 wavefronts of 64)
 // ---------------------------------------------------------------------------
+// Wavefront reductions on the DPP network: pairs, quads, half rows and
+// rows by quad_perm / mirror moves, then rows 0..3 through row_bcast15 and
+// row_bcast31; lane 63 ends with the total.  Lanes a row_mask leaves out
+// read the identity.
+#define W4A8_DPP(v, ident, ctrl, rowmask) \
+  __builtin_amdgcn_update_dpp((ident), (v), (ctrl), (rowmask), 0xF, false)
+
 __device__ __forceinline__ int32_t wave_max_i32(int32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o));
-  return v;
+  // v >= 0 (magnitudes), so 0 is the identity
+  v = max(v, W4A8_DPP(v, 0, 0xB1, 0xF));    // quad_perm [1,0,3,2]
+  v = max(v, W4A8_DPP(v, 0, 0x4E, 0xF));    // quad_perm [2,3,0,1]
+  v = max(v, W4A8_DPP(v, 0, 0x141, 0xF));   // row_half_mirror
+  v = max(v, W4A8_DPP(v, 0, 0x140, 0xF));   // row_mirror
+  v = max(v, W4A8_DPP(v, 0, 0x142, 0xA));   // row_bcast15 -> rows 1, 3
+  v = max(v, W4A8_DPP(v, 0, 0x143, 0xC));   // row_bcast31 -> rows 2, 3
+  return __builtin_amdgcn_readlane(v, 63);
 }
-__device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL,
+                                                            ROWMASK, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32),
+                                                            CTRL, ROWMASK, 0xF, false);
+  return ((uint64_t)hi << 32) | lo;
 }
+
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+  v += dpp_u64<0xB1, 0xF>(v);
+  v += dpp_u64<0x4E, 0xF>(v);
+  v += dpp_u64<0x141, 0xF>(v);
+  v += dpp_u64<0x140, 0xF>(v);
+  v += dpp_u64<0x142, 0xA>(v);
+  v += dpp_u64<0x143, 0xC>(v);
+  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+  const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
+  return ((uint64_t)hi << 32) | lo;
+}
+
 __device__ int32_t block_max_i32(int32_t v, int64_t *sm) {
   v = wave_max_i32(v);
-  const int w = threadIdx.x >> 6;
   __syncthreads();
-  if ((threadIdx.x & 63) == 0) sm[w] = v;
+  if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = v;
   __syncthreads();
   int32_t r = (int32_t)sm[0];
 #pragma unroll
   for (int i = 1; i < kWaves; ++i) r = max(r, (int32_t)sm[i]);
   return r;
 }
-__device__ int64_t block_sum_i64(int64_t v, int64_t *sm) {
-  v = wave_sum_i64(v);
-  const int w = threadIdx.x >> 6;
+__device__ uint64_t block_sum_u64(uint64_t v, int64_t *sm) {
+  v = wave_sum_u64(v);
   __syncthreads();
-  if ((threadIdx.x & 63) == 0) sm[w] = v;
+  if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = (int64_t)v;
   __syncthreads();
-  int64_t r = 0;
+  uint64_t r = 0;
 #pragma unroll
-  for (int i = 0; i < kWaves; ++i) r += sm[i];
+  for (int i = 0; i < kWaves; ++i) r += (uint64_t)sm[i];
   return r;
 }
 
@@ -125,31 +152,64 @@ __device__ __forceinline__ void piece_set(int4 &p, int j, int16_t v) {
   else       *w = (int32_t)(((uint32_t)*w & 0xFFFF0000u) | (uint32_t)(uint16_t)v);
 }
 
-// rshift_round of |v| * 2^-s with the sign of v restored (s uniform, >= 0)
+
+// The activation vector of one site, held in registers from the moment its
+// loads are issued (before any weight load, so it is not queued behind the
+// weight stream) until the prologue consumes it.
+constexpr int kNormPieces = 8192 / (kWG * 8);   // RMSNorm vectors are <= 8192
+
+struct XRegs {
+  int4 pc[kPieces];       // int16 x (or, for PRO_X8, 16 int8 per piece)
+  int4 wv[kNormPieces];   // int16 norm weights
+};
+
+__device__ __forceinline__ void prologue_load(const GemvParams &P, XRegs &X) {
+  const int tid = threadIdx.x;
+  const int K = P.K;
+  if (P.pro == PRO_X8) {
+    const int8_t *x = (const int8_t *)P.x;
+#pragma unroll
+    for (int c = 0; c < kPieces / 2; ++c) {
+      const int i = (c * kWG + tid) * 16;
+      if (i < K) X.pc[c] = *(const int4 *)(x + i);
+    }
+    return;
+  }
+  const int16_t *x16 = (const int16_t *)P.x;
+#pragma unroll
+  for (int c = 0; c < kPieces; ++c) {
+    const int base = c * kWG * 8 + tid * 8;
+    X.pc[c] = base < K ? *(const int4 *)(x16 + base) : make_int4(0, 0, 0, 0);
+  }
+  if (P.pro == PRO_RMSNORM_DYNQ8) {
+#pragma unroll
+    for (int c = 0; c < kNormPieces; ++c) {
+      const int base = c * kWG * 8 + tid * 8;
+      if (base < K) X.wv[c] = *(const int4 *)(P.norm_w + base);
+    }
+  }
+}
+
+// rshift_round of a magnitude (s uniform, >= 0)
 __device__ __forceinline__ uint64_t round_shift_mag(uint64_t mag, int s) {
   return s == 0 ? mag : ((mag + ((uint64_t)1 << (s - 1))) >> s);
 }
 
-__device__ int run_prologue(const GemvParams &P, int8_t *xs, int64_t *sm) {
+__device__ int prologue_compute(const GemvParams &P, XRegs &X, int8_t *xs, int64_t *sm) {
   const int tid = threadIdx.x;
   const int K = P.K;
   const bool writer = blockIdx.x == 0;
   if (P.pro == PRO_X8) {
-    const int8_t *x = (const int8_t *)P.x;
-    for (int i = tid * 16; i < K; i += kWG * 16) {
-      const int4 v = *(const int4 *)(x + i);
-      *(int4 *)(xs + i) = v;
-      if (writer && P.x8_out) *(int4 *)(P.x8_out + i) = v;
+#pragma unroll
+    for (int c = 0; c < kPieces / 2; ++c) {
+      const int i = (c * kWG + tid) * 16;
+      if (i < K) {
+        *(int4 *)(xs + i) = X.pc[c];
+        if (writer && P.x8_out) *(int4 *)(P.x8_out + i) = X.pc[c];
+      }
     }
     if (writer && P.e_x_out && tid == 0) *P.e_x_out = P.e_x_given;
     return P.e_x_given;
-  }
-  const int16_t *x16 = (const int16_t *)P.x;
-  int4 pc[kPieces];
-#pragma unroll
-  for (int c = 0; c < kPieces; ++c) {
-    const int base = c * kWG * 8 + tid * 8;
-    pc[c] = base < K ? *(const int4 *)(x16 + base) : make_int4(0, 0, 0, 0);
   }
   if (P.pro == PRO_RMSNORM_DYNQ8) {
     // layer_fixed.py:1262-1278, in sign-magnitude form: rshift_round rounds
@@ -157,13 +217,13 @@ __device__ int run_prologue(const GemvParams &P, int8_t *xs, int64_t *sm) {
     // sign is restored afterwards
     uint64_t ss = 0;
 #pragma unroll
-    for (int c = 0; c < kPieces; ++c)
+    for (int c = 0; c < kNormPieces; ++c)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int32_t v = piece_get(pc[c], j);
+        const int32_t v = piece_get(X.pc[c], j);
         ss += (uint64_t)(uint32_t)(v * v);
       }
-    ss = (uint64_t)block_sum_i64((int64_t)ss, sm);
+    ss = block_sum_u64(ss, sm);
     if (ss == 0) ss = 1;
     const int nbits = 31 - __clz(K);
     int64_t r;
@@ -172,27 +232,25 @@ __device__ int run_prologue(const GemvParams &P, int8_t *xs, int64_t *sm) {
     const int s1 = 30 - e;
     const int32_t one = P.one_plus ? (1 << 14) : 0;
 #pragma unroll
-    for (int c = 0; c < kPieces; ++c) {
+    for (int c = 0; c < kNormPieces; ++c) {
       const int base = c * kWG * 8 + tid * 8;
       if (base < K) {
-        const int4 wv = *(const int4 *)(P.norm_w + base);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const int32_t xv = piece_get(pc[c], j);
+          const int32_t xv = piece_get(X.pc[c], j);
           const uint64_t mag = (uint64_t)(uint32_t)abs(xv) * (uint64_t)r;
           uint64_t ym = s1 >= 0 ? round_shift_mag(mag, s1) : (mag << (-s1));
           // clip to [-2^32, 2^32 - 1]
           const uint64_t cap = xv < 0 ? ((uint64_t)1 << 32) : (((uint64_t)1 << 32) - 1);
           ym = ym > cap ? cap : ym;
-          const int32_t sc = (int32_t)piece_get(wv, j) + one;
-          const uint64_t m2 = ym * (uint64_t)(uint32_t)abs(sc);
-          const uint64_t q = round_shift_mag(m2, 14);
+          const int32_t sc = (int32_t)piece_get(X.wv[c], j) + one;
+          const uint64_t q = round_shift_mag(ym * (uint64_t)(uint32_t)abs(sc), 14);
           const bool neg = (xv < 0) != (sc < 0);
           const int32_t o = neg ? (q > 32768u ? -32768 : -(int32_t)q)
                                 : (q > 32767u ? 32767 : (int32_t)q);
-          piece_set(pc[c], j, (int16_t)o);
+          piece_set(X.pc[c], j, (int16_t)o);
         }
-        if (writer && P.xn_out) *(int4 *)(P.xn_out + base) = pc[c];
+        if (writer && P.xn_out) *(int4 *)(P.xn_out + base) = X.pc[c];
       }
     }
   }
@@ -200,7 +258,7 @@ __device__ int run_prologue(const GemvParams &P, int8_t *xs, int64_t *sm) {
 #pragma unroll
   for (int c = 0; c < kPieces; ++c)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) mx = max(mx, abs((int32_t)piece_get(pc[c], j)));
+    for (int j = 0; j < 8; ++j) mx = max(mx, abs((int32_t)piece_get(X.pc[c], j)));
   mx = block_max_i32(mx, sm);
   int e = 0;
   while (((mx + ((1 << e) >> 1)) >> e) > 127) ++e;
@@ -212,7 +270,7 @@ __device__ int run_prologue(const GemvParams &P, int8_t *xs, int64_t *sm) {
       uint32_t lo = 0, hi = 0;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int32_t v = piece_get(pc[c], j);
+        const int32_t v = piece_get(X.pc[c], j);
         const int32_t qm = min((abs(v) + half) >> e, 127);
         const uint32_t b = (uint32_t)(uint8_t)(int8_t)(v < 0 ? -qm : qm);
         if (j < 4) lo |= b << (8 * j);
@@ -326,8 +384,9 @@ __device__ __forceinline__ void tile_finish(const GemvJob &J, int t, int64_t p, 
                                             const int32_t *sig, int32_t *err,
                                             int64_t (*red)[kWaves][kTileRows],
                                             uint64_t &best) {
-  p += __shfl_xor(p, 1);
-  p += __shfl_xor(p, 2);
+  // sum the 4 k-quarter lanes of each row (lanes 4r..4r+3: one DPP quad)
+  p = (int64_t)((uint64_t)p + dpp_u64<0xB1, 0xF>((uint64_t)p));
+  p = (int64_t)((uint64_t)p + dpp_u64<0x4E, 0xF>((uint64_t)p));
   const int par = it & 1;
   if ((lane & 3) == 0) red[par][wave][lane >> 2] = p;
   __syncthreads();
@@ -394,12 +453,15 @@ __global__ __launch_bounds__(kWG) void gemv_kernel(GemvParams P) {
   // wave index as a scalar so the block loop below branches on SGPRs
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int NG = P.NG, nblk = P.nblk;
-  // The weights do not depend on x: put this wave's first block in flight
-  // before the prologue so the two memory latencies overlap.
+  // The activation loads go out first; the weights do not depend on x, so
+  // this wave's first block is put in flight right behind them and both
+  // memory latencies overlap with the prologue.
+  XRegs X;
+  prologue_load(P, X);
   BlockRegs cur;
   if ((int)blockIdx.x < P.total_tiles && wave < nblk)
     load_block(cur, block_addr(P, blockIdx.x, wave), groups_in(NG, wave), lane);
-  const int e_x = run_prologue(P, xs, sm);
+  const int e_x = prologue_compute(P, X, xs, sm);
   __syncthreads();
   build_corrections(xs, xlo, NG);
   __syncthreads();
@@ -527,7 +589,9 @@ __global__ __launch_bounds__(kWG) void stream_kernel(StreamParams S) {
     const GemvParams &P = S.sites[s];
     if (s > 0) site_wait(S.done + (s - 1), (uint32_t)G, S.err);
     if (S.trace && rank == 0 && tid == 0) S.trace[s] = wall_clock64();
-    const int e_x = run_prologue(P, xs, sm);
+    XRegs X;
+    prologue_load(P, X);
+    const int e_x = prologue_compute(P, X, xs, sm);
     __syncthreads();
     build_corrections(xs, xlo, P.NG);
     __syncthreads();
@@ -577,7 +641,9 @@ __global__ __launch_bounds__(kWG) void argmax_final_kernel(
 __global__ __launch_bounds__(kWG) void vec_prologue_kernel(GemvParams P) {
   __shared__ __align__(16) int8_t xs[kKMax];
   __shared__ int64_t sm[kWaves];
-  run_prologue(P, xs, sm);
+  XRegs X;
+  prologue_load(P, X);
+  prologue_compute(P, X, xs, sm);
 }
 
 // ---------------------------------------------------------------------------
