@@ -163,29 +163,43 @@ struct XRegs {
   int4 wv[kNormPieces];   // int16 norm weights
 };
 
+// Pieces c < npieces(K) hold data; the count is uniform, so the unrolled
+// piece loops below branch on scalars and never run masked-off pieces.
+__device__ __forceinline__ int npieces(int K, int per_piece) {
+  return (K + kWG * per_piece - 1) / (kWG * per_piece);
+}
+
 __device__ __forceinline__ void prologue_load(const GemvParams &P, XRegs &X) {
   const int tid = threadIdx.x;
   const int K = P.K;
   if (P.pro == PRO_X8) {
     const int8_t *x = (const int8_t *)P.x;
+    const int np = npieces(K, 16);
 #pragma unroll
     for (int c = 0; c < kPieces / 2; ++c) {
-      const int i = (c * kWG + tid) * 16;
-      if (i < K) X.pc[c] = *(const int4 *)(x + i);
+      if (c < np) {
+        const int i = (c * kWG + tid) * 16;
+        if (i < K) X.pc[c] = *(const int4 *)(x + i);
+      }
     }
     return;
   }
   const int16_t *x16 = (const int16_t *)P.x;
+  const int np = npieces(K, 8);
 #pragma unroll
   for (int c = 0; c < kPieces; ++c) {
-    const int base = c * kWG * 8 + tid * 8;
-    X.pc[c] = base < K ? *(const int4 *)(x16 + base) : make_int4(0, 0, 0, 0);
+    if (c < np) {
+      const int base = c * kWG * 8 + tid * 8;
+      X.pc[c] = base < K ? *(const int4 *)(x16 + base) : make_int4(0, 0, 0, 0);
+    }
   }
   if (P.pro == PRO_RMSNORM_DYNQ8) {
 #pragma unroll
     for (int c = 0; c < kNormPieces; ++c) {
-      const int base = c * kWG * 8 + tid * 8;
-      if (base < K) X.wv[c] = *(const int4 *)(P.norm_w + base);
+      if (c < np) {
+        const int base = c * kWG * 8 + tid * 8;
+        X.wv[c] = base < K ? *(const int4 *)(P.norm_w + base) : make_int4(0, 0, 0, 0);
+      }
     }
   }
 }
@@ -200,10 +214,11 @@ __device__ int prologue_compute(const GemvParams &P, XRegs &X, int8_t *xs, int64
   const int K = P.K;
   const bool writer = blockIdx.x == 0;
   if (P.pro == PRO_X8) {
+    const int np8 = npieces(K, 16);
 #pragma unroll
     for (int c = 0; c < kPieces / 2; ++c) {
       const int i = (c * kWG + tid) * 16;
-      if (i < K) {
+      if (c < np8 && i < K) {
         *(int4 *)(xs + i) = X.pc[c];
         if (writer && P.x8_out) *(int4 *)(P.x8_out + i) = X.pc[c];
       }
@@ -211,18 +226,22 @@ __device__ int prologue_compute(const GemvParams &P, XRegs &X, int8_t *xs, int64
     if (writer && P.e_x_out && tid == 0) *P.e_x_out = P.e_x_given;
     return P.e_x_given;
   }
+  const int np = npieces(K, 8);
   if (P.pro == PRO_RMSNORM_DYNQ8) {
     // layer_fixed.py:1262-1278, in sign-magnitude form: rshift_round rounds
     // the magnitude, so |x * r| and |y * sc| carry the rounding and the
     // sign is restored afterwards
     uint64_t ss = 0;
 #pragma unroll
-    for (int c = 0; c < kNormPieces; ++c)
+    for (int c = 0; c < kNormPieces; ++c) {
+      if (c < np) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int32_t v = piece_get(X.pc[c], j);
-        ss += (uint64_t)(uint32_t)(v * v);
+        for (int j = 0; j < 8; j += 2) {
+          const int32_t a = piece_get(X.pc[c], j), b = piece_get(X.pc[c], j + 1);
+          ss += (uint64_t)((uint32_t)(a * a) + (uint32_t)(b * b));
+        }
       }
+    }
     ss = block_sum_u64(ss, sm);
     if (ss == 0) ss = 1;
     const int nbits = 31 - __clz(K);
@@ -234,7 +253,7 @@ __device__ int prologue_compute(const GemvParams &P, XRegs &X, int8_t *xs, int64
 #pragma unroll
     for (int c = 0; c < kNormPieces; ++c) {
       const int base = c * kWG * 8 + tid * 8;
-      if (base < K) {
+      if (c < np && base < K) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int32_t xv = piece_get(X.pc[c], j);
@@ -257,8 +276,9 @@ __device__ int prologue_compute(const GemvParams &P, XRegs &X, int8_t *xs, int64
   int32_t mx = 0;
 #pragma unroll
   for (int c = 0; c < kPieces; ++c)
+    if (c < np)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) mx = max(mx, abs((int32_t)piece_get(X.pc[c], j)));
+      for (int j = 0; j < 8; ++j) mx = max(mx, abs((int32_t)piece_get(X.pc[c], j)));
   mx = block_max_i32(mx, sm);
   int e = 0;
   while (((mx + ((1 << e) >> 1)) >> e) > 127) ++e;
@@ -266,7 +286,7 @@ __device__ int prologue_compute(const GemvParams &P, XRegs &X, int8_t *xs, int64
 #pragma unroll
   for (int c = 0; c < kPieces; ++c) {
     const int base = c * kWG * 8 + tid * 8;
-    if (base < K) {
+    if (c < np && base < K) {
       uint32_t lo = 0, hi = 0;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -344,8 +364,10 @@ __device__ __forceinline__ int64_t dot_block(const BlockRegs &R, int ng, int g0,
 }
 
 __device__ __forceinline__ int job_of(const GemvParams &P, int tg) {
+  // unrolled over the fixed job table so every tile0 is loaded at once
   int j = 0;
-  while (j + 1 < P.njobs && tg >= P.job[j + 1].tile0) ++j;
+#pragma unroll
+  for (int k = 1; k < kMaxJobs; ++k) j += (k < P.njobs && tg >= P.job[k].tile0) ? 1 : 0;
   return j;
 }
 
