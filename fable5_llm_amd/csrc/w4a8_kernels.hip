@@ -250,26 +250,36 @@ __device__ int prologue_compute(const GemvParams &P, XRegs &X, int8_t *xs, int64
     rsqrt_q(ss, 2 * P.in_f + nbits, P.tables + kRsqrtOff, &r, &e);
     const int s1 = 30 - e;
     const int32_t one = P.one_plus ? (1 << 14) : 0;
+    // |x| * r < 2^46.  Every element step below is branch-free: the right
+    // shift (s1 >= 0, capped at 63) and the left shift (s1 < 0) are both
+    // formed and the uniform sign of s1 selects one
+    const int rs = s1 < 0 ? 0 : (s1 > 63 ? 63 : s1);
+    const int ls = s1 < 0 ? (-s1 > 63 ? 63 : -s1) : 0;
+    const uint64_t half1 = rs > 0 ? ((uint64_t)1 << (rs - 1)) : 0;
+    const bool right = s1 >= 0;
+    // pieces past K hold zeros (loaded as such), which normalise to zero:
+    // only the stores need the per-thread bound
 #pragma unroll
     for (int c = 0; c < kNormPieces; ++c) {
       const int base = c * kWG * 8 + tid * 8;
-      if (c < np && base < K) {
+      if (c < np) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int32_t xv = piece_get(X.pc[c], j);
-          const uint64_t mag = (uint64_t)(uint32_t)abs(xv) * (uint64_t)r;
-          uint64_t ym = s1 >= 0 ? round_shift_mag(mag, s1) : (mag << (-s1));
-          // clip to [-2^32, 2^32 - 1]
-          const uint64_t cap = xv < 0 ? ((uint64_t)1 << 32) : (((uint64_t)1 << 32) - 1);
-          ym = ym > cap ? cap : ym;
           const int32_t sc = (int32_t)piece_get(X.wv[c], j) + one;
-          const uint64_t q = round_shift_mag(ym * (uint64_t)(uint32_t)abs(sc), 14);
+          const uint64_t mag = (uint64_t)(uint32_t)abs(xv) * (uint64_t)r;
+          uint64_t ym = right ? ((mag + half1) >> rs) : (mag << ls);
+          // clip to [-2^32, 2^32 - 1]
+          const uint64_t cap = (uint64_t)0xFFFFFFFFu + (uint64_t)(xv < 0);
+          ym = ym < cap ? ym : cap;
+          // rshift_round(y * sc, 14) on the magnitude, then clip16
+          const uint64_t q = (ym * (uint64_t)(uint32_t)abs(sc) + 8192u) >> 14;
           const bool neg = (xv < 0) != (sc < 0);
-          const int32_t o = neg ? (q > 32768u ? -32768 : -(int32_t)q)
-                                : (q > 32767u ? 32767 : (int32_t)q);
-          piece_set(X.pc[c], j, (int16_t)o);
+          const int32_t q32 = q > 65535u ? 65535 : (int32_t)q;
+          const int32_t qm = min(q32, 32767 + (int32_t)neg);
+          piece_set(X.pc[c], j, (int16_t)(neg ? -qm : qm));
         }
-        if (writer && P.xn_out) *(int4 *)(P.xn_out + base) = X.pc[c];
+        if (writer && P.xn_out && base < K) *(int4 *)(P.xn_out + base) = X.pc[c];
       }
     }
   }
@@ -286,7 +296,7 @@ __device__ int prologue_compute(const GemvParams &P, XRegs &X, int8_t *xs, int64
 #pragma unroll
   for (int c = 0; c < kPieces; ++c) {
     const int base = c * kWG * 8 + tid * 8;
-    if (c < np && base < K) {
+    if (c < np) {
       uint32_t lo = 0, hi = 0;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -296,8 +306,10 @@ __device__ int prologue_compute(const GemvParams &P, XRegs &X, int8_t *xs, int64
         if (j < 4) lo |= b << (8 * j);
         else       hi |= b << (8 * (j - 4));
       }
-      *(uint2 *)(xs + base) = make_uint2(lo, hi);
-      if (writer && P.x8_out) *(uint2 *)(P.x8_out + base) = make_uint2(lo, hi);
+      if (base < K) {
+        *(uint2 *)(xs + base) = make_uint2(lo, hi);
+        if (writer && P.x8_out) *(uint2 *)(P.x8_out + base) = make_uint2(lo, hi);
+      }
     }
   }
   if (writer && P.e_x_out && tid == 0) *P.e_x_out = e;
