@@ -770,14 +770,17 @@ static int plan_build_persistent(w4a8_plan *p) {
     }
   p->G = c->num_cu * stream_max_blocks_per_cu();
   std::vector<GemvParams> sites(n);
+  // tile t of site s goes to team (off_s + t) mod V, V = G * teams, so the
+  // teams that finish a site early start the next one first
+  const int64_t V = (int64_t)p->G * kStreamTeams;
   int64_t off = 0;
   for (int i = 0; i < n; ++i) {
     sites[i] = p->steps[i].P;
-    sites[i].tile_rot = (int32_t)((p->G - off % p->G) % p->G);
+    sites[i].tile_rot = (int32_t)((V - off % V) % V);
     off += sites[i].total_tiles;
   }
   HIP_TRY(hipMalloc(&p->d_sites, sizeof(GemvParams) * (size_t)n));
-  HIP_TRY(hipMalloc(&p->d_done, sizeof(uint32_t) * (size_t)n));
+  HIP_TRY(hipMalloc(&p->d_done, sizeof(uint32_t) * stream_counter_words(n)));
   HIP_TRY(hipMalloc(&p->d_pkeys, sizeof(uint64_t) * (size_t)p->G));
   HIP_TRY(hipMemcpy(p->d_sites, sites.data(), sizeof(GemvParams) * (size_t)n,
                     hipMemcpyHostToDevice));
@@ -794,7 +797,7 @@ static int plan_launch_persistent(w4a8_plan *p, hipStream_t s, hipEvent_t e0,
   sp.err = p->ctx->d_err;
   sp.partials = p->d_pkeys;
   sp.trace = trace;
-  HIP_TRY(launch_fill_i32((int32_t *)p->d_done, 0, sp.nsites, s));
+  HIP_TRY(launch_fill_i32((int32_t *)p->d_done, 0, (int64_t)stream_counter_words(sp.nsites), s));
   if (e0) HIP_TRY(hipEventRecord(e0, s));
   HIP_TRY(launch_stream(sp, p->G, s));
   if (e1) HIP_TRY(hipEventRecord(e1, s));

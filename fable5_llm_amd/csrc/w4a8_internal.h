@@ -110,12 +110,15 @@ hipError_t launch_gemv(const GemvParams &p, int grid, hipStream_t s);
 hipError_t launch_gemv_timed(const GemvParams &p, int grid, hipStream_t s,
                              hipEvent_t start, hipEvent_t stop);
 // Persistent decode-step kernel: every site of a plan in one cooperative
+// launch of one workgroup per CU with kStreamTeams teams of 4 wavefronts;
+constexpr int kStreamTeams = 2;
+//
 // launch, site order kept by per-site completion counters.
 struct StreamParams {
   const GemvParams *sites;  // device array, nsites entries
   int32_t nsites;
   int32_t head_site;        // index of the LM-head site, or -1
-  uint32_t *done;           // nsites counters, zero at launch
+  uint32_t *done;           // stream_counter_words(nsites) words, zero at launch
   int32_t *err;             // bit 1: a completion wait gave up
   uint64_t *partials;       // head: one key per workgroup
   uint64_t *trace;          // optional: nsites + 1 wall-clock stamps taken by
@@ -123,6 +126,8 @@ struct StreamParams {
 };
 hipError_t launch_stream(const StreamParams &sp, int grid, hipStream_t s);
 int stream_max_blocks_per_cu();
+// uint32 words of completion counters a plan of nsites needs
+size_t stream_counter_words(int nsites);
 
 hipError_t launch_argmax_final(const uint64_t *partials, int n,
                                int32_t *result, hipStream_t s);

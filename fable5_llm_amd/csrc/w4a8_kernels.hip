@@ -528,127 +528,370 @@ __global__ __launch_bounds__(kWG) void gemv_kernel(GemvParams P) {
 // ---------------------------------------------------------------------------
 // persistent decode-step kernel
 //
-// One cooperative launch runs every site of a plan.  Workgroup r processes
-// tiles (r + tile_rot) mod G, + G, ... of each site; the 4 wavefronts split
-// a tile's scale blocks as in gemv_kernel.  Site s+1 starts (prologue and
-// compute) only after all G workgroups have finished site s, which they
-// signal on done[s]: the dependency a decode step has between consecutive
-// DYNQ8 sites.  Weights do not depend on any activation, so each wavefront
-// keeps its next (site, tile, block) in flight across that wait.
+// One cooperative launch runs every site of a plan, one 512-thread
+// workgroup per CU: two teams of four wavefronts.  Team v (of V = 2G) takes
+// tiles (v + tile_rot) mod V, + V, ... of each site; its four wavefronts
+// split a tile's scale blocks.  Site s+1 starts only after all G workgroups
+// have finished site s -- the dependency a decode step has between
+// consecutive DYNQ8 sites -- counted per XCD, then globally.  The data that
+// crosses that dependency travels with agent-coherent accesses: outputs are
+// stored and activation vectors loaded with device-scope atomics, so the
+// ordering needs no cache-wide writeback or invalidation.  Weights never
+// depend on an activation, so each wavefront keeps its next weight block in
+// flight across the wait.
 // ---------------------------------------------------------------------------
-constexpr uint32_t kSpinLimit = 1u << 21;   // ~0.1 s: a wait that never ends
-                                            // flags err bit 1 and moves on
+constexpr int kSWG = 512;                 // threads per stream workgroup
+constexpr int kSWaves = kSWG / 64;        // 8
+constexpr int kTeams = kStreamTeams;      // 2 teams of 4 wavefronts
+static_assert(kSWaves == 4 * kTeams, "a team is 4 wavefronts");
+constexpr int kSPieces = kKMax / (kSWG * 8);       // 3 pieces of 8 x per thread
+constexpr int kSNormPieces = 8192 / (kSWG * 8);    // 2
+constexpr uint32_t kSpinLimit = 1u << 18;          // a wait that never ends
+                                                   // flags err bit 1, moves on
+constexpr int kXcds = 8;
+constexpr int kCounterStride = 64;                 // uint32 words: 256 B apart
 
-__device__ __forceinline__ int first_tile(const GemvParams &P, int rank, int G) {
-  return (rank + P.tile_rot) % G;
+struct SRegs {
+  int4 pc[kSPieces];
+  int4 wv[kSNormPieces];
+};
+
+__device__ __forceinline__ int4 load_coherent16(const void *p) {
+  const uint64_t *q = (const uint64_t *)p;
+  const uint64_t a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_int4((int)(uint32_t)a, (int)(uint32_t)(a >> 32), (int)(uint32_t)b,
+                   (int)(uint32_t)(b >> 32));
 }
 
-// next (site, tile, block) of this wavefront after (s, tg, b); site -1 = none
-__device__ __forceinline__ void next_item(const StreamParams &S, int s, int tg, int b,
-                                          int rank, int wave, int G, int &ns, int &ntg,
-                                          int &nb) {
+template <typename T>
+__device__ __forceinline__ void store_coherent(T *p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ int32_t sblock_max(int32_t v, int64_t *sm) {
+  v = wave_max_i32(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = v;
+  __syncthreads();
+  int32_t r = (int32_t)sm[0];
+#pragma unroll
+  for (int i = 1; i < kSWaves; ++i) r = max(r, (int32_t)sm[i]);
+  return r;
+}
+__device__ __forceinline__ uint64_t sblock_sum(uint64_t v, int64_t *sm) {
+  v = wave_sum_u64(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = (int64_t)v;
+  __syncthreads();
+  uint64_t r = 0;
+#pragma unroll
+  for (int i = 0; i < kSWaves; ++i) r += (uint64_t)sm[i];
+  return r;
+}
+
+// the site's activation vector -> x8 in LDS (512 threads, coherent loads)
+__device__ int stream_prologue(const GemvParams &P, int8_t *xs, int64_t *sm) {
+  const int tid = threadIdx.x;
+  const int K = P.K;
+  const bool writer = blockIdx.x == 0;
+  SRegs X;
+  if (P.pro == PRO_X8) {
+    for (int i = tid * 16; i < K; i += kSWG * 16) {
+      const int4 v = load_coherent16((const int8_t *)P.x + i);
+      *(int4 *)(xs + i) = v;
+      if (writer && P.x8_out) *(int4 *)(P.x8_out + i) = v;
+    }
+    if (writer && P.e_x_out && tid == 0) *P.e_x_out = P.e_x_given;
+    return P.e_x_given;
+  }
+  const int np = (K + kSWG * 8 - 1) / (kSWG * 8);
+  const int16_t *x16 = (const int16_t *)P.x;
+#pragma unroll
+  for (int c = 0; c < kSPieces; ++c) {
+    if (c < np) {
+      const int base = c * kSWG * 8 + tid * 8;
+      X.pc[c] = base < K ? load_coherent16(x16 + base) : make_int4(0, 0, 0, 0);
+    }
+  }
+  if (P.pro == PRO_RMSNORM_DYNQ8) {
+#pragma unroll
+    for (int c = 0; c < kSNormPieces; ++c) {
+      if (c < np) {
+        const int base = c * kSWG * 8 + tid * 8;
+        X.wv[c] = base < K ? *(const int4 *)(P.norm_w + base) : make_int4(0, 0, 0, 0);
+      }
+    }
+    uint64_t ss = 0;
+#pragma unroll
+    for (int c = 0; c < kSNormPieces; ++c)
+      if (c < np)
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+          const int32_t a = piece_get(X.pc[c], j), b2 = piece_get(X.pc[c], j + 1);
+          ss += (uint64_t)((uint32_t)(a * a) + (uint32_t)(b2 * b2));
+        }
+    ss = sblock_sum(ss, sm);
+    if (ss == 0) ss = 1;
+    int64_t r;
+    int e;
+    rsqrt_q(ss, 2 * P.in_f + (31 - __clz(K)), P.tables + kRsqrtOff, &r, &e);
+    const int s1 = 30 - e;
+    const int32_t one = P.one_plus ? (1 << 14) : 0;
+    const int rs = s1 < 0 ? 0 : (s1 > 63 ? 63 : s1);
+    const int ls = s1 < 0 ? (-s1 > 63 ? 63 : -s1) : 0;
+    const uint64_t half1 = rs > 0 ? ((uint64_t)1 << (rs - 1)) : 0;
+    const bool right = s1 >= 0;
+#pragma unroll
+    for (int c = 0; c < kSNormPieces; ++c) {
+      const int base = c * kSWG * 8 + tid * 8;
+      if (c < np) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int32_t xv = piece_get(X.pc[c], j);
+          const int32_t sc = (int32_t)piece_get(X.wv[c], j) + one;
+          const uint64_t mag = (uint64_t)(uint32_t)abs(xv) * (uint64_t)r;
+          uint64_t ym = right ? ((mag + half1) >> rs) : (mag << ls);
+          const uint64_t cap = (uint64_t)0xFFFFFFFFu + (uint64_t)(xv < 0);
+          ym = ym < cap ? ym : cap;
+          const uint64_t q = (ym * (uint64_t)(uint32_t)abs(sc) + 8192u) >> 14;
+          const bool neg = (xv < 0) != (sc < 0);
+          const int32_t q32 = q > 65535u ? 65535 : (int32_t)q;
+          const int32_t qm = min(q32, 32767 + (int32_t)neg);
+          piece_set(X.pc[c], j, (int16_t)(neg ? -qm : qm));
+        }
+        if (writer && P.xn_out && base < K) *(int4 *)(P.xn_out + base) = X.pc[c];
+      }
+    }
+  }
+  int32_t mx = 0;
+#pragma unroll
+  for (int c = 0; c < kSPieces; ++c)
+    if (c < np)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mx = max(mx, abs((int32_t)piece_get(X.pc[c], j)));
+  mx = sblock_max(mx, sm);
+  int e = 0;
+  while (((mx + ((1 << e) >> 1)) >> e) > 127) ++e;
+  const int32_t half = (1 << e) >> 1;
+#pragma unroll
+  for (int c = 0; c < kSPieces; ++c) {
+    const int base = c * kSWG * 8 + tid * 8;
+    if (c < np) {
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int32_t v = piece_get(X.pc[c], j);
+        const int32_t qm = min((abs(v) + half) >> e, 127);
+        const uint32_t b8 = (uint32_t)(uint8_t)(int8_t)(v < 0 ? -qm : qm);
+        if (j < 4) lo |= b8 << (8 * j);
+        else       hi |= b8 << (8 * (j - 4));
+      }
+      if (base < K) {
+        *(uint2 *)(xs + base) = make_uint2(lo, hi);
+        if (writer && P.x8_out) *(uint2 *)(P.x8_out + base) = make_uint2(lo, hi);
+      }
+    }
+  }
+  if (writer && P.e_x_out && tid == 0) *P.e_x_out = e;
+  return e;
+}
+
+__device__ __forceinline__ void sbuild_corrections(const int8_t *xs, int32_t *xlo, int NG) {
+  for (int c = threadIdx.x; c < NG * 4; c += kSWG) {
+    const int *xw = (const int *)(xs + 32 * c);
+    int t = 0;
+    t = __builtin_amdgcn_sdot4(xw[0], 0x01010101, t, false);
+    t = __builtin_amdgcn_sdot4(xw[2], 0x01010101, t, false);
+    t = __builtin_amdgcn_sdot4(xw[4], 0x01010101, t, false);
+    t = __builtin_amdgcn_sdot4(xw[6], 0x01010101, t, false);
+    xlo[c] = -8 * t;
+  }
+}
+
+// first tile of team v (of V) in a site
+__device__ __forceinline__ int team_first(const GemvParams &P, int v, int V) {
+  return (v + P.tile_rot) % V;
+}
+
+// next (site, tile, block) of wavefront wt of team v after (s, t, b)
+__device__ __forceinline__ void snext(const StreamParams &S, int s, int t, int b, int v,
+                                      int V, int wt, int &ns, int &nt, int &nb) {
   const GemvParams &P = S.sites[s];
-  if (b + kWaves < P.nblk) {
-    ns = s; ntg = tg; nb = b + kWaves;
+  if (b + 4 < P.nblk) {
+    ns = s; nt = t; nb = b + 4;
     return;
   }
-  if (tg + G < P.total_tiles) {
-    ns = s; ntg = tg + G; nb = wave;
+  if (t + V < P.total_tiles) {
+    ns = s; nt = t + V; nb = wt;
     return;
   }
   for (int s2 = s + 1; s2 < S.nsites; ++s2) {
     const GemvParams &Q = S.sites[s2];
-    const int t0 = first_tile(Q, rank, G);
-    if (t0 < Q.total_tiles && wave < Q.nblk) {
-      ns = s2; ntg = t0; nb = wave;
+    const int t0 = team_first(Q, v, V);
+    if (t0 < Q.total_tiles && wt < Q.nblk) {
+      ns = s2; nt = t0; nb = wt;
       return;
     }
   }
-  ns = -1; ntg = 0; nb = 0;
+  ns = -1; nt = 0; nb = 0;
 }
 
+// this workgroup's stores are complete and counted: per XCD, then, by the
+// XCD's last workgroup, globally
 __device__ __forceinline__ void site_arrive(uint32_t *cnt) {
-  // the barrier's workgroup-scope release completes every wavefront's
-  // stores to L2; thread 0's agent-scope release then writes L2 back before
-  // the workgroup is counted
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0)
-    __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) {
+    const int xcd = blockIdx.x % kXcds;
+    const uint32_t per = (gridDim.x - xcd + kXcds - 1) / kXcds;
+    const uint32_t old = __hip_atomic_fetch_add(cnt + kCounterStride * (1 + xcd), 1u,
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old + 1 == per)
+      __hip_atomic_fetch_add(cnt, per, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 __device__ __forceinline__ void site_wait(const uint32_t *cnt, uint32_t target,
                                           int32_t *err) {
   if (threadIdx.x == 0) {
     uint32_t n = 0;
-    // relaxed polls (no cache invalidation per poll), one acquire at the end
     while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-      __builtin_amdgcn_s_sleep(2);
+      __builtin_amdgcn_s_sleep(1);
       if (++n > kSpinLimit) {
         atomicOr(err, 2);
         break;
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
 }
 
-__global__ __launch_bounds__(kWG) void stream_kernel(StreamParams S) {
+// as tile_finish, for a team of the stream workgroup; outputs are stored
+// coherently (they cross the site dependency)
+__device__ __forceinline__ void sfinish(const GemvJob &J, int t, bool valid, int64_t p,
+                                        int it, int team, int wt, int lane, int e_x,
+                                        const int32_t *sig, int32_t *err,
+                                        int64_t (*red)[kTeams][4][kTileRows],
+                                        uint64_t &best) {
+  p = (int64_t)((uint64_t)p + dpp_u64<0xB1, 0xF>((uint64_t)p));
+  p = (int64_t)((uint64_t)p + dpp_u64<0x4E, 0xF>((uint64_t)p));
+  const int par = it & 1;
+  if ((lane & 3) == 0) red[par][team][wt][lane >> 2] = p;
+  __syncthreads();
+  if (valid && wt == (it & 3) && lane < kTileRows) {
+    const int64_t tot = red[par][team][0][lane] + red[par][team][1][lane] +
+                        red[par][team][2][lane] + red[par][team][3][lane];
+    const int row = t * kTileRows + lane;
+    if (row < J.nrows) {
+      const int64_t y = rshr64(tot >> 4, J.sh);
+      if (y > 2147483647LL || y < -2147483647LL) atomicOr(err, 1);
+      const int shift = J.p0 - e_x;
+      switch (J.epi) {
+        case EPI_Y32:
+          store_coherent((int32_t *)J.out + row, (int32_t)y);
+          break;
+        case EPI_MOVY_I16:
+          store_coherent((int16_t *)J.out + row,
+                         (int16_t)clamp64(movy_shift(y, shift), -32768, 32767));
+          break;
+        case EPI_MOVY_P32:
+          store_coherent((int32_t *)J.out + row,
+                         (int32_t)clamp64(movy_shift(y, shift), -2147483648LL, 2147483647LL));
+          break;
+        case EPI_SILU32:
+          store_coherent((int16_t *)J.out + row, (int16_t)silu32(y, shift, sig));
+          break;
+        case EPI_SHIFT_I64:
+          store_coherent((int64_t *)J.out + row, movy_shift(y, shift));
+          break;
+        default: {
+          const uint64_t k = argmax_key((int32_t)y, (uint32_t)row);
+          best = k > best ? k : best;
+        }
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(kSWG) void stream_kernel(StreamParams S) {
   __shared__ __align__(16) int8_t xs[kKMax];
   __shared__ int32_t xlo[kKMax / 32];
-  __shared__ int64_t red[2][kWaves][kTileRows];
-  __shared__ int64_t sm[kWaves];
-  __shared__ uint64_t keys[kWaves];
+  __shared__ int64_t red[2][kTeams][4][kTileRows];
+  __shared__ int64_t sm[kSWaves];
+  __shared__ uint64_t keys[kSWaves];
 
   const int tid = threadIdx.x, lane = tid & 63, q = lane & 3;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int rank = blockIdx.x, G = gridDim.x;
+  const int team = wave >> 2, wt = wave & 3;
+  const int G = gridDim.x, V = G * kTeams;
+  const int v = blockIdx.x * kTeams + team;
 
   // the wavefront's pending item and its registers
-  int cs = -1, ctg = 0, cb = 0;
+  int cs = -1, ct = 0, cb = 0;
   for (int s2 = 0; s2 < S.nsites && cs < 0; ++s2) {
     const GemvParams &Q = S.sites[s2];
-    const int t0 = first_tile(Q, rank, G);
-    if (t0 < Q.total_tiles && wave < Q.nblk) {
-      cs = s2; ctg = t0; cb = wave;
+    const int t0 = team_first(Q, v, V);
+    if (t0 < Q.total_tiles && wt < Q.nblk) {
+      cs = s2; ct = t0; cb = wt;
     }
   }
   BlockRegs cur;
   if (cs >= 0)
-    load_block(cur, block_addr(S.sites[cs], ctg, cb), groups_in(S.sites[cs].NG, cb), lane);
+    load_block(cur, block_addr(S.sites[cs], ct, cb), groups_in(S.sites[cs].NG, cb), lane);
 
   uint64_t best = 0;
   int it = 0;
   for (int s = 0; s < S.nsites; ++s) {
     const GemvParams &P = S.sites[s];
-    if (s > 0) site_wait(S.done + (s - 1), (uint32_t)G, S.err);
-    if (S.trace && rank == 0 && tid == 0) S.trace[s] = wall_clock64();
-    XRegs X;
-    prologue_load(P, X);
-    const int e_x = prologue_compute(P, X, xs, sm);
+    if (s > 0) site_wait(S.done + kCounterStride * (kXcds + 1) * (s - 1), (uint32_t)G, S.err);
+    if (S.trace && blockIdx.x == 0 && tid == 0) S.trace[s] = wall_clock64();
+    const int e_x = stream_prologue(P, xs, sm);
     __syncthreads();
-    build_corrections(xs, xlo, P.NG);
+    sbuild_corrections(xs, xlo, P.NG);
     __syncthreads();
     const int32_t *sig = P.tables + kSigmoidOff;
-    for (int tg = first_tile(P, rank, G); tg < P.total_tiles; tg += G, ++it) {
-      const GemvJob &J = P.job[job_of(P, tg)];
-      const int t = tg - J.tile0;
+    const int first = team_first(P, v, V);
+    // every team runs the same number of iterations (the barriers inside
+    // are workgroup-wide); a team past its last tile idles through them
+    const int iters = (P.total_tiles + V - 1) / V;
+    for (int i = 0; i < iters; ++i, ++it) {
+      const int t = first + i * V;
+      const bool valid = t < P.total_tiles;
+      const GemvJob &J = P.job[job_of(P, valid ? t : 0)];
       int64_t p = 0;
-      for (int b = wave; b < P.nblk; b += kWaves) {
-        int ns, ntg, nb;
-        next_item(S, s, tg, b, rank, wave, G, ns, ntg, nb);
-        BlockRegs nxt;
-        if (ns >= 0)
-          load_block(nxt, block_addr(S.sites[ns], ntg, nb), groups_in(S.sites[ns].NG, nb), lane);
-        p = dot_block(cur, groups_in(P.NG, b), b * kGroupsPerBlock, q, xs, xlo, p);
-        if (ns >= 0) cur = nxt;
+      if (valid) {
+        for (int b = wt; b < P.nblk; b += 4) {
+          int ns, nt, nb;
+          snext(S, s, t, b, v, V, wt, ns, nt, nb);
+          BlockRegs nxt;
+          if (ns >= 0)
+            load_block(nxt, block_addr(S.sites[ns], nt, nb), groups_in(S.sites[ns].NG, nb), lane);
+          p = dot_block(cur, groups_in(P.NG, b), b * kGroupsPerBlock, q, xs, xlo, p);
+          if (ns >= 0) cur = nxt;
+        }
       }
-      tile_finish(J, t, p, it, wave, lane, e_x, sig, S.err, red, best);
+      sfinish(J, valid ? t - J.tile0 : 0, valid, p, it, team, wt, lane, e_x, sig, S.err,
+              red, best);
     }
-    site_arrive(S.done + s);
+    site_arrive(S.done + kCounterStride * (kXcds + 1) * s);
   }
-  if (S.trace && rank == 0 && tid == 0) S.trace[S.nsites] = wall_clock64();
-  if (S.head_site >= 0) write_partial(best, S.partials, keys, wave, lane);
+  if (S.trace && blockIdx.x == 0 && tid == 0) S.trace[S.nsites] = wall_clock64();
+  if (S.head_site >= 0) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const uint64_t other = __shfl_xor(best, o);
+      best = other > best ? other : best;
+    }
+    __syncthreads();
+    if (lane == 0) keys[wave] = best;
+    __syncthreads();
+    if (tid == 0) {
+      uint64_t k = keys[0];
+      for (int w = 1; w < kSWaves; ++w) k = keys[w] > k ? keys[w] : k;
+      S.partials[blockIdx.x] = k;
+    }
+  }
 }
 
 __global__ __launch_bounds__(kWG) void argmax_final_kernel(
@@ -924,16 +1167,14 @@ hipError_t launch_alu(int op, const int32_t *y, const int16_t *b, int64_t n, int
 
 hipError_t launch_stream(const StreamParams &sp, int grid, hipStream_t s) {
   void *args[] = {(void *)&sp};
-  return hipLaunchCooperativeKernel((const void *)stream_kernel, dim3(grid), dim3(kWG),
+  return hipLaunchCooperativeKernel((const void *)stream_kernel, dim3(grid), dim3(kSWG),
                                     args, 0, s);
 }
 
-int stream_max_blocks_per_cu() {
-  int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, stream_kernel, kWG, 0) !=
-          hipSuccess || n < 1)
-    n = 1;
-  return n;
+int stream_max_blocks_per_cu() { return 1; }
+
+size_t stream_counter_words(int nsites) {
+  return (size_t)kCounterStride * (kXcds + 1) * (size_t)nsites;
 }
 
 int gemv_max_blocks_per_cu() {
