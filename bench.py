@@ -5,8 +5,10 @@ One step = one pass of the W4A8 matvec path over the whole stream: 129 DYNQ8
 sites (65 with a fused RMSNorm), 249 matrices, 4,091,805,696 bytes of int4
 weights + uint16 scales, every matvec followed by its MOVY / SILU32 epilogue
 and the 248,320-row LM head by its argmax.  Sites run in order (site s+1
-starts after site s completes), replayed as one HIP graph.  All inputs are
+starts after site s completes).  All inputs are
 synthetic, seeded and resident in HBM before the timed region.
+--mode graph (default) replays one GEMV launch per site as a HIP graph;
+--mode persistent runs the whole step in one cooperative launch.
 
 Prints one JSON line.  `value` = stream bytes / wall time per step.
 `roofline` = the GEMV kernel alone: stream bytes / sum of its per-launch
@@ -73,7 +75,10 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--mode", choices=["persistent", "graph"], default="persistent",
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain 1 GiB device copy (known bytes), the "
+                         "reference point for rocprofv3 FETCH_SIZE/WRITE_SIZE")
+    ap.add_argument("--mode", choices=["persistent", "graph"], default="graph",
                     help="one cooperative launch per step, or one launch per "
                          "site replayed as a HIP graph")
     args = ap.parse_args()
@@ -86,6 +91,16 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.copy_calibration:
+        # one dispatch that reads and writes exactly 1 GiB
+        src = torch.ones(1 << 28, dtype=torch.int32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": src.numel() * 4,
+                          "copy_bytes_written": dst.numel() * 4}), flush=True)
+        return
     from fable5_llm_amd import stream9b
     from fable5_llm_amd.engine import Context
 
