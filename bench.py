@@ -26,6 +26,20 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_kernel_9b_stream_traffic.md")
+
+
+def pmc_traffic():
+    """HBM bytes per gemv_kernel launch from the committed rocprofv3
+    FETCH_SIZE + WRITE_SIZE passes (copy-calibrated); counters cannot be
+    read from inside this process, so the figure comes from that summary."""
+    try:
+        for line in open(TRAFFIC_PROFILE):
+            if line.startswith("| traffic_bytes_per_launch |"):
+                return int(line.split("|")[2])
+    except OSError:
+        pass
+    return None
 METRIC = "achieved HBM GB/s (% of peak) on W4A8 GEMV; ms per 9B-shape weight stream"
 
 
@@ -171,7 +185,10 @@ def main():
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": pmc_traffic() if args.mode == "graph" else None,
+            "traffic_source": ("rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated, "
+                               "profiles/gemv_kernel_9b_stream_traffic.md"
+                               if args.mode == "graph" else None),
             "kernel": "stream_kernel" if args.mode == "persistent" else "gemv_kernel",
             "launches_per_step": nlaunch,
             "avg_launch_us": round(kern_ms / nlaunch * 1e3, 3),

@@ -13,10 +13,13 @@ How each function is pinned (the checks live in tests/test_oracle_*.py):
                     matvec_engine.sv:252-258, tb/vec_s*/params.txt, manifests
   sh_for_k          manifests (K 1024/2048/3584 -> 5/6/7), closed form
   pack/unpack       tb/vec_s*/beats.hex byte images and the committed
-                    tb/scripts/*_w*.bin images (row subsets)
+                    tb/scripts/*_w*.bin images (row subsets); at K = 4096 /
+                    8192 / 12288 (2-3 scale beats) the bytes the reference's
+                    pack_ddr_rows wrote (tests/golden/q9_vectors.npz)
   matvec_y32        tb/vec_s1..s4 golden y32; every V record of
-                    tb/scripts/{layer,token}_s*.txt (row subsets); brute
-                    force with Python ints; dequantised-float bound
+                    tb/scripts/{layer,token}_s*.txt (row subsets); y32 the
+                    reference's matvec_y32 wrote at K = 4096 / 8192 / 12288;
+                    brute force with Python ints; dequantised-float bound
   dyn_quant_i8      tb/vectors/s*/alu_dynq8_{x,y,e}; R+E records before each
                     V record; brute-force exponent search
   rsqrt_lut/rsqrt_q roms/rsqrt_rom.hex; tb/rsqrt_cases_s*.txt (2000 cases)

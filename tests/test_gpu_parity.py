@@ -49,6 +49,18 @@ def test_upload_download_roundtrip_scripts(engine, scripts):
             w.free()
 
 
+def test_q9_images_and_y32(engine, q9):
+    """Reference bytes and y32 at K = 4096 / 8192 / 12288 (1-3 scale beats)."""
+    from tests.conftest import q9_cases
+    for c in q9_cases(q9):
+        w = engine.upload(c["img"], c["N"], c["K"], c["sh"])
+        assert w.download() == c["img"], c["tag"]
+        assert np.array_equal(engine.matvec_y32(w, c["x8"]), c["y32"]), c["tag"]
+        ext = np.full(c["K"], -128, dtype=np.int8)
+        assert np.array_equal(engine.matvec_y32(w, ext), c["y32_ext"]), c["tag"]
+        w.free()
+
+
 # ---------------------------------------------------- matvec goldens
 def test_matvec_vec_goldens(engine, vectors):
     for s in range(1, 5):

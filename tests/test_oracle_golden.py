@@ -113,6 +113,28 @@ def test_pack_roundtrip_script_images(scripts):
             assert law.pack_ddr_rows(w4, m)[0] == rec["img"]
 
 
+def test_q9_images_and_y32(q9):
+    """The 9B row geometry (2 and 3 scale beats per row): the reference's
+    own pack_ddr_rows bytes and matvec_y32 outputs, incl. all-(-8) x all-(-128)
+    products at full-range mantissas."""
+    from tests.conftest import q9_cases
+    n = 0
+    for c in q9_cases(q9):
+        assert c["sh"] == law.sh_for_k(c["K"])
+        assert c["stride"] == law.row_stride(c["K"])
+        img, stride = law.pack_ddr_rows(c["w4"], c["m"])
+        assert stride == c["stride"] and img == c["img"], c["tag"]
+        w4, m = law.unpack_ddr_rows(c["img"], c["N"], c["K"])
+        assert np.array_equal(w4, c["w4"]) and np.array_equal(m, c["m"])
+        y = law.matvec_y32(c["w4"], c["m"], c["sh"], c["x8"])
+        assert np.array_equal(y, c["y32"]), c["tag"]
+        ext = np.full(c["K"], -128, dtype=np.int8)
+        y = law.matvec_y32_image(c["img"], c["N"], c["K"], c["sh"], ext)
+        assert np.array_equal(y, c["y32_ext"]), c["tag"]
+        n += 1
+    assert n == 9
+
+
 def test_pack_w4_nibble_order():
     # low nibble = even k (w4a8_ref.py:331-334)
     w = np.array([[1, -2, 7, -8]], dtype=np.int8)
