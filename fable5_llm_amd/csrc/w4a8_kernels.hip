@@ -342,9 +342,7 @@ __device__ __forceinline__ uint32_t scale_of(const uint4 &sc, int i) {
   return (i & 1) ? (w >> 16) : (w & 0xFFFFu);
 }
 
-__device__ __forceinline__ uint4 ldg16(const uint8_t *p) {
-  return *(const uint4 *)p;
-}
+__device__ __forceinline__ uint4 ldg16(const uint8_t *p) { return ldg16_nt(p); }
 
 // One scale block (8 groups, fewer in the last block) of one tile, as held
 // by one lane: its 16-byte scale row and 8 weight pieces of 32 weights.

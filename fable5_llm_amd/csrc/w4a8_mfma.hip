@@ -48,12 +48,11 @@ __global__ __launch_bounds__(kWG) void matmul_kernel(
       const uint8_t *bb = tb + (int64_t)b * kBlockBytes;
       uint4 sc[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sc[r] = *(const uint4 *)(bb + (4 * q + r) * 16);
+      for (int r = 0; r < 4; ++r) sc[r] = ldg16_nt(bb + (4 * q + r) * 16);
       const int ng = min(kGroupsPerBlock, NG - b * kGroupsPerBlock);
       for (int i = 0; i < ng; ++i) {
         const int g = b * kGroupsPerBlock + i;
-        const uint4 wp = *(const uint4 *)(bb + kScaleChunk + i * kGroupChunk +
-                                          (c * 4 + q) * 16);
+        const uint4 wp = ldg16_nt(bb + kScaleChunk + i * kGroupChunk + (c * 4 + q) * 16);
         const v4i a0 = {cvt_lo16(wp.x), cvt_hi16(wp.x), cvt_lo16(wp.y), cvt_hi16(wp.y)};
         const v4i a1 = {cvt_lo16(wp.z), cvt_hi16(wp.z), cvt_lo16(wp.w), cvt_hi16(wp.w)};
         uint32_t m[4];
