@@ -137,6 +137,8 @@ int take_err(w4a8_ctx *c) {
     if (h & 1) return fail(W4A8_E_Y32_OVF, "y32 overflow — sh miscomputed");
     if (h & 2)
       return fail(W4A8_E_HIP, "a persistent plan's site-completion wait timed out");
+    if (h & 4)
+      return fail(W4A8_E_HIP, "a persistent plan's in-workgroup wait timed out");
   }
   return W4A8_OK;
 }
@@ -161,6 +163,9 @@ int set_prologue(w4a8_ctx *c, GemvParams &P, int32_t K, int32_t prologue,
                                     " is not a power of 2");
     if (K > 8192)
       return fail(W4A8_E_RANGE, "rmsnorm_fx: n=" + std::to_string(K) + " > 8192");
+    if (in_f < 0 || in_f > kRmsInFMax)
+      return fail(W4A8_E_RANGE, "rmsnorm_fx: in_f=" + std::to_string(in_f) +
+                                    " outside 0.." + std::to_string(kRmsInFMax));
   }
   P.K = K;
   P.NG = K / kGroup;
@@ -509,6 +514,9 @@ static int vec_prologue(w4a8_ctx *c, int32_t pro, const int16_t *x16,
     if ((n & (n - 1)) != 0)
       return fail(W4A8_E_RANGE, "rmsnorm_fx: n=" + std::to_string(n) + " is not a power of 2");
     if (n > 8192) return fail(W4A8_E_RANGE, "rmsnorm_fx: n > 8192");
+    if (in_f < 0 || in_f > kRmsInFMax)
+      return fail(W4A8_E_RANGE, "rmsnorm_fx: in_f=" + std::to_string(in_f) +
+                                    " outside 0.." + std::to_string(kRmsInFMax));
   }
   P.K = n;
   P.NG = 0;
@@ -770,17 +778,23 @@ static int plan_build_persistent(w4a8_plan *p) {
     }
   p->G = c->num_cu * stream_max_blocks_per_cu();
   std::vector<GemvParams> sites(n);
-  // tile t of site s goes to team (off_s + t) mod V, V = G * teams, so the
-  // teams that finish a site early start the next one first
-  const int64_t V = (int64_t)p->G * kStreamTeams;
+  // tile t of site s goes to workgroup (off_s + t) mod G: the tiles of
+  // consecutive sites continue one round-robin, so every workgroup's share
+  // of the whole plan differs from the others' by at most one tile
+  const int64_t V = (int64_t)p->G;
   int64_t off = 0;
   for (int i = 0; i < n; ++i) {
     sites[i] = p->steps[i].P;
+    if (sites[i].pro == PRO_RMSNORM_DYNQ8 && sites[i].K > kStreamNormKMax)
+      return fail(W4A8_E_ARG, "a persistent plan takes RMSNorm sites of K <= " +
+                                  std::to_string(kStreamNormKMax) + " (step " +
+                                  std::to_string(i) + " has K=" +
+                                  std::to_string(sites[i].K) + ")");
     sites[i].tile_rot = (int32_t)((V - off % V) % V);
     off += sites[i].total_tiles;
   }
   HIP_TRY(hipMalloc(&p->d_sites, sizeof(GemvParams) * (size_t)n));
-  HIP_TRY(hipMalloc(&p->d_done, sizeof(uint32_t) * stream_counter_words(n)));
+  HIP_TRY(hipMalloc(&p->d_done, sizeof(uint32_t) * stream_counter_words(p->G)));
   HIP_TRY(hipMalloc(&p->d_pkeys, sizeof(uint64_t) * (size_t)p->G));
   HIP_TRY(hipMemcpy(p->d_sites, sites.data(), sizeof(GemvParams) * (size_t)n,
                     hipMemcpyHostToDevice));
@@ -797,7 +811,7 @@ static int plan_launch_persistent(w4a8_plan *p, hipStream_t s, hipEvent_t e0,
   sp.err = p->ctx->d_err;
   sp.partials = p->d_pkeys;
   sp.trace = trace;
-  HIP_TRY(launch_fill_i32((int32_t *)p->d_done, 0, (int64_t)stream_counter_words(sp.nsites), s));
+  HIP_TRY(launch_fill_i32((int32_t *)p->d_done, 0, (int64_t)stream_counter_words(p->G), s));
   if (e0) HIP_TRY(hipEventRecord(e0, s));
   HIP_TRY(launch_stream(sp, p->G, s));
   if (e1) HIP_TRY(hipEventRecord(e1, s));

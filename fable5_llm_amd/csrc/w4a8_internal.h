@@ -73,6 +73,13 @@ __device__ __forceinline__ uint4 ldg16_nt(const uint8_t *p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// RMSNorm output binary point.  Within 0..40 the reference's int64 steps
+// (x * r << (e - 30) for e > 30, layer_fixed.py:1274) never wrap: |x * r| <
+// 2^46 and e - 30 <= 17, so the kernels' 64-bit magnitudes are exact.
+// Larger in_f (no 16-bit activation format has one) would make the
+// reference's numpy shift wrap, so the engine refuses them.
+constexpr int kRmsInFMax = 40;
+
 // Table offsets inside the device table buffer (int32 entries).
 constexpr int kRsqrtOff = 0;      // 512 Q1.15 seeds
 constexpr int kSigmoidOff = 512;  // 257 Q15 knots
@@ -119,24 +126,24 @@ hipError_t launch_gemv(const GemvParams &p, int grid, hipStream_t s);
 hipError_t launch_gemv_timed(const GemvParams &p, int grid, hipStream_t s,
                              hipEvent_t start, hipEvent_t stop);
 // Persistent decode-step kernel: every site of a plan in one cooperative
-// launch of one workgroup per CU with kStreamTeams teams of 4 wavefronts;
-constexpr int kStreamTeams = 2;
-//
-// launch, site order kept by per-site completion counters.
+// launch of one workgroup per CU (8 weight wavefronts streaming through LDS
+// rings + 1 control wavefront); site order kept by one completion flag per
+// workgroup.
+constexpr int kStreamNormKMax = 4096;   // RMSNorm sites of a persistent plan
 struct StreamParams {
   const GemvParams *sites;  // device array, nsites entries
   int32_t nsites;
   int32_t head_site;        // index of the LM-head site, or -1
-  uint32_t *done;           // stream_counter_words(nsites) words, zero at launch
-  int32_t *err;             // bit 1: a completion wait gave up
+  uint32_t *done;           // stream_counter_words(grid) words, zero at launch
+  int32_t *err;             // bit 1: a completion wait gave up; bit 2: an LDS wait did
   uint64_t *partials;       // head: one key per workgroup
   uint64_t *trace;          // optional: nsites + 1 wall-clock stamps taken by
                             // workgroup 0 as it starts each site, and at its end
 };
 hipError_t launch_stream(const StreamParams &sp, int grid, hipStream_t s);
 int stream_max_blocks_per_cu();
-// uint32 words of completion counters a plan of nsites needs
-size_t stream_counter_words(int nsites);
+// uint32 words of completion flags a grid of `grid` workgroups needs
+size_t stream_counter_words(int grid);
 
 hipError_t launch_argmax_final(const uint64_t *partials, int n,
                                int32_t *result, hipStream_t s);

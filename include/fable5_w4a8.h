@@ -35,7 +35,7 @@ extern "C" {
 #define W4A8_E_Y32_OVF  (-4) /* |y32| >= 2^31: w4a8_ref.py:288 "y32 overflow — sh miscomputed" */
 #define W4A8_E_HIP      (-5) /* HIP runtime failure */
 #define W4A8_E_ARG      (-6) /* null / misaligned pointer, bad handle, bad enum */
-#define W4A8_E_RANGE    (-7) /* value outside the law's domain: rmsnorm n not a power of 2
+#define W4A8_E_RANGE    (-7) /* value outside the law's domain: rmsnorm n not a power of 2 or in_f outside 0..40
                                 (layer_fixed.py:1270-1272), vocab > 2^18 (gen_model_script.py:564-565),
                                 ALU count > 16383 (gen_layer_script.py:1377-1386) */
 
