@@ -11,159 +11,150 @@
 
 namespace w4a8 {
 
-__device__ int32_t block_max_i32(int32_t v, int64_t *sm) {
-  v = wave_max_i32(v);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = v;
-  __syncthreads();
-  int32_t r = (int32_t)sm[0];
-#pragma unroll
-  for (int i = 1; i < kWaves; ++i) r = max(r, (int32_t)sm[i]);
-  return r;
-}
-__device__ uint64_t block_sum_u64(uint64_t v, int64_t *sm) {
-  v = wave_sum_u64(v);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = (int64_t)v;
-  __syncthreads();
-  uint64_t r = 0;
-#pragma unroll
-  for (int i = 0; i < kWaves; ++i) r += (uint64_t)sm[i];
-  return r;
-}
-
 // ---------------------------------------------------------------------------
 // prologue: produce x8 (and e_x) in LDS.  Every workgroup computes the same
 // values (DYNQ8 is one exponent over the whole vector and cannot be chunked,
-// SEQ_ISA.md:560-569), so no grid-wide synchronisation is needed.
+// SEQ_ISA.md:560-569), so no grid-wide synchronisation is needed.  NT
+// threads take pieces of 8 elements: thread t holds elements
+// [c*NT*8 + 8t, +8) of piece c, so the 4 threads of a DPP quad hold 32
+// consecutive elements -- one (group, k-quarter) of the weight layout.
 // ---------------------------------------------------------------------------
-constexpr int kPieces = kKMax / (kWG * 8);   // 6 pieces of 8 int16 per thread
-
-
-
-// The activation vector of one site, held in registers from the moment its
-// loads are issued (before any weight load, so it is not queued behind the
-// weight stream) until the prologue consumes it.
-constexpr int kNormPieces = 8192 / (kWG * 8);   // RMSNorm vectors are <= 8192
-
-struct XRegs {
-  int4 pc[kPieces];       // int16 x (or, for PRO_X8, 16 int8 per piece)
-  int4 wv[kNormPieces];   // int16 norm weights
-};
-
-// Pieces c < npieces(K) hold data; the count is uniform, so the unrolled
-// piece loops below branch on scalars and never run masked-off pieces.
-__device__ __forceinline__ int npieces(int K, int per_piece) {
-  return (K + kWG * per_piece - 1) / (kWG * per_piece);
+// v has been loaded: uses after this point need no wait, and no memory
+// access is moved above it
+__device__ __forceinline__ void arrived(int4 &v) {
+  int a = v.x, b = v.y, c = v.z, d = v.w;
+  asm volatile("" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) :: "memory");
+  v = make_int4(a, b, c, d);
 }
 
-__device__ __forceinline__ void prologue_load(const GemvParams &P, XRegs &X) {
-  const int tid = threadIdx.x;
+template <int NT>
+struct ProRegs {
+  static constexpr int kPc = (kKMax + NT * 8 - 1) / (NT * 8);   // int16 pieces
+  static constexpr int kNw = (8192 + NT * 8 - 1) / (NT * 8);    // norm pieces (K <= 8192)
+  int4 pc[kPc];   // int16 x (PRO_X8: 16 int8 per piece)
+  int4 wv[kNw];   // int16 RMSNorm weights
+};
+
+// The activation loads are issued before any weight load, so they are not
+// queued behind the weight stream.  Every piece is loaded without a branch
+// (the address clamped to the vector, the value zeroed past K), so all of a
+// thread's loads are in flight together and one wait covers them.
+template <int NT>
+__device__ __forceinline__ void pro_load(const GemvParams &P, ProRegs<NT> &X, int tid) {
   const int K = P.K;
+  const int4 z = make_int4(0, 0, 0, 0);
   if (P.pro == PRO_X8) {
     const int8_t *x = (const int8_t *)P.x;
-    const int np = npieces(K, 16);
 #pragma unroll
-    for (int c = 0; c < kPieces / 2; ++c) {
-      if (c < np) {
-        const int i = (c * kWG + tid) * 16;
-        if (i < K) X.pc[c] = *(const int4 *)(x + i);
-      }
+    for (int c = 0; c < ProRegs<NT>::kPc; ++c) {
+      const int i = (c * NT + tid) * 16;
+      const int4 v = *(const int4 *)(x + (i < K ? i : K - 16));
+      X.pc[c] = i < K ? v : z;
     }
     return;
   }
   const int16_t *x16 = (const int16_t *)P.x;
-  const int np = npieces(K, 8);
 #pragma unroll
-  for (int c = 0; c < kPieces; ++c) {
-    if (c < np) {
-      const int base = c * kWG * 8 + tid * 8;
-      X.pc[c] = base < K ? *(const int4 *)(x16 + base) : make_int4(0, 0, 0, 0);
-    }
+  for (int c = 0; c < ProRegs<NT>::kPc; ++c) {
+    const int base = c * NT * 8 + tid * 8;
+    const int4 v = *(const int4 *)(x16 + (base < K ? base : K - 8));
+    X.pc[c] = base < K ? v : z;
   }
   if (P.pro == PRO_RMSNORM_DYNQ8) {
 #pragma unroll
-    for (int c = 0; c < kNormPieces; ++c) {
-      if (c < np) {
-        const int base = c * kWG * 8 + tid * 8;
-        X.wv[c] = base < K ? *(const int4 *)(P.norm_w + base) : make_int4(0, 0, 0, 0);
-      }
+    for (int c = 0; c < ProRegs<NT>::kNw; ++c) {
+      const int base = c * NT * 8 + tid * 8;
+      const int4 v = *(const int4 *)(P.norm_w + (base < K ? base : K - 8));
+      X.wv[c] = base < K ? v : z;
     }
   }
 }
 
-// rshift_round of a magnitude (s uniform, >= 0)
-__device__ __forceinline__ uint64_t round_shift_mag(uint64_t mag, int s) {
-  return s == 0 ? mag : ((mag + ((uint64_t)1 << (s - 1))) >> s);
-}
-
-__device__ int prologue_compute(const GemvParams &P, XRegs &X, int8_t *xs, int64_t *sm) {
-  const int tid = threadIdx.x;
+// sm: 2 * NT / 64 int64 of LDS.  Leaves x8 in xs[0, K) and the offset
+// corrections -8 * (sum of the x8 met by the offset-form low nibbles of
+// each (group, k-quarter)) in xlo; returns e_x.
+template <int NT, typename TabT>
+__device__ int pro_compute(const GemvParams &P, ProRegs<NT> &X, int8_t *xs, int32_t *xlo,
+                           int64_t *sm, const TabT *rsqrt_lut, int tid) {
+  constexpr int NW = NT / 64;
   const int K = P.K;
+  const int lane = tid & 63, wave = tid >> 6;
   const bool writer = blockIdx.x == 0;
   if (P.pro == PRO_X8) {
-    const int np8 = npieces(K, 16);
+    const int np = (K + NT * 16 - 1) / (NT * 16);
 #pragma unroll
-    for (int c = 0; c < kPieces / 2; ++c) {
-      const int i = (c * kWG + tid) * 16;
-      if (c < np8 && i < K) {
+    for (int c = 0; c < ProRegs<NT>::kPc; ++c) {
+      const int i = (c * NT + tid) * 16;
+      if (c < np && i < K) {
         *(int4 *)(xs + i) = X.pc[c];
         if (writer && P.x8_out) *(int4 *)(P.x8_out + i) = X.pc[c];
       }
     }
+    __syncthreads();
+    for (int c = tid; c < P.NG * 4; c += NT) {
+      const int *xw = (const int *)(xs + 32 * c);
+      int s = 0;
+      s = __builtin_amdgcn_sdot4(xw[0], 0x01010101, s, false);
+      s = __builtin_amdgcn_sdot4(xw[2], 0x01010101, s, false);
+      s = __builtin_amdgcn_sdot4(xw[4], 0x01010101, s, false);
+      s = __builtin_amdgcn_sdot4(xw[6], 0x01010101, s, false);
+      xlo[c] = -8 * s;
+    }
     if (writer && P.e_x_out && tid == 0) *P.e_x_out = P.e_x_given;
+    __syncthreads();
     return P.e_x_given;
   }
-  const int np = npieces(K, 8);
+  const int np = (K + NT * 8 - 1) / (NT * 8);
   if (P.pro == PRO_RMSNORM_DYNQ8) {
-    // layer_fixed.py:1262-1278, in sign-magnitude form: rshift_round rounds
+    // layer_fixed.py:1262-1278 in sign-magnitude form: rshift_round rounds
     // the magnitude, so |x * r| and |y * sc| carry the rounding and the
     // sign is restored afterwards
     uint64_t ss = 0;
 #pragma unroll
-    for (int c = 0; c < kNormPieces; ++c) {
-      if (c < np) {
+    for (int c = 0; c < ProRegs<NT>::kNw; ++c)
+      if (c < np)
 #pragma unroll
         for (int j = 0; j < 8; j += 2) {
           const int32_t a = piece_get(X.pc[c], j), b = piece_get(X.pc[c], j + 1);
           ss += (uint64_t)((uint32_t)(a * a) + (uint32_t)(b * b));
         }
-      }
-    }
-    ss = block_sum_u64(ss, sm);
+    ss = wave_sum_u64(ss);
+    if (lane == 0) sm[wave] = (int64_t)ss;
+    __syncthreads();
+    ss = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) ss += (uint64_t)sm[w];
     if (ss == 0) ss = 1;
-    const int nbits = 31 - __clz(K);
     int64_t r;
     int e;
-    rsqrt_q(ss, 2 * P.in_f + nbits, P.tables + kRsqrtOff, &r, &e);
+    rsqrt_q(ss, 2 * P.in_f + (31 - __clz(K)), rsqrt_lut, &r, &e);
     const int s1 = 30 - e;
     const int32_t one = P.one_plus ? (1 << 14) : 0;
-    // |x| * r < 2^46.  Every element step below is branch-free: the right
-    // shift (s1 >= 0, capped at 63) and the left shift (s1 < 0) are both
-    // formed and the uniform sign of s1 selects one
     const int rs = s1 < 0 ? 0 : (s1 > 63 ? 63 : s1);
     const int ls = s1 < 0 ? (-s1 > 63 ? 63 : -s1) : 0;
     const uint64_t half1 = rs > 0 ? ((uint64_t)1 << (rs - 1)) : 0;
     const bool right = s1 >= 0;
-    // pieces past K hold zeros (loaded as such), which normalise to zero:
-    // only the stores need the per-thread bound
+    // r < 2^31 (a Q30 reciprocal square root) and |x| <= 2^15; for in_f in
+    // 0..40 (checked on the host) the left shift is at most 17, so the
+    // shifted |x| * r stays below 2^63
+    const uint32_t r32 = (uint32_t)r;
 #pragma unroll
-    for (int c = 0; c < kNormPieces; ++c) {
-      const int base = c * kWG * 8 + tid * 8;
+    for (int c = 0; c < ProRegs<NT>::kNw; ++c) {
+      const int base = c * NT * 8 + tid * 8;
       if (c < np) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int32_t xv = piece_get(X.pc[c], j);
           const int32_t sc = (int32_t)piece_get(X.wv[c], j) + one;
-          const uint64_t mag = (uint64_t)(uint32_t)abs(xv) * (uint64_t)r;
+          const uint64_t mag = (uint64_t)(uint32_t)abs(xv) * (uint64_t)r32;
           uint64_t ym = right ? ((mag + half1) >> rs) : (mag << ls);
-          // clip to [-2^32, 2^32 - 1]
-          const uint64_t cap = (uint64_t)0xFFFFFFFFu + (uint64_t)(xv < 0);
-          ym = ym < cap ? ym : cap;
-          // rshift_round(y * sc, 14) on the magnitude, then clip16
-          const uint64_t q = (ym * (uint64_t)(uint32_t)abs(sc) + 8192u) >> 14;
+          // y is clipped to [-2^32, 2^32 - 1]; a magnitude of 2^32 or more
+          // saturates the int16 result for any nonzero scale exactly as
+          // 2^32 - 1 does, so the product is formed in 32 x 32 bits
+          ym = ym < 0xFFFFFFFFull ? ym : 0xFFFFFFFFull;
+          const uint64_t qv = ((uint64_t)(uint32_t)ym * (uint64_t)(uint32_t)abs(sc) + 8192u) >> 14;
           const bool neg = (xv < 0) != (sc < 0);
-          const int32_t q32 = q > 65535u ? 65535 : (int32_t)q;
+          const int32_t q32 = qv > 65535u ? 65535 : (int32_t)qv;
           const int32_t qm = min(q32, 32767 + (int32_t)neg);
           piece_set(X.pc[c], j, (int16_t)(neg ? -qm : qm));
         }
@@ -173,80 +164,81 @@ __device__ int prologue_compute(const GemvParams &P, XRegs &X, int8_t *xs, int64
   }
   int32_t mx = 0;
 #pragma unroll
-  for (int c = 0; c < kPieces; ++c)
+  for (int c = 0; c < ProRegs<NT>::kPc; ++c)
     if (c < np)
 #pragma unroll
       for (int j = 0; j < 8; ++j) mx = max(mx, abs((int32_t)piece_get(X.pc[c], j)));
-  mx = block_max_i32(mx, sm);
-  int e = 0;
-  while (((mx + ((1 << e) >> 1)) >> e) > 127) ++e;
+  mx = wave_max_i32(mx);
+  if (lane == 0) sm[NW + wave] = mx;
+  __syncthreads();
+  mx = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) mx = max(mx, (int32_t)sm[NW + w]);
+  // fixedpoint.py:24-33: the least e with rshift_round(max, e) <= 127 is
+  // bitlen(max) - 7, or one more when rounding carries past 127
+  int e = mx > 127 ? 25 - __clz(mx) : 0;
+  if (e > 0 && ((mx + (1 << (e - 1))) >> e) > 127) ++e;
   const int32_t half = (1 << e) >> 1;
 #pragma unroll
-  for (int c = 0; c < kPieces; ++c) {
-    const int base = c * kWG * 8 + tid * 8;
+  for (int c = 0; c < ProRegs<NT>::kPc; ++c) {
+    const int base = c * NT * 8 + tid * 8;
     if (c < np) {
       uint32_t lo = 0, hi = 0;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int32_t v = piece_get(X.pc[c], j);
         const int32_t qm = min((abs(v) + half) >> e, 127);
-        const uint32_t b = (uint32_t)(uint8_t)(int8_t)(v < 0 ? -qm : qm);
-        if (j < 4) lo |= b << (8 * j);
-        else       hi |= b << (8 * (j - 4));
+        const uint32_t b8 = (uint32_t)(uint8_t)(int8_t)(v < 0 ? -qm : qm);
+        if (j < 4) lo |= b8 << (8 * j);
+        else       hi |= b8 << (8 * (j - 4));
       }
+      int t4 = __builtin_amdgcn_sdot4((int)lo, 0x01010101, 0, false);
+      t4 += __builtin_amdgcn_update_dpp(0, t4, 0xB1, 0xF, 0xF, false);
+      t4 += __builtin_amdgcn_update_dpp(0, t4, 0x4E, 0xF, 0xF, false);
       if (base < K) {
         *(uint2 *)(xs + base) = make_uint2(lo, hi);
+        if ((tid & 3) == 0) xlo[base / 32] = -8 * t4;
         if (writer && P.x8_out) *(uint2 *)(P.x8_out + base) = make_uint2(lo, hi);
       }
     }
   }
   if (writer && P.e_x_out && tid == 0) *P.e_x_out = e;
+  __syncthreads();
   return e;
 }
 
 // ---------------------------------------------------------------------------
-// the GEMV
+// the GEMV: one 768-thread workgroup per CU, 3 teams of 4 wavefronts that
+// share one prologue.  Team v of workgroup r takes tiles r + G*(v + 3i);
+// its 4 wavefronts split a tile's scale blocks, each keeping its next block
+// in flight while it computes the current one.
 // ---------------------------------------------------------------------------
-
 __device__ __forceinline__ const uint8_t *block_addr(const GemvParams &P, int tg, int b) {
   const int j = job_of(P, tg);
   return P.job[j].w + (int64_t)(tg - P.job[j].tile0) * P.tile_bytes +
          (int64_t)b * kBlockBytes;
 }
 
+constexpr int kGT = 768;
+constexpr int kGWaves = kGT / 64;
+constexpr int kGTeams = kGWaves / 4;
 
-// x8 in LDS -> -8 * sum of the x8 values that meet the offset-form low
-// nibbles of each (group, quarter): dwords 0,2,4,6 of every 32-byte piece
-__device__ __forceinline__ void build_corrections(const int8_t *xs, int32_t *xlo, int NG) {
-  for (int c = threadIdx.x; c < NG * 4; c += kWG) {
-    const int *xw = (const int *)(xs + 32 * c);
-    int s = 0;
-    s = __builtin_amdgcn_sdot4(xw[0], 0x01010101, s, false);
-    s = __builtin_amdgcn_sdot4(xw[2], 0x01010101, s, false);
-    s = __builtin_amdgcn_sdot4(xw[4], 0x01010101, s, false);
-    s = __builtin_amdgcn_sdot4(xw[6], 0x01010101, s, false);
-    xlo[c] = -8 * s;
-  }
-}
-
-
-// reduce a tile's 16 * p over the 4 k-quarter lanes and the 4 wavefronts,
-// then round, check and write the 16 rows (one wavefront, rotating per tile)
-__device__ __forceinline__ void tile_finish(const GemvJob &J, int t, int64_t p, int it,
-                                            int wave, int lane, int e_x,
-                                            const int32_t *sig, int32_t *err,
-                                            int64_t (*red)[kWaves][kTileRows],
-                                            uint64_t &best) {
-  // sum the 4 k-quarter lanes of each row (lanes 4r..4r+3: one DPP quad)
+// reduce a tile's 16 * p over the 4 k-quarter lanes and the team's 4
+// wavefronts, then round, check and write its 16 rows (one wavefront of the
+// team, rotating per tile)
+__device__ __forceinline__ void team_tile_finish(const GemvJob &J, int t, bool valid, int64_t p,
+                                                 int it, int team, int wt, int lane, int e_x,
+                                                 const uint16_t *sig, int32_t *err,
+                                                 int64_t (*red)[kGTeams][4][kTileRows],
+                                                 uint64_t &best) {
   p = (int64_t)((uint64_t)p + dpp_u64<0xB1, 0xF>((uint64_t)p));
   p = (int64_t)((uint64_t)p + dpp_u64<0x4E, 0xF>((uint64_t)p));
   const int par = it & 1;
-  if ((lane & 3) == 0) red[par][wave][lane >> 2] = p;
+  if ((lane & 3) == 0) red[par][team][wt][lane >> 2] = p;
   __syncthreads();
-  if (wave == (it & (kWaves - 1)) && lane < kTileRows) {
-    int64_t tot = 0;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) tot += red[par][w][lane];
+  if (valid && wt == (it & 3) && lane < kTileRows) {
+    const int64_t tot = red[par][team][0][lane] + red[par][team][1][lane] +
+                        red[par][team][2][lane] + red[par][team][3][lane];
     const int row = t * kTileRows + lane;
     if (row < J.nrows) {
       const int64_t y = rshr64(tot >> 4, J.sh);   // tot is 16 * p exactly
@@ -278,70 +270,92 @@ __device__ __forceinline__ void tile_finish(const GemvJob &J, int t, int64_t p, 
   }
 }
 
-__device__ __forceinline__ void write_partial(uint64_t best, uint64_t *partials,
-                                              uint64_t *keys, int wave, int lane) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint64_t other = __shfl_xor(best, o);
-    best = other > best ? other : best;
-  }
-  __syncthreads();
-  if (lane == 0) keys[wave] = best;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint64_t k = keys[0];
-    for (int w = 1; w < kWaves; ++w) k = keys[w] > k ? keys[w] : k;
-    partials[blockIdx.x] = k;
-  }
-}
-
-__global__ __launch_bounds__(kWG) void gemv_kernel(GemvParams P) {
+__global__ __launch_bounds__(kGT) void gemv_kernel(GemvParams P) {
   __shared__ __align__(16) int8_t xs[kKMax];
   __shared__ int32_t xlo[kKMax / 32];
-  __shared__ int64_t red[2][kWaves][kTileRows];
-  __shared__ int64_t sm[kWaves];
-  __shared__ uint64_t keys[kWaves];
+  __shared__ int64_t red[2][kGTeams][4][kTileRows];
+  __shared__ int64_t sm[2 * kGWaves];
+  __shared__ uint64_t keys[kGWaves];
+  __shared__ uint16_t tab_rsqrt[512], tab_sig[264];
 
   const int tid = threadIdx.x, lane = tid & 63, q = lane & 3;
-  // wave index as a scalar so the block loop below branches on SGPRs
+  // wave index as a scalar so the block loops below branch on SGPRs
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int NG = P.NG, nblk = P.nblk;
+  const int team = wave >> 2, wt = wave & 3;
+  const int NG = P.NG, nblk = P.nblk, T = P.total_tiles;
+  const int G = gridDim.x, r = blockIdx.x, VS = G * kGTeams;
   // The activation loads go out first; the weights do not depend on x, so
-  // this wave's first block is put in flight right behind them and both
+  // this wavefront's first block is put in flight right behind them and both
   // memory latencies overlap with the prologue.
-  XRegs X;
-  prologue_load(P, X);
+  // The rsqrt seeds and sigmoid knots move to LDS with the activations:
+  // a table read from global memory after the weight loads are issued would
+  // wait for those (vector loads complete in order).
+  static_assert(kGT >= 512, "one table entry per thread");
+  int trs = P.tables[kRsqrtOff + (tid < 512 ? tid : 0)];
+  int tsg = P.tables[kSigmoidOff + (tid < 257 ? tid : 0)];
+  ProRegs<kGT> X;
+  pro_load<kGT>(P, X, tid);
+  // x has arrived before any weight load is issued: each piece passes
+  // through an empty asm, which the compiler must wait for and cannot move
+  // the weight loads above.  Otherwise it waits for "all loads" before the
+  // prologue and the prologue inherits a full weight-load latency.
+#pragma unroll
+  for (int c = 0; c < ProRegs<kGT>::kPc; ++c) arrived(X.pc[c]);
+#pragma unroll
+  for (int c = 0; c < ProRegs<kGT>::kNw; ++c) arrived(X.wv[c]);
+  asm volatile("" : "+v"(trs), "+v"(tsg) :: "memory");
+  if (tid < 512) tab_rsqrt[tid] = (uint16_t)trs;
+  if (tid < 257) tab_sig[tid] = (uint16_t)tsg;
   BlockRegs cur;
-  if ((int)blockIdx.x < P.total_tiles && wave < nblk)
-    load_block(cur, block_addr(P, blockIdx.x, wave), groups_in(NG, wave), lane);
-  const int e_x = prologue_compute(P, X, xs, sm);
-  __syncthreads();
-  build_corrections(xs, xlo, NG);
-  __syncthreads();
-
-  const int32_t *sig = P.tables + kSigmoidOff;
-  uint64_t best = 0;   // argmax key (0 == none)
-  int it = 0;
-  for (int tg = blockIdx.x; tg < P.total_tiles; tg += gridDim.x, ++it) {
-    const GemvJob &J = P.job[job_of(P, tg)];
-    const int t = tg - J.tile0;
-    int64_t p = 0;
-    for (int b = wave; b < nblk; b += kWaves) {
-      // prefetch this wave's next block (same tile, or its next tile)
-      int nb = b + kWaves, ntg = tg;
-      if (nb >= nblk) {
-        nb = wave;
-        ntg = tg + gridDim.x;
-      }
-      const bool more = ntg < P.total_tiles;
-      BlockRegs nxt;
-      if (more) load_block(nxt, block_addr(P, ntg, nb), groups_in(NG, nb), lane);
-      p = dot_block(cur, groups_in(NG, b), b * kGroupsPerBlock, q, xs, xlo, p);
-      if (more) cur = nxt;
-    }
-    tile_finish(J, t, p, it, wave, lane, e_x, sig, P.err, red, best);
+  {
+    const int tg = r + G * team;
+    if (tg < T && wt < nblk)
+      load_block(cur, block_addr(P, tg, wt), groups_in(NG, wt), lane);
   }
-  if (P.partials) write_partial(best, P.partials, keys, wave, lane);
+  const int e_x = pro_compute<kGT>(P, X, xs, xlo, sm, tab_rsqrt, tid);
+
+  const uint16_t *sig = tab_sig;
+  uint64_t best = 0;   // argmax key (0 == none)
+  // every team runs the same number of iterations (the reductions inside are
+  // workgroup barriers); team 0 has the most tiles
+  const int iters = T > r ? (T - r + VS - 1) / VS : 0;
+  for (int it = 0; it < iters; ++it) {
+    const int tg = r + G * (team + kGTeams * it);
+    const bool valid = tg < T;
+    const GemvJob &J = P.job[job_of(P, valid ? tg : 0)];
+    int64_t p = 0;
+    if (valid) {
+      for (int b = wt; b < nblk; b += 4) {
+        // prefetch this wavefront's next block (same tile, or its next tile)
+        int nb = b + 4, ntg = tg;
+        if (nb >= nblk) {
+          nb = wt;
+          ntg = tg + VS;
+        }
+        const bool more = ntg < T;
+        BlockRegs nxt;
+        if (more) load_block(nxt, block_addr(P, ntg, nb), groups_in(NG, nb), lane);
+        p = dot_block(cur, groups_in(NG, b), b * kGroupsPerBlock, q, xs, xlo, p);
+        if (more) cur = nxt;
+      }
+    }
+    team_tile_finish(J, valid ? tg - J.tile0 : 0, valid, p, it, team, wt, lane, e_x, sig,
+                     P.err, red, best);
+  }
+  if (P.partials) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const uint64_t other = __shfl_xor(best, o);
+      best = other > best ? other : best;
+    }
+    if (lane == 0) keys[wave] = best;
+    __syncthreads();
+    if (tid == 0) {
+      uint64_t k = keys[0];
+      for (int w = 1; w < kGWaves; ++w) k = keys[w] > k ? keys[w] : k;
+      P.partials[r] = k;
+    }
+  }
 }
 
 __global__ __launch_bounds__(kWG) void argmax_final_kernel(
@@ -367,10 +381,11 @@ __global__ __launch_bounds__(kWG) void argmax_final_kernel(
 // prologue only: DYNQ8 / RMSNorm(+DYNQ8) of one vector, one workgroup
 __global__ __launch_bounds__(kWG) void vec_prologue_kernel(GemvParams P) {
   __shared__ __align__(16) int8_t xs[kKMax];
-  __shared__ int64_t sm[kWaves];
-  XRegs X;
-  prologue_load(P, X);
-  prologue_compute(P, X, xs, sm);
+  __shared__ int32_t xlo[kKMax / 32];
+  __shared__ int64_t sm[2 * kWaves];
+  ProRegs<kWG> X;
+  pro_load<kWG>(P, X, threadIdx.x);
+  pro_compute<kWG>(P, X, xs, xlo, sm, P.tables + kRsqrtOff, threadIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -572,13 +587,13 @@ hipError_t launch_unpack(const uint8_t *src, int64_t nrows, const Layout &L,
 }
 
 hipError_t launch_gemv(const GemvParams &p, int grid, hipStream_t s) {
-  hipLaunchKernelGGL(gemv_kernel, dim3(grid), dim3(kWG), 0, s, p);
+  hipLaunchKernelGGL(gemv_kernel, dim3(grid), dim3(kGT), 0, s, p);
   return hipGetLastError();
 }
 
 hipError_t launch_gemv_timed(const GemvParams &p, int grid, hipStream_t s,
                              hipEvent_t start, hipEvent_t stop) {
-  hipExtLaunchKernelGGL(gemv_kernel, dim3(grid), dim3(kWG), 0, s, start, stop, 0, p);
+  hipExtLaunchKernelGGL(gemv_kernel, dim3(grid), dim3(kGT), 0, s, start, stop, 0, p);
   return hipGetLastError();
 }
 
@@ -617,9 +632,9 @@ hipError_t launch_alu(int op, const int32_t *y, const int16_t *b, int64_t n, int
 
 int gemv_max_blocks_per_cu() {
   int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_kernel, kWG, 0) !=
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_kernel, kGT, 0) !=
           hipSuccess || n < 1)
-    n = 4;
+    n = 1;
   return n;
 }
 
