@@ -95,6 +95,9 @@ def main():
     ap.add_argument("--mode", choices=["persistent", "graph"], default="graph",
                     help="one cooperative launch per step, or one launch per "
                          "site replayed as a HIP graph")
+    ap.add_argument("--fences", choices=["all", "auto"], default="all",
+                    help="persistent mode: every site waits for all earlier ones, "
+                         "or only where it shares a buffer with one")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -125,7 +128,8 @@ def main():
     t_build = time.perf_counter()
     from fable5_llm_amd import _native as N
     mode = N.PLAN_PERSISTENT if args.mode == "persistent" else N.PLAN_GRAPH
-    st = stream9b.Stream9B(ctx, seed=args.seed, mode=mode)
+    fences = N.FENCE_AUTO if args.fences == "auto" else N.FENCE_ALL
+    st = stream9b.Stream9B(ctx, seed=args.seed, mode=mode, fences=fences)
     ctx.sync()
     t_build = time.perf_counter() - t_build
     tot = stream9b.totals(st.sites)

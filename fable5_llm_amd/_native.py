@@ -18,6 +18,7 @@ EPI_Y32, EPI_MOVY_I16, EPI_MOVY_P32, EPI_SILU32, EPI_SHIFT_I64 = 0, 1, 2, 3, 4
 ALU_SHIFT32, ALU_SILU32, ALU_EMUL32, ALU_SHIFT32W = 1, 6, 8, 9
 MOVY_PAIRS32, MOVY_INT16 = 0, 1
 PLAN_GRAPH, PLAN_PERSISTENT = 0, 1
+FENCE_ALL, FENCE_AUTO = 0, 1
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
@@ -59,6 +60,7 @@ SIGNATURES = {
                            _I32, _P, _P, _P],
     "w4a8_plan_add_head": [_P, _P, _I32, _P, _P, _I32, _I32, _I32, _P],
     "w4a8_plan_set_mode": [_P, _I32],
+    "w4a8_plan_set_fences": [_P, _I32],
     "w4a8_plan_run": [_P],
     "w4a8_plan_profile": [_P, _I32, _P],
     "w4a8_plan_destroy": [_P],

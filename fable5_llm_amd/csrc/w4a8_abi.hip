@@ -138,7 +138,7 @@ int take_err(w4a8_ctx *c) {
     if (h & 2)
       return fail(W4A8_E_HIP, "a persistent plan's site-completion wait timed out");
     if (h & 4)
-      return fail(W4A8_E_HIP, "a persistent plan's in-workgroup wait timed out");
+      return fail(W4A8_E_HIP, "a wait between wavefronts of one workgroup timed out");
   }
   return W4A8_OK;
 }
@@ -734,6 +734,7 @@ int w4a8_matmul_y32_async(w4a8_ctx *c, const w4a8_weights *w, const int8_t *d_x8
 struct w4a8_plan {
   w4a8_ctx *ctx = nullptr;
   int32_t mode = W4A8_PLAN_GRAPH;
+  int32_t fences = W4A8_FENCE_ALL;
   struct Step {
     GemvParams P;
     int grid;
@@ -765,6 +766,62 @@ static void plan_drop_persistent(w4a8_plan *p) {
   p->G = 0;
 }
 
+// Byte ranges a step reads and writes (the weights are read-only for the
+// plan's lifetime and never written by a step).
+struct ByteRange {
+  uintptr_t lo, hi;
+};
+static void step_ranges(const w4a8_plan::Step &st, std::vector<ByteRange> &rd,
+                        std::vector<ByteRange> &wr) {
+  const GemvParams &P = st.P;
+  auto add = [](std::vector<ByteRange> &v, const void *q, int64_t n) {
+    if (q && n > 0) v.push_back({(uintptr_t)q, (uintptr_t)q + (uintptr_t)n});
+  };
+  add(rd, P.x, P.pro == PRO_X8 ? (int64_t)P.K : 2 * (int64_t)P.K);
+  if (P.pro == PRO_RMSNORM_DYNQ8) add(rd, P.norm_w, 2 * (int64_t)P.K);
+  for (int j = 0; j < P.njobs; ++j) {
+    const GemvJob &J = P.job[j];
+    int64_t es = 0;
+    switch (J.epi) {
+      case EPI_MOVY_I16:
+      case EPI_SILU32: es = 2; break;
+      case EPI_Y32:
+      case EPI_MOVY_P32: es = 4; break;
+      case EPI_SHIFT_I64: es = 8; break;
+      default: es = 0; break;   // EPI_ARGMAX writes the head result below
+    }
+    add(wr, J.out, es * J.nrows);
+  }
+  add(wr, P.x8_out, P.K);
+  add(wr, P.e_x_out, 4);
+  add(wr, P.xn_out, 2 * (int64_t)P.K);
+  if (st.head) add(wr, st.result, 2 * sizeof(int32_t));
+}
+static bool ranges_meet(const std::vector<ByteRange> &a, const std::vector<ByteRange> &b) {
+  for (const auto &x : a)
+    for (const auto &y : b)
+      if (x.lo < y.hi && y.lo < x.hi) return true;
+  return false;
+}
+
+// W4A8_FENCE_AUTO: a site waits for the whole GPU only when it reads what a
+// site since the last fence writes, or writes what one of those reads or
+// writes -- the reference sequencer's FENCE rule (a result is waited for
+// before it is consumed, seq_format.py:2077-2231), applied across sites.
+static void plan_fences(const w4a8_plan *p, std::vector<GemvParams> &sites) {
+  const int n = (int)p->steps.size();
+  std::vector<std::vector<ByteRange>> rd(n), wr(n);
+  for (int i = 0; i < n; ++i) step_ranges(p->steps[i], rd[i], wr[i]);
+  int last = 0;   // first site since the last fence
+  for (int i = 0; i < n; ++i) {
+    bool f = i > 0 && p->fences == W4A8_FENCE_ALL;
+    for (int j = last; j < i && !f; ++j)
+      f = ranges_meet(rd[i], wr[j]) || ranges_meet(wr[i], rd[j]) || ranges_meet(wr[i], wr[j]);
+    sites[i].fence = f ? 1 : 0;
+    if (f) last = i;
+  }
+}
+
 static int plan_build_persistent(w4a8_plan *p) {
   w4a8_ctx *c = p->ctx;
   const int n = (int)p->steps.size();
@@ -793,6 +850,7 @@ static int plan_build_persistent(w4a8_plan *p) {
     sites[i].tile_rot = (int32_t)((V - off % V) % V);
     off += sites[i].total_tiles;
   }
+  plan_fences(p, sites);
   HIP_TRY(hipMalloc(&p->d_sites, sizeof(GemvParams) * (size_t)n));
   HIP_TRY(hipMalloc(&p->d_done, sizeof(uint32_t) * stream_counter_words(p->G)));
   HIP_TRY(hipMalloc(&p->d_pkeys, sizeof(uint64_t) * (size_t)p->G));
@@ -899,6 +957,14 @@ int w4a8_plan_set_mode(w4a8_plan *p, int32_t mode) {
     return fail(W4A8_E_ARG, "unknown plan mode");
   if (mode != p->mode) plan_drop_graph(p);
   p->mode = mode;
+  return W4A8_OK;
+}
+
+int w4a8_plan_set_fences(w4a8_plan *p, int32_t fences) {
+  if (!p || (fences != W4A8_FENCE_ALL && fences != W4A8_FENCE_AUTO))
+    return fail(W4A8_E_ARG, "unknown fence mode");
+  if (fences != p->fences) plan_drop_graph(p);
+  p->fences = fences;
   return W4A8_OK;
 }
 

@@ -163,6 +163,41 @@ __device__ __forceinline__ uint64_t argmax_key(int32_t v, uint32_t row) {
 
 __device__ __forceinline__ uint4 ldg16(const uint8_t *p) { return ldg16_nt(p); }
 
+// ---------------------------------------------------------------------------
+// LDS flags between wavefronts.  Written as inline assembly: the compiler's
+// own LDS synchronisation (workgroup fences, __syncthreads) also waits for
+// every outstanding global load of the wavefront.  A wavefront's LDS
+// instructions execute in order, so a flag written after data is seen after
+// it, and data read after a flag was seen is current.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ uint32_t lds_off(const void *p) {
+  return (uint32_t)(uintptr_t)(lds_void_t *)p;
+}
+__device__ __forceinline__ int32_t lds_read_i32(const int32_t *p) {
+  int32_t v;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_off(p)) : "memory");
+  return v;
+}
+__device__ __forceinline__ void lds_write_i32(int32_t *p, int32_t v) {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\tds_write_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)"
+               :: "v"(lds_off(p)), "v"(v) : "memory");
+}
+__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+constexpr uint32_t kLdsSpin = 1u << 20;   // polls before an LDS wait gives up
+
+// the wavefront waits until the LDS word at p is at least v; false if it
+// gave up after kLdsSpin polls
+__device__ __forceinline__ bool lds_wait_ge(const int32_t *p, int32_t v) {
+  for (uint32_t n = 0; n < kLdsSpin; ++n) {
+    if (lds_read_i32(p) >= v) return true;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return false;
+}
+
 // One scale block (8 groups, fewer in the last block) of one tile, as held
 // by one lane: its 16-byte scale row and 8 weight pieces of 32 weights.
 struct BlockRegs {

@@ -68,6 +68,7 @@ inline Layout layout_for(int32_t K) {
 // from displacing activations, outputs and counters in the caches (a plain
 // 4 GiB stream: 6.1 TB/s with ordinary loads, 7.0 TB/s non-temporal).
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+constexpr int kAuxNt = 2;   // cache-policy operand of the buffer-load builtins: nt
 __device__ __forceinline__ uint4 ldg16_nt(const uint8_t *p) {
   const u32x4_t v = __builtin_nontemporal_load((const u32x4_t *)p);
   return make_uint4(v.x, v.y, v.z, v.w);
@@ -107,11 +108,13 @@ struct GemvParams {
   const int16_t *norm_w;    // int16[K] Q14 (RMSNorm)
   int32_t in_f, one_plus, e_x_given;
   int32_t tile_rot;         // persistent stream: first tile of WG r is (r + tile_rot) % G
+  int32_t fence;            // persistent stream: every earlier site completes on all
+                            // workgroups before this one reads its activations
   int8_t *x8_out;           // optional (written by workgroup 0)
   int32_t *e_x_out;         // optional
   int16_t *xn_out;          // optional RMSNorm output
   const int32_t *tables;    // kTableLen entries
-  int32_t *err;             // bit 0: y32 overflow
+  int32_t *err;             // bit 0: y32 overflow; bit 2: an LDS wait gave up
   uint64_t *partials;       // EPI_ARGMAX: one key per workgroup
 };
 
@@ -126,9 +129,9 @@ hipError_t launch_gemv(const GemvParams &p, int grid, hipStream_t s);
 hipError_t launch_gemv_timed(const GemvParams &p, int grid, hipStream_t s,
                              hipEvent_t start, hipEvent_t stop);
 // Persistent decode-step kernel: every site of a plan in one cooperative
-// launch of one workgroup per CU (8 weight wavefronts streaming through LDS
-// rings + 1 control wavefront); site order kept by one completion flag per
-// workgroup.
+// launch of one workgroup per CU (8 weight wavefronts holding their next two
+// blocks in registers + 1 control wavefront); a site with `fence` set waits
+// for one completion flag per workgroup.
 constexpr int kStreamNormKMax = 4096;   // RMSNorm sites of a persistent plan
 struct StreamParams {
   const GemvParams *sites;  // device array, nsites entries

@@ -37,19 +37,18 @@ struct ProRegs {
 
 // The activation loads are issued before any weight load, so they are not
 // queued behind the weight stream.  Every piece is loaded without a branch
-// (the address clamped to the vector, the value zeroed past K), so all of a
-// thread's loads are in flight together and one wait covers them.
+// (the address clamped to the vector), so all of a thread's loads are in
+// flight together and one wait covers them; pieces past K are zeroed by
+// pro_mask, at first use, so nothing between the two waits for the loads.
 template <int NT>
 __device__ __forceinline__ void pro_load(const GemvParams &P, ProRegs<NT> &X, int tid) {
   const int K = P.K;
-  const int4 z = make_int4(0, 0, 0, 0);
   if (P.pro == PRO_X8) {
     const int8_t *x = (const int8_t *)P.x;
 #pragma unroll
     for (int c = 0; c < ProRegs<NT>::kPc; ++c) {
       const int i = (c * NT + tid) * 16;
-      const int4 v = *(const int4 *)(x + (i < K ? i : K - 16));
-      X.pc[c] = i < K ? v : z;
+      X.pc[c] = *(const int4 *)(x + (i < K ? i : K - 16));
     }
     return;
   }
@@ -57,29 +56,72 @@ __device__ __forceinline__ void pro_load(const GemvParams &P, ProRegs<NT> &X, in
 #pragma unroll
   for (int c = 0; c < ProRegs<NT>::kPc; ++c) {
     const int base = c * NT * 8 + tid * 8;
-    const int4 v = *(const int4 *)(x16 + (base < K ? base : K - 8));
-    X.pc[c] = base < K ? v : z;
+    X.pc[c] = *(const int4 *)(x16 + (base < K ? base : K - 8));
   }
   if (P.pro == PRO_RMSNORM_DYNQ8) {
 #pragma unroll
     for (int c = 0; c < ProRegs<NT>::kNw; ++c) {
       const int base = c * NT * 8 + tid * 8;
-      const int4 v = *(const int4 *)(P.norm_w + (base < K ? base : K - 8));
-      X.wv[c] = base < K ? v : z;
+      X.wv[c] = *(const int4 *)(P.norm_w + (base < K ? base : K - 8));
     }
   }
 }
 
+template <int NT>
+__device__ __forceinline__ void pro_mask(const GemvParams &P, ProRegs<NT> &X, int tid) {
+  const int K = P.K;
+  const int4 z = make_int4(0, 0, 0, 0);
+  const int per = P.pro == PRO_X8 ? 16 : 8;
+#pragma unroll
+  for (int c = 0; c < ProRegs<NT>::kPc; ++c)
+    if ((c * NT + tid) * per >= K) X.pc[c] = z;
+  if (P.pro == PRO_RMSNORM_DYNQ8)
+#pragma unroll
+    for (int c = 0; c < ProRegs<NT>::kNw; ++c)
+      if ((c * NT + tid) * 8 >= K) X.wv[c] = z;
+}
+
+// The prologue's barrier when the whole workgroup runs it.
+struct WgSync {
+  __device__ void operator()() const { __syncthreads(); }
+};
+
+// A barrier of wavefronts w0 .. w0+NW-1 only, in LDS: each posts its phase
+// and polls the others', so wavefronts outside the group -- stalled behind
+// their own weight loads -- are never waited for.  ok turns false if a poll
+// gave up.
+template <int NW>
+struct GroupSync {
+  int32_t *flags;   // NW LDS words, zero before the first phase
+  int w0;
+  int phase;
+  bool ok;
+  __device__ void operator()() {
+    const int lane = threadIdx.x & 63, wave = (threadIdx.x >> 6) - w0;
+    ++phase;
+    wait_lds();
+    if (lane == 0) lds_write_i32(flags + wave, phase);
+    bool done = false;
+    for (uint32_t n = 0; n < kLdsSpin && !done; ++n) {
+      done = __all(lds_read_i32(flags + lane % NW) >= phase);
+      if (!done) __builtin_amdgcn_s_sleep(1);
+    }
+    ok = ok && done;
+  }
+};
+
 // sm: 2 * NT / 64 int64 of LDS.  Leaves x8 in xs[0, K) and the offset
 // corrections -8 * (sum of the x8 met by the offset-form low nibbles of
-// each (group, k-quarter)) in xlo; returns e_x.
-template <int NT, typename TabT>
+// each (group, k-quarter)) in xlo; returns e_x.  sync() is a barrier of the
+// NT threads.
+template <int NT, typename TabT, typename Sync>
 __device__ int pro_compute(const GemvParams &P, ProRegs<NT> &X, int8_t *xs, int32_t *xlo,
-                           int64_t *sm, const TabT *rsqrt_lut, int tid) {
+                           int64_t *sm, const TabT *rsqrt_lut, int tid, Sync &sync) {
   constexpr int NW = NT / 64;
   const int K = P.K;
   const int lane = tid & 63, wave = tid >> 6;
   const bool writer = blockIdx.x == 0;
+  pro_mask<NT>(P, X, tid);
   if (P.pro == PRO_X8) {
     const int np = (K + NT * 16 - 1) / (NT * 16);
 #pragma unroll
@@ -90,7 +132,7 @@ __device__ int pro_compute(const GemvParams &P, ProRegs<NT> &X, int8_t *xs, int3
         if (writer && P.x8_out) *(int4 *)(P.x8_out + i) = X.pc[c];
       }
     }
-    __syncthreads();
+    sync();
     for (int c = tid; c < P.NG * 4; c += NT) {
       const int *xw = (const int *)(xs + 32 * c);
       int s = 0;
@@ -101,7 +143,7 @@ __device__ int pro_compute(const GemvParams &P, ProRegs<NT> &X, int8_t *xs, int3
       xlo[c] = -8 * s;
     }
     if (writer && P.e_x_out && tid == 0) *P.e_x_out = P.e_x_given;
-    __syncthreads();
+    sync();
     return P.e_x_given;
   }
   const int np = (K + NT * 8 - 1) / (NT * 8);
@@ -120,7 +162,7 @@ __device__ int pro_compute(const GemvParams &P, ProRegs<NT> &X, int8_t *xs, int3
         }
     ss = wave_sum_u64(ss);
     if (lane == 0) sm[wave] = (int64_t)ss;
-    __syncthreads();
+    sync();
     ss = 0;
 #pragma unroll
     for (int w = 0; w < NW; ++w) ss += (uint64_t)sm[w];
@@ -170,7 +212,7 @@ __device__ int pro_compute(const GemvParams &P, ProRegs<NT> &X, int8_t *xs, int3
       for (int j = 0; j < 8; ++j) mx = max(mx, abs((int32_t)piece_get(X.pc[c], j)));
   mx = wave_max_i32(mx);
   if (lane == 0) sm[NW + wave] = mx;
-  __syncthreads();
+  sync();
   mx = 0;
 #pragma unroll
   for (int w = 0; w < NW; ++w) mx = max(mx, (int32_t)sm[NW + w]);
@@ -203,7 +245,7 @@ __device__ int pro_compute(const GemvParams &P, ProRegs<NT> &X, int8_t *xs, int3
     }
   }
   if (writer && P.e_x_out && tid == 0) *P.e_x_out = e;
-  __syncthreads();
+  sync();
   return e;
 }
 
@@ -219,9 +261,51 @@ __device__ __forceinline__ const uint8_t *block_addr(const GemvParams &P, int tg
          (int64_t)b * kBlockBytes;
 }
 
+// This wavefront's blocks over the kernel: for its team's tiles it = 0, 1,
+// ... (tile r + G*(team + 3*it) < total_tiles), blocks b = wt, wt + 4, ...
+// < nblk -- nbw blocks per tile, the same for every tile.
+struct Item {
+  int k;    // position in the sequence
+  int it;   // tile iteration
+  int j;    // b = wt + 4j
+};
+__device__ __forceinline__ void item_next(Item &c, int nbw) {
+  ++c.k;
+  if (++c.j == nbw) {
+    c.j = 0;
+    ++c.it;
+  }
+}
+
+// Put a block in flight: always exactly 1 + kGroupsPerBlock loads, so the
+// compiler's count of outstanding loads is the same on every path and a
+// wait for one register set never waits for the other.  The loads are
+// buffer loads whose range ends with the block's data: past the end of the
+// sequence (range 0), and for the missing groups of a short block, they are
+// out of range, return zero and make no memory access.
+constexpr int kBufDword3 = 0x00020000;   // raw buffer, 32-bit data format (gfx9)
+
+__device__ __forceinline__ void issue_block(BlockRegs &R, const GemvParams &P, int tg, int b,
+                                            bool real, int lane) {
+  const uint8_t *bb = real ? block_addr(P, tg, b) : (const uint8_t *)P.tables;
+  const int len = real ? kScaleChunk + groups_in(P.NG, b) * kGroupChunk : 0;
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc((void *)bb, (short)0, len, kBufDword3);
+  const u32x4_t sc = __builtin_amdgcn_raw_buffer_load_b128(rs, (lane >> 2) * 16, 0, kAuxNt);
+  R.sc = make_uint4(sc.x, sc.y, sc.z, sc.w);
+#pragma unroll
+  for (int i = 0; i < kGroupsPerBlock; ++i) {
+    const u32x4_t w = __builtin_amdgcn_raw_buffer_load_b128(
+        rs, kScaleChunk + i * kGroupChunk + lane * 16, 0, kAuxNt);
+    R.w[i] = make_uint4(w.x, w.y, w.z, w.w);
+  }
+}
+
 constexpr int kGT = 768;
 constexpr int kGWaves = kGT / 64;
 constexpr int kGTeams = kGWaves / 4;
+constexpr int kPW0 = 4;                // teams 1 and 2 (wavefronts 4..11) run the prologue
+constexpr int kPT = kGT - 64 * kPW0;   // 512 threads
 
 // reduce a tile's 16 * p over the 4 k-quarter lanes and the team's 4
 // wavefronts, then round, check and write its 16 rows (one wavefront of the
@@ -277,6 +361,7 @@ __global__ __launch_bounds__(kGT) void gemv_kernel(GemvParams P) {
   __shared__ int64_t sm[2 * kGWaves];
   __shared__ uint64_t keys[kGWaves];
   __shared__ uint16_t tab_rsqrt[512], tab_sig[264];
+  __shared__ int32_t tsync[16];   // prologue group's phases [0, 8), done [8], e_x [9]
 
   const int tid = threadIdx.x, lane = tid & 63, q = lane & 3;
   // wave index as a scalar so the block loops below branch on SGPRs
@@ -284,64 +369,100 @@ __global__ __launch_bounds__(kGT) void gemv_kernel(GemvParams P) {
   const int team = wave >> 2, wt = wave & 3;
   const int NG = P.NG, nblk = P.nblk, T = P.total_tiles;
   const int G = gridDim.x, r = blockIdx.x, VS = G * kGTeams;
-  // The activation loads go out first; the weights do not depend on x, so
-  // this wavefront's first block is put in flight right behind them and both
-  // memory latencies overlap with the prologue.
-  // The rsqrt seeds and sigmoid knots move to LDS with the activations:
-  // a table read from global memory after the weight loads are issued would
-  // wait for those (vector loads complete in order).
-  static_assert(kGT >= 512, "one table entry per thread");
-  int trs = P.tables[kRsqrtOff + (tid < 512 ? tid : 0)];
-  int tsg = P.tables[kSigmoidOff + (tid < 257 ? tid : 0)];
-  ProRegs<kGT> X;
-  pro_load<kGT>(P, X, tid);
-  // x has arrived before any weight load is issued: each piece passes
-  // through an empty asm, which the compiler must wait for and cannot move
-  // the weight loads above.  Otherwise it waits for "all loads" before the
-  // prologue and the prologue inherits a full weight-load latency.
-#pragma unroll
-  for (int c = 0; c < ProRegs<kGT>::kPc; ++c) arrived(X.pc[c]);
-#pragma unroll
-  for (int c = 0; c < ProRegs<kGT>::kNw; ++c) arrived(X.wv[c]);
-  asm volatile("" : "+v"(trs), "+v"(tsg) :: "memory");
-  if (tid < 512) tab_rsqrt[tid] = (uint16_t)trs;
-  if (tid < 257) tab_sig[tid] = (uint16_t)tsg;
-  BlockRegs cur;
-  {
-    const int tg = r + G * team;
-    if (tg < T && wt < nblk)
-      load_block(cur, block_addr(P, tg, wt), groups_in(NG, wt), lane);
+  if (tid < 16) tsync[tid] = 0;
+
+  // A CU's first weight blocks take microseconds to drain at its share of
+  // HBM bandwidth, and a wavefront cannot issue past a load the memory
+  // pipeline has no room for.  So teams 1 and 2 run the prologue alone,
+  // with their own LDS barrier: they issue the activation and table loads,
+  // the workgroup meets once (nothing is waited for), and only then does
+  // team 0 put its first blocks in flight, behind the activations.  Team 0
+  // waits for the prologue's result; teams 1 and 2 start their blocks after
+  // it.
+  // Two register sets per wavefront, A and B, hold its next two blocks.
+  // Team 0 puts both in flight at once; teams 1 and 2 after the prologue.
+  const int tg0 = r + G * team;
+  const int nbw = wt < nblk ? (nblk - wt + 3) / 4 : 0;
+  const int nitems = tg0 < T ? ((T - 1 - tg0) / VS + 1) * nbw : 0;
+  Item ca{0, 0, 0}, cb = ca;
+  if (nbw > 0) item_next(cb, nbw);
+  Item cn = cb;
+  if (nbw > 0) item_next(cn, nbw);
+  BlockRegs A, B;
+  const int pt = tid - kPW0 * 64;   // thread index within the prologue group
+  int e_x;
+  bool ok;
+  if (team == 0) {
+    __syncthreads();
+    issue_block(A, P, tg0, wt, nitems > 0, lane);
+    issue_block(B, P, tg0 + VS * cb.it, wt + 4 * cb.j, cb.k < nitems, lane);
+    ok = lds_wait_ge(&tsync[8], 1);
+    e_x = lds_read_i32(&tsync[9]);
+  } else {
+    static_assert(kPT >= 512 && kPT >= 257, "one table entry per thread");
+    const int trs = P.tables[kRsqrtOff + (pt < 512 ? pt : 0)];
+    const int tsg = P.tables[kSigmoidOff + (pt < 257 ? pt : 0)];
+    ProRegs<kPT> X;
+    pro_load<kPT>(P, X, pt);
+    __syncthreads();
+    if (pt < 512) tab_rsqrt[pt] = (uint16_t)trs;
+    if (pt < 257) tab_sig[pt] = (uint16_t)tsg;
+    GroupSync<kPT / 64> sync{tsync, kPW0, 0, true};
+    e_x = pro_compute<kPT>(P, X, xs, xlo, sm, tab_rsqrt, pt, sync);
+    ok = sync.ok;
+    // every LDS write of the group is complete (its last barrier): publish
+    if (pt == 0) {
+      lds_write_i32(&tsync[9], e_x);
+      lds_write_i32(&tsync[8], 1);
+    }
+    issue_block(A, P, tg0, wt, nitems > 0, lane);
+    issue_block(B, P, tg0 + VS * cb.it, wt + 4 * cb.j, cb.k < nitems, lane);
   }
-  const int e_x = pro_compute<kGT>(P, X, xs, xlo, sm, tab_rsqrt, tid);
 
   const uint16_t *sig = tab_sig;
   uint64_t best = 0;   // argmax key (0 == none)
-  // every team runs the same number of iterations (the reductions inside are
-  // workgroup barriers); team 0 has the most tiles
+  // every team runs the same number of tile iterations (the reductions
+  // inside are workgroup barriers); team 0 has the most tiles
   const int iters = T > r ? (T - r + VS - 1) / VS : 0;
-  for (int it = 0; it < iters; ++it) {
-    const int tg = r + G * (team + kGTeams * it);
+  int fin = 0;   // tile iterations finished
+  int64_t p = 0;
+  // consume the block in R (item c), finish its tile after the wavefront's
+  // last block of it, and refill R with the item two ahead
+  auto step = [&](BlockRegs &R, Item &c) {
+    // lane-derived offsets are recomputed from an opaque copy of the thread
+    // index, so the compiler does not keep them all live across the loop
+    int tid_s = tid;
+    asm volatile("" : "+v"(tid_s));
+    const int lane = tid_s & 63, q = lane & 3;
+    const int b = wt + 4 * c.j;
+    const int tg = tg0 + VS * c.it;
+    p = dot_block(R, groups_in(NG, b), b * kGroupsPerBlock, q, xs, xlo, p);
+    if (c.j == nbw - 1) {
+      const GemvJob &J = P.job[job_of(P, tg)];
+      team_tile_finish(J, tg - J.tile0, true, p, fin, team, wt, lane, e_x, sig, P.err, red,
+                       best);
+      ++fin;
+      p = 0;
+    }
+    c = cn;
+    item_next(cn, nbw);
+    issue_block(R, P, tg0 + VS * c.it, wt + 4 * c.j, c.k < nitems, lane);
+  };
+  for (int k = 0; k < nitems; k += 2) {
+    step(A, ca);
+    if (k + 1 >= nitems) break;
+    step(B, cb);
+  }
+  // tiles this wavefront has no block of: it still takes part in the
+  // team's reduction, and is the writer of every fourth
+  for (; fin < iters; ++fin) {
+    const int tg = tg0 + VS * fin;
     const bool valid = tg < T;
     const GemvJob &J = P.job[job_of(P, valid ? tg : 0)];
-    int64_t p = 0;
-    if (valid) {
-      for (int b = wt; b < nblk; b += 4) {
-        // prefetch this wavefront's next block (same tile, or its next tile)
-        int nb = b + 4, ntg = tg;
-        if (nb >= nblk) {
-          nb = wt;
-          ntg = tg + VS;
-        }
-        const bool more = ntg < T;
-        BlockRegs nxt;
-        if (more) load_block(nxt, block_addr(P, ntg, nb), groups_in(NG, nb), lane);
-        p = dot_block(cur, groups_in(NG, b), b * kGroupsPerBlock, q, xs, xlo, p);
-        if (more) cur = nxt;
-      }
-    }
-    team_tile_finish(J, valid ? tg - J.tile0 : 0, valid, p, it, team, wt, lane, e_x, sig,
+    team_tile_finish(J, valid ? tg - J.tile0 : 0, valid, 0, fin, team, wt, lane, e_x, sig,
                      P.err, red, best);
   }
+  if (!ok && lane == 0) atomicOr(P.err, 4);
   if (P.partials) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
@@ -385,7 +506,8 @@ __global__ __launch_bounds__(kWG) void vec_prologue_kernel(GemvParams P) {
   __shared__ int64_t sm[2 * kWaves];
   ProRegs<kWG> X;
   pro_load<kWG>(P, X, threadIdx.x);
-  pro_compute<kWG>(P, X, xs, xlo, sm, P.tables + kRsqrtOff, threadIdx.x);
+  WgSync sync;
+  pro_compute<kWG>(P, X, xs, xlo, sm, P.tables + kRsqrtOff, threadIdx.x, sync);
 }
 
 // ---------------------------------------------------------------------------

@@ -7,14 +7,17 @@
 //    weight blocks this CU owns over the whole plan form one fixed sequence
 //    (its tiles of site 0, then of site 1, ...; 8448-byte scale blocks
 //    within a tile), dealt round-robin to the 8 wavefronts.  Each wavefront
-//    copies its next blocks straight from HBM into a private 2-slot LDS
-//    ring (global_load_lds, non-temporal) and refills a slot as soon as it
-//    has consumed it -- also when the next block belongs to a later site,
-//    since weights never depend on an activation.  The ring keeps streaming
-//    while the workgroup waits for the rest of the GPU and computes the next
-//    prologue.  A wavefront waits for slot i with vmcnt = the copies it
-//    issued after slot i; it makes no other global loads, so nothing else is
-//    ever waited for.
+//    holds its next two blocks in two register sets, A and B, and refills a
+//    set as soon as it has consumed it -- also when the next block belongs
+//    to a later site, since weights never depend on an activation.  So the
+//    next site's blocks stream while the workgroup waits for the rest of the
+//    GPU and computes the next prologue.
+//  * A weight wavefront makes no global access but its weight loads, and
+//    every refill is the same 9 buffer loads (out of range, so without a
+//    memory access, past the end of the sequence).  The compiler's count of
+//    a wavefront's outstanding loads is therefore exact on every path, and
+//    the wait for one register set never waits for the other.  Outputs,
+//    error bits and the exported prologue vectors go through LDS.
 //  * A tile's 16 rows are complete when every wavefront holding one of its
 //    blocks has added its partial sums into an LDS slot; the wavefront that
 //    completes the count rounds, checks and applies the epilogue, then
@@ -22,17 +25,16 @@
 //  * The control wavefront does every other global access: it stores the
 //    staged outputs, signals this workgroup's completion of a site, waits for
 //    all workgroups (one flag per workgroup), and copies the next site's
-//    activation vector (and RMSNorm weights) into LDS.  Only its own stores
-//    are waited for before it signals.
+//    activation vector (and RMSNorm weights) into LDS.
 //
-// The copies into LDS, the LDS flags and the workgroup barriers are written
-// as inline assembly: the compiler's own forms of each make a wavefront wait
-// for all of its outstanding loads (vmcnt(0)), which would empty the ring.
-// The data crossing a site boundary (outputs, activation vectors, flags)
-// moves with agent-coherent accesses (sc1), so no cache-wide writeback or
-// invalidation is needed.  Every result is bit-exact with the reference's
-// integer law (ref/w4a8_ref.py:254-289 and the epilogues of
-// gen_layer_script.py:1397-1433, seq_model.py:1027-1050).
+// The LDS flags and the workgroup barriers are inline assembly: the
+// compiler's own forms make a wavefront wait for all of its outstanding
+// loads (vmcnt(0)), which would drain the register pipeline.  The data
+// crossing a site boundary (outputs, activation vectors, flags) moves with
+// agent-coherent accesses (sc1), so no cache-wide writeback or invalidation
+// is needed.  Every result is bit-exact with the reference's integer law
+// (ref/w4a8_ref.py:254-289 and the epilogues of gen_layer_script.py:1397-1433,
+// seq_model.py:1027-1050).
 #include "w4a8_device.h"
 
 namespace w4a8 {
@@ -45,55 +47,45 @@ constexpr int kThreads = (kCW + 1) * 64;    // 576
 constexpr int kWThreads = kCW * 64;         // 512 threads run the prologue
 constexpr int kPiece = kWThreads * 8;       // 4096 elements per prologue piece
 constexpr int kXPieces = (kKMax + kPiece - 1) / kPiece;   // 3
-constexpr int kSlots = 2;                   // ring slots per weight wavefront
 constexpr int kXBytes = 2 * kKMax;          // x16 (24 KiB) / x8 + corrections
 constexpr int kXloOff = kKMax;              // int32 corrections after x8
 constexpr int kNormOff = 16384;             // RMSNorm weights (K <= 4096)
 constexpr int kTSlots = 8;                  // tiles being reduced at once
 constexpr uint32_t kGridSpin = 1u << 18;    // polls before a grid wait gives up
-constexpr uint32_t kLdsSpin = 1u << 20;     // polls before an LDS wait gives up
+constexpr int kBufDword3 = 0x00020000;      // raw buffer, 32-bit data format
 
 static_assert(kPiece % 32 == 0, "a DPP quad of threads covers one (group, quarter)");
 static_assert(kStreamNormKMax <= kPiece, "RMSNorm takes one piece per thread");
 static_assert(kNormOff + 2 * kStreamNormKMax <= kXBytes, "norm weights fit");
 static_assert(kXloOff + 4 * kKMax / 32 <= kNormOff, "corrections fit");
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-
 // The site table is read-only for the whole launch.  Read through the
 // constant address space, every (uniform) field load is a scalar load, also
 // after barriers, so weight wavefronts never issue a vector load of their
-// own besides the ring copies.
+// own besides the weight loads.
 typedef const __attribute__((address_space(4))) GemvParams CSite;
 typedef const __attribute__((address_space(4))) GemvJob CJob;
 
 struct __align__(16) Lds {
-  uint8_t ring[kCW][kSlots][kBlockBytes];
-  int8_t x[kXBytes];
+  int8_t x[2][kXBytes];             // activations of site s in x[s & 1]
+  int16_t xn[kStreamNormKMax];      // the site's RMSNorm output (workgroup 0 exports it)
   int64_t tv[kTSlots][kTileRows];   // partial sums, then staged outputs
   int32_t tcnt[kTSlots];            // contributions added to the slot
   int32_t tgen[kTSlots];            // tile number the slot is open for
   int32_t tready[kTSlots];          // tile number + 1 once its outputs are staged
   int32_t abort;                    // set by the first LDS wait that gives up
+  int32_t err;                      // error bits found by the weight wavefronts
   uint16_t rsqrt[512];
   uint16_t sig[264];
   int64_t part[2][kCW];             // prologue partial reductions
-  uint64_t keys[kCW];
+  uint64_t best;                    // argmax key of the head's rows seen here (0: none)
 };
 
 // ---------------------------------------------------------------------------
-// copies into LDS and LDS synchronisation
+// copies into LDS (control wavefront) and LDS synchronisation
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t lds_off(const void *p) {
-  return (uint32_t)(uintptr_t)(lds_void_t *)p;
-}
-
 // lane l copies 16 bytes from src (its own address) to LDS lds_base + 16 * l;
 // lds_base must be uniform
-__device__ __forceinline__ void copy16_nt(const void *src, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt"
-               :: "v"(src), "s"(lds_base) : "memory", "m0");
-}
 __device__ __forceinline__ void copy16_sc1(const void *src, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off sc1"
                :: "v"(src), "s"(lds_base) : "memory", "m0");
@@ -102,39 +94,16 @@ __device__ __forceinline__ void copy16(const void *src, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
                :: "v"(src), "s"(lds_base) : "memory", "m0");
 }
-
-// wait until at most `younger` vector-memory operations of this wavefront
-// are outstanding: loads return in order, so every copy issued before the
-// last `younger` ones has landed
-__device__ __forceinline__ void wait_vm(int younger) {
-  switch (younger) {
-    case 9: asm volatile("s_waitcnt vmcnt(9)" ::: "memory"); break;
-    case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
-    case 7: asm volatile("s_waitcnt vmcnt(7)" ::: "memory"); break;
-    case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
-    case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
-    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
-    case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
-    case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
-    case 1: asm volatile("s_waitcnt vmcnt(1)" ::: "memory"); break;
-    default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-  }
-}
 __device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// A wavefront's LDS instructions execute in order, so a flag written after
-// data is seen after it, and data read after a flag was seen is current.
-__device__ __forceinline__ int32_t lds_read_i32(const int32_t *p) {
-  int32_t v;
-  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_off(p)) : "memory");
-  return v;
-}
-__device__ __forceinline__ void lds_write_i32(int32_t *p, int32_t v) {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\tds_write_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)"
-               :: "v"(lds_off(p)), "v"(v) : "memory");
-}
 __device__ __forceinline__ void lds_add_u64(int64_t *p, int64_t v) {
   asm volatile("ds_add_u64 %0, %1" :: "v"(lds_off(p)), "v"(v) : "memory");
+}
+__device__ __forceinline__ void lds_max_u64(uint64_t *p, uint64_t v) {
+  asm volatile("ds_max_u64 %0, %1" :: "v"(lds_off(p)), "v"(v) : "memory");
+}
+__device__ __forceinline__ void lds_or_i32(int32_t *p, int32_t v) {
+  asm volatile("ds_or_b32 %0, %1" :: "v"(lds_off(p)), "v"(v) : "memory");
 }
 __device__ __forceinline__ int32_t lds_add_rtn_i32(int32_t *p, int32_t v) {
   int32_t old;
@@ -146,20 +115,23 @@ __device__ __forceinline__ int32_t lds_add_rtn_i32(int32_t *p, int32_t v) {
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
-__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-// lane 0 polls an LDS word until it equals v.  Bounded: the first wait that
-// gives up sets bit 2 of err and the workgroup's abort word, after which no
-// wait of the workgroup polls again, so a launch always drains quickly.
-__device__ __forceinline__ void lds_wait_eq(Lds &L, const int32_t *p, int v, int lane,
-                                            int32_t *err) {
+// lane 0 polls an LDS word until it equals v (or, with kAtLeast, until it
+// is at least v).  Bounded: the first wait that
+// gives up sets bit 2 of the error word and the workgroup's abort word,
+// after which no wait of the workgroup polls again, so a launch always
+// drains quickly.
+template <bool kAtLeast = false>
+__device__ __forceinline__ void lds_wait_eq(Lds &L, const int32_t *p, int v, int lane) {
   if (lane == 0) {
     uint32_t n = 0;
-    while (lds_read_i32(p) != v && lds_read_i32(&L.abort) == 0) {
+    for (;;) {
+      const int32_t cur = lds_read_i32(p);
+      if ((kAtLeast ? cur >= v : cur == v) || lds_read_i32(&L.abort) != 0) break;
       __builtin_amdgcn_s_sleep(1);
       if (++n > kLdsSpin) {
         lds_write_i32(&L.abort, 1);
-        atomicOr(err, 4);
+        lds_or_i32(&L.err, 4);
         break;
       }
     }
@@ -217,56 +189,50 @@ __device__ __forceinline__ void cur_next(CSite *sites, int nsites, int r, int G,
   cur_settle(sites, nsites, r, G, c);
 }
 
-// copy block (item) c into an LDS slot; returns the number of copies issued
-__device__ __forceinline__ int issue_block(CSite *sites, int G, const Cursor &c,
-                                           const uint8_t *slot, int lane) {
-  CSite &P = sites[c.s];
-  const int i = c.j / c.nblk, b = c.j - i * c.nblk;
-  const int t = c.first + i * G;
-  const int jb = job_of(P, t);
-  const uint8_t *src = P.job[jb].w + (int64_t)(t - P.job[jb].tile0) * P.tile_bytes +
-                       (int64_t)b * kBlockBytes;
-  const int ng = groups_in(P.NG, b);
-  const uint32_t base = lds_off(slot);
-  if (lane < kTileRows) copy16_nt(src + 16 * lane, base);
+// Put block c in flight into R: always the same 1 + kGroupsPerBlock buffer
+// loads.  The buffer's range ends with the block's data, so for an item past
+// the end of the sequence (range 0), and for the missing groups of a short
+// block, the loads are out of range: they return zero without a memory
+// access, and keep the count of outstanding loads the same on every path.
+__device__ __forceinline__ void issue_block(BlockRegs &R, CSite *sites, int nsites, int G,
+                                            const Cursor &c, int lane) {
+  const uint8_t *bb = (const uint8_t *)sites[0].tables;   // any mapped address: range 0
+  int len = 0;
+  if (c.s < nsites) {
+    CSite &P = sites[c.s];
+    const int i = c.j / c.nblk, b = c.j - i * c.nblk;
+    const int t = c.first + i * G;
+    CJob &J = P.job[job_of(P, t)];
+    bb = J.w + (int64_t)(t - J.tile0) * P.tile_bytes + (int64_t)b * kBlockBytes;
+    len = kScaleChunk + groups_in(P.NG, b) * kGroupChunk;
+  }
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc((void *)bb, (short)0, len, kBufDword3);
+  const u32x4_t sc = __builtin_amdgcn_raw_buffer_load_b128(rs, (lane >> 2) * 16, 0, kAuxNt);
+  R.sc = make_uint4(sc.x, sc.y, sc.z, sc.w);
 #pragma unroll
-  for (int g = 0; g < kGroupsPerBlock; ++g)
-    if (g < ng)
-      copy16_nt(src + kScaleChunk + kGroupChunk * g + 16 * lane,
-                base + kScaleChunk + kGroupChunk * g);
-  return 1 + ng;
-}
-
-// one lane's share of a ring slot (its scale row and 8 weight pieces) ->
-// registers; the caller waits for the reads before refilling the slot
-__device__ __forceinline__ void read_slot(const uint8_t *sl, int ng, int lane, BlockRegs &R) {
-  R.sc = *(const uint4 *)(sl + 16 * (lane >> 2));
-  if (ng == kGroupsPerBlock) {
-#pragma unroll
-    for (int i = 0; i < kGroupsPerBlock; ++i)
-      R.w[i] = *(const uint4 *)(sl + kScaleChunk + kGroupChunk * i + 16 * lane);
-  } else {
-#pragma unroll
-    for (int i = 0; i < kGroupsPerBlock; ++i)
-      if (i < ng) R.w[i] = *(const uint4 *)(sl + kScaleChunk + kGroupChunk * i + 16 * lane);
+  for (int i = 0; i < kGroupsPerBlock; ++i) {
+    const u32x4_t w = __builtin_amdgcn_raw_buffer_load_b128(
+        rs, kScaleChunk + i * kGroupChunk + lane * 16, 0, kAuxNt);
+    R.w[i] = make_uint4(w.x, w.y, w.z, w.w);
   }
 }
 
 // ------------------------------------------------------------- prologue
-// The site's activation vector is in LDS (int16 x at x[0, 2K), int8 x at
-// x[0, K) for PRO_X8; RMSNorm weights at x[kNormOff, +2K)).  Leaves x8 at
-// x[0, K) and the offset corrections at x[kXloOff]; returns e_x.  All 9
-// wavefronts call it (the same barriers); the control wavefront computes
-// nothing.
-__device__ int stream_prologue(CSite &P, Lds &L, int tid, bool ctrl) {
+// The site's activation vector is in LDS buffer xb (int16 x at xb[0, 2K),
+// int8 x at xb[0, K) for PRO_X8; RMSNorm weights at xb[kNormOff, +2K)).
+// Leaves x8 at xb[0, K) and the offset corrections at xb[kXloOff] (and, in
+// workgroup 0 when the site exports it, the RMSNorm output at L.xn); returns
+// e_x.  All 9 wavefronts call it (the same barriers); the control wavefront
+// computes nothing.
+__device__ int stream_prologue(CSite &P, Lds &L, int8_t *xb, int tid, bool ctrl) {
   const int K = P.K;
   const int lane = tid & 63, wave = tid >> 6;
-  const bool writer = blockIdx.x == 0 && !ctrl;
-  int32_t *xlo = (int32_t *)(L.x + kXloOff);
+  int32_t *xlo = (int32_t *)(xb + kXloOff);
   if (P.pro == PRO_X8) {
     if (!ctrl) {
       for (int c = tid; c < P.NG * 4; c += kWThreads) {
-        const int *xw = (const int *)(L.x + 32 * c);
+        const int *xw = (const int *)(xb + 32 * c);
         int s = 0;
         s = __builtin_amdgcn_sdot4(xw[0], 0x01010101, s, false);
         s = __builtin_amdgcn_sdot4(xw[2], 0x01010101, s, false);
@@ -274,10 +240,6 @@ __device__ int stream_prologue(CSite &P, Lds &L, int tid, bool ctrl) {
         s = __builtin_amdgcn_sdot4(xw[6], 0x01010101, s, false);
         xlo[c] = -8 * s;
       }
-      if (writer && P.x8_out)
-        for (int i = tid * 16; i < K; i += kWThreads * 16)
-          *(int4 *)(P.x8_out + i) = *(const int4 *)(L.x + i);
-      if (writer && P.e_x_out && tid == 0) *P.e_x_out = P.e_x_given;
     }
     lds_barrier();
     return P.e_x_given;
@@ -288,14 +250,14 @@ __device__ int stream_prologue(CSite &P, Lds &L, int tid, bool ctrl) {
   for (int c = 0; c < kXPieces; ++c) {
     const int base = c * kPiece + tid * 8;
     pc[c] = make_int4(0, 0, 0, 0);
-    if (!ctrl && c < np && base < K) pc[c] = *(const int4 *)(L.x + 2 * base);
+    if (!ctrl && c < np && base < K) pc[c] = *(const int4 *)(xb + 2 * base);
   }
   if (P.pro == PRO_RMSNORM_DYNQ8) {
     // layer_fixed.py:1262-1278 in sign-magnitude form (rshift_round rounds
     // the magnitude); K <= kStreamNormKMax, so one piece per thread
     const int base = tid * 8;
     int4 wv = make_int4(0, 0, 0, 0);
-    if (!ctrl && base < K) wv = *(const int4 *)(L.x + kNormOff + 2 * base);
+    if (!ctrl && base < K) wv = *(const int4 *)(xb + kNormOff + 2 * base);
     uint64_t ss = 0;
 #pragma unroll
     for (int j = 0; j < 8; j += 2) {
@@ -338,7 +300,7 @@ __device__ int stream_prologue(CSite &P, Lds &L, int tid, bool ctrl) {
       const int32_t qm = min(q32, 32767 + (int32_t)neg);
       piece_set(pc[0], j, (int16_t)(neg ? -qm : qm));
     }
-    if (writer && P.xn_out && base < K) *(int4 *)(P.xn_out + base) = pc[0];
+    if (!ctrl && blockIdx.x == 0 && P.xn_out && base < K) *(int4 *)(L.xn + base) = pc[0];
   }
   int32_t mx = 0;
 #pragma unroll
@@ -376,13 +338,11 @@ __device__ int stream_prologue(CSite &P, Lds &L, int tid, bool ctrl) {
         t4 += __builtin_amdgcn_update_dpp(0, t4, 0xB1, 0xF, 0xF, false);
         t4 += __builtin_amdgcn_update_dpp(0, t4, 0x4E, 0xF, 0xF, false);
         if (base < K) {
-          *(uint2 *)(L.x + base) = make_uint2(lo, hi);
+          *(uint2 *)(xb + base) = make_uint2(lo, hi);
           if ((tid & 3) == 0) xlo[base / 32] = -8 * t4;
-          if (writer && P.x8_out) *(uint2 *)(P.x8_out + base) = make_uint2(lo, hi);
         }
       }
     }
-    if (writer && P.e_x_out && tid == 0) *P.e_x_out = e;
   }
   lds_barrier();
   return e;
@@ -391,9 +351,9 @@ __device__ int stream_prologue(CSite &P, Lds &L, int tid, bool ctrl) {
 // ------------------------------------------------------------- tiles
 // Add this wavefront's share of tile kt; true if it completed the tile.
 __device__ __forceinline__ bool tile_add(Lds &L, int kt, int64_t p, int contributors,
-                                         int lane, int32_t *err) {
+                                         int lane) {
   const int slot = kt & (kTSlots - 1);
-  lds_wait_eq(L, &L.tgen[slot], kt, lane, err);
+  lds_wait_eq(L, &L.tgen[slot], kt, lane);
   // rows: lanes 4r..4r+3 hold the 4 k-quarters of row r
   p = (int64_t)((uint64_t)p + dpp_u64<0xB1, 0xF>((uint64_t)p));
   p = (int64_t)((uint64_t)p + dpp_u64<0x4E, 0xF>((uint64_t)p));
@@ -405,10 +365,11 @@ __device__ __forceinline__ bool tile_add(Lds &L, int kt, int64_t p, int contribu
 }
 
 // The completing wavefront: round, check and apply the epilogue to the 16
-// rows of tile kt (tile tl of job J).  Argmax tiles update `best` and free
-// the slot; the others are staged for the control wavefront.
+// rows of tile kt (tile tl of job J).  Argmax tiles fold their rows into the
+// workgroup's key in LDS and free the slot; the others are staged for the
+// control wavefront.
 __device__ __forceinline__ void tile_epilogue(Lds &L, int kt, CJob &J, int tl, int e_x,
-                                              int lane, int32_t *err, uint64_t &best) {
+                                              int lane) {
   const int slot = kt & (kTSlots - 1);
   const bool argmax = J.epi == EPI_ARGMAX;
   if (lane < kTileRows) {
@@ -417,7 +378,7 @@ __device__ __forceinline__ void tile_epilogue(Lds &L, int kt, CJob &J, int tl, i
     int64_t outv = 0;
     if (row < J.nrows) {
       const int64_t y = rshr64(tot >> 4, J.sh);   // tot is 16 * p exactly
-      if (y > 2147483647LL || y < -2147483647LL) atomicOr(err, 1);
+      if (y > 2147483647LL || y < -2147483647LL) lds_or_i32(&L.err, 1);
       const int shift = J.p0 - e_x;
       switch (J.epi) {
         case EPI_Y32: outv = y; break;
@@ -427,10 +388,9 @@ __device__ __forceinline__ void tile_epilogue(Lds &L, int kt, CJob &J, int tl, i
           break;
         case EPI_SILU32: outv = silu32(y, shift, L.sig); break;
         case EPI_SHIFT_I64: outv = movy_shift(y, shift); break;
-        default: {   // EPI_ARGMAX: raw y32, seq_format.py:2225-2226
-          const uint64_t k = argmax_key((int32_t)y, (uint32_t)row);
-          best = k > best ? k : best;
-        }
+        default:   // EPI_ARGMAX: raw y32, seq_format.py:2225-2226
+          lds_max_u64(&L.best, argmax_key((int32_t)y, (uint32_t)row));
+
       }
     }
     L.tv[slot][lane] = argmax ? 0 : outv;
@@ -447,28 +407,60 @@ __device__ __forceinline__ void tile_epilogue(Lds &L, int kt, CJob &J, int tl, i
 }
 
 // ------------------------------------------------------------- control
-// the site's activation vector (agent-coherent) and RMSNorm weights -> LDS
-__device__ __forceinline__ void ctrl_load_inputs(CSite &P, Lds &L, int lane) {
+// start copying the site's activation vector (agent-coherent) and RMSNorm
+// weights into LDS buffer xb; the caller waits (vmcnt) before the barrier
+// that hands the buffer to the weight wavefronts
+__device__ __forceinline__ void ctrl_issue_inputs(CSite &P, int8_t *xb, int lane) {
   const uint8_t *x = (const uint8_t *)P.x;
-  const int xb = P.pro == PRO_X8 ? P.K : 2 * P.K;
-  for (int off = 0; off < xb; off += 1024)
-    if (off + 16 * lane < xb) copy16_sc1(x + off + 16 * lane, lds_off(L.x + off));
+  const int nb = P.pro == PRO_X8 ? P.K : 2 * P.K;
+  for (int off = 0; off < nb; off += 1024)
+    if (off + 16 * lane < nb) copy16_sc1(x + off + 16 * lane, lds_off(xb + off));
   if (P.pro == PRO_RMSNORM_DYNQ8) {
     const uint8_t *w = (const uint8_t *)P.norm_w;
     for (int off = 0; off < 2 * P.K; off += 1024)
-      if (off + 16 * lane < 2 * P.K) copy16(w + off + 16 * lane, lds_off(L.x + kNormOff + off));
+      if (off + 16 * lane < 2 * P.K) copy16(w + off + 16 * lane, lds_off(xb + kNormOff + off));
   }
-  wait_vm_all();
 }
 
-// store the outputs of this CU's tiles of site P (tile numbers kt0, ...)
-__device__ void ctrl_serve(CSite &P, Lds &L, int kt0, int r, int G, int lane, int32_t *err) {
+// workgroup 0: the prologue's exported vectors (x8, the RMSNorm output, e_x)
+__device__ void ctrl_export(CSite &P, Lds &L, const int8_t *xb, int e_x, int lane) {
+  const int K = P.K;
+  if (P.x8_out)
+    for (int off = 16 * lane; off < K; off += 1024) {
+      const int4 v = *(const int4 *)(xb + off);
+      int32_t *o = (int32_t *)(P.x8_out + off);
+      store_coherent(o, v.x);
+      store_coherent(o + 1, v.y);
+      store_coherent(o + 2, v.z);
+      store_coherent(o + 3, v.w);
+    }
+  if (P.pro == PRO_RMSNORM_DYNQ8 && P.xn_out)
+    for (int i = 8 * lane; i < K; i += 512) {
+      const int4 v = *(const int4 *)(L.xn + i);
+      int32_t *o = (int32_t *)(P.xn_out + i);
+      store_coherent(o, v.x);
+      store_coherent(o + 1, v.y);
+      store_coherent(o + 2, v.z);
+      store_coherent(o + 3, v.w);
+    }
+  if (P.e_x_out && lane == 0) store_coherent(P.e_x_out, (int32_t)e_x);
+}
+
+// Store the outputs of this CU's tiles of site P (tile numbers kt0, ...).
+// Argmax tiles stage nothing: their slot is freed by the wavefront that
+// completes them, which is waited for here too, so that no wavefront still
+// reads this site's activations once this returns.
+__device__ void ctrl_serve(CSite &P, Lds &L, int kt0, int r, int G, int lane) {
   const int first = (r + P.tile_rot) % G;
   for (int i = 0, t = first; t < P.total_tiles; ++i, t += G) {
     CJob &J = P.job[job_of(P, t)];
-    if (J.epi == EPI_ARGMAX) continue;
     const int kt = kt0 + i, slot = kt & (kTSlots - 1);
-    lds_wait_eq(L, &L.tready[slot], kt + 1, lane, err);
+    if (J.epi == EPI_ARGMAX) {
+      // later argmax tiles may have reused and freed the slot since
+      lds_wait_eq<true>(L, &L.tgen[slot], kt + kTSlots, lane);
+      continue;
+    }
+    lds_wait_eq(L, &L.tready[slot], kt + 1, lane);
     if (lane < kTileRows) {
       const int64_t v = L.tv[slot][lane];
       const int row = (t - J.tile0) * kTileRows + lane;
@@ -525,107 +517,117 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
     L.tgen[tid] = tid;
     L.tready[tid] = 0;
   }
-  if (tid == 0) L.abort = 0;
-  wait_vm_all();   // the table loads, before any ring copy is counted
-
-  Cursor c{}, d{};       // weight wavefronts: the item computed next / copied next
-  int nd0 = 0, nd1 = 0;  // copies in flight per ring slot
-  int k = 0;             // items consumed (slot = k & 1)
-  int kt0c = 0;          // control: CU-local number of the site's first tile
-  uint64_t best = 0;
-  if (ctrl) {
-    if (nsites > 0) ctrl_load_inputs(sites[0], L, lane);
-    if (S.trace && r == 0 && lane == 0) S.trace[0] = wall_clock64();
-  } else {
-    cur_init(sites, nsites, r, G, wave, c);
-    d = c;
-    if (d.s < nsites) {
-      nd0 = issue_block(sites, G, d, L.ring[wave][0], lane);
-      cur_next(sites, nsites, r, G, d);
-    }
-    if (d.s < nsites) {
-      nd1 = issue_block(sites, G, d, L.ring[wave][1], lane);
-      cur_next(sites, nsites, r, G, d);
-    }
+  if (tid == 0) {
+    L.abort = 0;
+    L.err = 0;
+    L.best = 0;
   }
+  wait_vm_all();   // the table loads, before any weight load is counted
 
-  for (int s = 0; s < nsites; ++s) {
-    CSite &P = sites[s];
-    // the lane-derived addresses of this site are recomputed from an opaque
-    // copy of the thread index, so the compiler does not keep them all live
-    // across the whole plan
-    int tid_s = tid;
-    asm volatile("" : "+v"(tid_s));
-    const int lane_s = tid_s & 63;
-    lds_barrier();   // site s's activation vector is in LDS
-    const int e_x = stream_prologue(P, L, tid_s, ctrl);
-    if (!ctrl) {
-      const int8_t *xs = L.x;
-      const int32_t *xlo = (const int32_t *)(L.x + kXloOff);
-      const int contributors = min(P.nblk, kCW);
-      int64_t p = 0;
-      while (c.s == s) {
-        const int slot = k & 1;
-        wait_vm(slot ? nd0 : nd1);   // every copy but the other slot's has landed
-        const int i = c.j / c.nblk, b = c.j - i * c.nblk;
-        const int ng = groups_in(P.NG, b);
-        // the block moves to registers and its slot is refilled at once, so
-        // the ring holds copies in flight, not blocks being computed
-        BlockRegs R;
-        read_slot(L.ring[wave][slot], ng, lane_s, R);
-        wait_lds();
-        int nd = 0;
-        if (d.s < nsites) {
-          nd = issue_block(sites, G, d, L.ring[wave][slot], lane_s);
-          cur_next(sites, nsites, r, G, d);
-        }
-        if (slot) nd1 = nd; else nd0 = nd;
-        ++k;
-        p = dot_block(R, ng, b * kGroupsPerBlock, lane_s & 3, xs, xlo, p);
-        const Cursor done = c;
-        cur_next(sites, nsites, r, G, c);
-        if (!(c.s == s && c.j / c.nblk == i)) {   // this wavefront's last block of the tile
-          const int kt = done.kt0 + i;
-          if (tile_add(L, kt, p, contributors, lane_s, S.err)) {
-            const int t = done.first + i * G;
-            CJob &J = P.job[job_of(P, t)];
-            tile_epilogue(L, kt, J, t - J.tile0, e_x, lane_s, S.err, best);
-          }
-          p = 0;
-        }
-      }
-    } else {
-      ctrl_serve(P, L, kt0c, r, G, lane_s, S.err);
+  if (ctrl) {
+    // Site s's activations go to x[s & 1].  Unless site s+1 is fenced, its
+    // activations are copied into the other buffer while site s computes
+    // (every weight wavefront is past site s-1, the buffer's last user); a
+    // fenced site first waits until every workgroup has stored its outputs
+    // of all earlier sites (flag value s+1), then copies.
+    int kt0 = 0;   // CU-local number of the site's first tile
+    if (nsites > 0) ctrl_issue_inputs(sites[0], L.x[0], lane);
+    wait_vm_all();
+    for (int s = 0; s < nsites; ++s) {
+      CSite &P = sites[s];
+      int8_t *xb = L.x[s & 1];
+      lds_barrier();   // site s's activation vector is in LDS
+      if (S.trace && r == 0 && lane == 0) S.trace[s] = wall_clock64();
+      const bool ahead = s + 1 < nsites && !sites[s + 1].fence;
+      if (ahead) ctrl_issue_inputs(sites[s + 1], L.x[(s + 1) & 1], lane);
+      const int e_x = stream_prologue(P, L, xb, tid, true);
+      if (r == 0) ctrl_export(P, L, xb, e_x, lane);
+      // the next site's activations have landed (this site's output stores,
+      // issued below, are only waited for at a fence)
+      wait_vm_all();
+      ctrl_serve(P, L, kt0, r, G, lane);
       {
         const int first = (r + P.tile_rot) % G;
-        kt0c += first < P.total_tiles ? (P.total_tiles - 1 - first) / G + 1 : 0;
+        kt0 += first < P.total_tiles ? (P.total_tiles - 1 - first) / G + 1 : 0;
       }
-      wait_vm_all();   // outputs stored
-      if (s + 1 < nsites) {
-        if (lane_s == 0) store_coherent(S.done + r, (uint32_t)(s + 1));
-        grid_wait(S.done, G, (uint32_t)(s + 1), lane_s, S.err);
-        if (S.trace && r == 0 && lane_s == 0) S.trace[s + 1] = wall_clock64();
-        ctrl_load_inputs(sites[s + 1], L, lane_s);
+      if (s + 1 < nsites && !ahead) {
+        wait_vm_all();   // outputs stored
+        if (lane == 0) store_coherent(S.done + r, (uint32_t)(s + 1));
+        grid_wait(S.done, G, (uint32_t)(s + 1), lane, S.err);
+        ctrl_issue_inputs(sites[s + 1], L.x[(s + 1) & 1], lane);
+        wait_vm_all();
       }
     }
+  } else {
+    // A holds item k of this wavefront's sequence, B item k + 1; cn is the
+    // next item to put in flight
+    Cursor ca, cb, cn;
+    cur_init(sites, nsites, r, G, wave, ca);
+    cb = ca;
+    cur_next(sites, nsites, r, G, cb);
+    cn = cb;
+    cur_next(sites, nsites, r, G, cn);
+    BlockRegs A, B;
+    issue_block(A, sites, nsites, G, ca, lane);
+    issue_block(B, sites, nsites, G, cb, lane);
+    int s_cur = -1, e_x = 0, contributors = 0;
+    int64_t p = 0;
+    // join site s's barriers and compute its prologue; the lane-derived
+    // addresses are recomputed from an opaque copy of the thread index, so
+    // the compiler does not keep them all live across the whole plan
+    auto enter = [&](int s) {
+      int tid_s = tid;
+      asm volatile("" : "+v"(tid_s));
+      lds_barrier();   // site s's activation vector is in LDS
+      e_x = stream_prologue(sites[s], L, L.x[s & 1], tid_s, false);
+      contributors = min(sites[s].nblk, kCW);
+    };
+    // consume the block in R (item c; this wavefront's next item is nx),
+    // refill R with the item two ahead, and add into the tile after this
+    // wavefront's last block of it
+    auto step = [&](BlockRegs &R, Cursor &c, const Cursor &nx) {
+      while (s_cur < c.s) enter(++s_cur);
+      int tid_s = tid;
+      asm volatile("" : "+v"(tid_s));
+      const int lane_s = tid_s & 63;
+      CSite &P = sites[c.s];
+      const int i = c.j / c.nblk, b = c.j - i * c.nblk;
+      const int8_t *xb = L.x[c.s & 1];
+      p = dot_block(R, groups_in(P.NG, b), b * kGroupsPerBlock, lane_s & 3, xb,
+                    (const int32_t *)(xb + kXloOff), p);
+      const bool last = !(nx.s == c.s && nx.j / nx.nblk == i);
+      const Cursor done = c;
+      c = cn;
+      cur_next(sites, nsites, r, G, cn);
+      issue_block(R, sites, nsites, G, c, lane_s);
+      if (last) {
+        const int kt = done.kt0 + i;
+        if (tile_add(L, kt, p, contributors, lane_s)) {
+          const int t = done.first + i * G;
+          CJob &J = P.job[job_of(P, t)];
+          tile_epilogue(L, kt, J, t - J.tile0, e_x, lane_s);
+        }
+        p = 0;
+      }
+    };
+    for (;;) {
+      if (ca.s >= nsites) break;
+      step(A, ca, cb);
+      if (cb.s >= nsites) break;
+      step(B, cb, ca);
+    }
+    // sites after this wavefront's last block: it still joins their barriers
+    while (s_cur < nsites - 1) enter(++s_cur);
   }
 
   int tid_e = tid;
   asm volatile("" : "+v"(tid_e));
   const int lane_e = tid_e & 63;
-  if (S.head_site >= 0) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const uint64_t other = __shfl_xor(best, o);
-      best = other > best ? other : best;
-    }
-    if (!ctrl && lane_e == 0) L.keys[wave] = best;
-    lds_barrier();
-    if (tid_e == 0) {
-      uint64_t kmax = L.keys[0];
-      for (int w = 1; w < kCW; ++w) kmax = L.keys[w] > kmax ? L.keys[w] : kmax;
-      S.partials[r] = kmax;
-    }
+  lds_barrier();
+  if (ctrl && lane_e == 0) {
+    const int32_t e = lds_read_i32(&L.err);
+    if (e) atomicOr(S.err, e);
+    if (S.head_site >= 0) S.partials[r] = L.best;
   }
   if (S.trace && r == 0 && ctrl && lane_e == 0) S.trace[nsites] = wall_clock64();
 }

@@ -299,6 +299,12 @@ class Plan:
     def set_mode(self, mode):
         N.check(N.lib().w4a8_plan_set_mode(self.h, int(mode)), "plan_set_mode")
 
+    def set_fences(self, fences):
+        """Persistent mode: FENCE_ALL (every site waits for all earlier ones)
+        or FENCE_AUTO (only where a site shares a buffer with an earlier
+        one); results are the same either way."""
+        N.check(N.lib().w4a8_plan_set_fences(self.h, int(fences)), "plan_set_fences")
+
     def run(self):
         N.check(N.lib().w4a8_plan_run(self.h), "plan_run")
 

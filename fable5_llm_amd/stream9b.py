@@ -166,7 +166,7 @@ class Stream9B:
     """All 249 matrices resident on one device with their inputs and
     outputs, wired into one Plan (site order kept)."""
 
-    def __init__(self, ctx, seed=0, sites=None, mode=N.PLAN_PERSISTENT):
+    def __init__(self, ctx, seed=0, sites=None, mode=N.PLAN_PERSISTENT, fences=N.FENCE_ALL):
         import torch
         from .engine import Plan
         self.ctx = ctx
@@ -215,6 +215,7 @@ class Stream9B:
             self.x8.append(x8)
         torch.cuda.synchronize(dev)
         self.plan.set_mode(mode)
+        self.plan.set_fences(fences)
         self.bytes = self.plan.bytes
 
     def run(self):
