@@ -819,6 +819,7 @@ static void plan_fences(const w4a8_plan *p, std::vector<GemvParams> &sites) {
       f = ranges_meet(rd[i], wr[j]) || ranges_meet(wr[i], rd[j]) || ranges_meet(wr[i], wr[j]);
     sites[i].fence = f ? 1 : 0;
     if (f) last = i;
+    sites[i].fence_at = last;
   }
 }
 

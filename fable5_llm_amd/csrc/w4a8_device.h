@@ -198,6 +198,30 @@ __device__ __forceinline__ bool lds_wait_ge(const int32_t *p, int32_t v) {
   return false;
 }
 
+// A barrier of wavefronts w0 .. w0+NW-1 only, in LDS: each posts its phase
+// and polls the others', so wavefronts outside the group -- stalled behind
+// their own weight loads -- are never waited for.  ok turns false if a poll
+// gave up.
+template <int NW>
+struct GroupSync {
+  int32_t *flags;   // NW LDS words, zero before the first phase
+  int w0;
+  int phase;
+  bool ok;
+  __device__ void operator()() {
+    const int lane = threadIdx.x & 63, wave = (threadIdx.x >> 6) - w0;
+    ++phase;
+    wait_lds();
+    if (lane == 0) lds_write_i32(flags + wave, phase);
+    bool done = false;
+    for (uint32_t n = 0; n < kLdsSpin && !done; ++n) {
+      done = __all(lds_read_i32(flags + lane % NW) >= phase);
+      if (!done) __builtin_amdgcn_s_sleep(1);
+    }
+    ok = ok && done;
+  }
+};
+
 // One scale block (8 groups, fewer in the last block) of one tile, as held
 // by one lane: its 16-byte scale row and 8 weight pieces of 32 weights.
 struct BlockRegs {

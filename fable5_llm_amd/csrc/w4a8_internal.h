@@ -110,6 +110,7 @@ struct GemvParams {
   int32_t tile_rot;         // persistent stream: first tile of WG r is (r + tile_rot) % G
   int32_t fence;            // persistent stream: every earlier site completes on all
                             // workgroups before this one reads its activations
+  int32_t fence_at;         // persistent stream: the last fenced site <= this one (0: none)
   int8_t *x8_out;           // optional (written by workgroup 0)
   int32_t *e_x_out;         // optional
   int16_t *xn_out;          // optional RMSNorm output

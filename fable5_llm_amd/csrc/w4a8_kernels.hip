@@ -86,30 +86,6 @@ struct WgSync {
   __device__ void operator()() const { __syncthreads(); }
 };
 
-// A barrier of wavefronts w0 .. w0+NW-1 only, in LDS: each posts its phase
-// and polls the others', so wavefronts outside the group -- stalled behind
-// their own weight loads -- are never waited for.  ok turns false if a poll
-// gave up.
-template <int NW>
-struct GroupSync {
-  int32_t *flags;   // NW LDS words, zero before the first phase
-  int w0;
-  int phase;
-  bool ok;
-  __device__ void operator()() {
-    const int lane = threadIdx.x & 63, wave = (threadIdx.x >> 6) - w0;
-    ++phase;
-    wait_lds();
-    if (lane == 0) lds_write_i32(flags + wave, phase);
-    bool done = false;
-    for (uint32_t n = 0; n < kLdsSpin && !done; ++n) {
-      done = __all(lds_read_i32(flags + lane % NW) >= phase);
-      if (!done) __builtin_amdgcn_s_sleep(1);
-    }
-    ok = ok && done;
-  }
-};
-
 // sm: 2 * NT / 64 int64 of LDS.  Leaves x8 in xs[0, K) and the offset
 // corrections -8 * (sum of the x8 met by the offset-form low nibbles of
 // each (group, k-quarter)) in xlo; returns e_x.  sync() is a barrier of the

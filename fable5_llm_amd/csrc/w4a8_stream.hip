@@ -1,99 +1,98 @@
 // Persistent decode-step kernel (W4A8_PLAN_PERSISTENT) for gfx950.
 //
-// One cooperative launch runs every site of a plan in order, one workgroup
-// per CU: 8 weight wavefronts and 1 control wavefront.
+// One cooperative launch runs every site of a plan, one workgroup per CU of
+// 12 wavefronts with three roles, which meet only through LDS flags -- no
+// workgroup barrier while the plan runs:
 //
-//  * Weight wavefronts stream the weights and do the dot products.  The
+//  * 8 weight wavefronts stream the weights and do the dot products.  The
 //    weight blocks this CU owns over the whole plan form one fixed sequence
 //    (its tiles of site 0, then of site 1, ...; 8448-byte scale blocks
 //    within a tile), dealt round-robin to the 8 wavefronts.  Each wavefront
 //    holds its next two blocks in two register sets, A and B, and refills a
 //    set as soon as it has consumed it -- also when the next block belongs
-//    to a later site, since weights never depend on an activation.  So the
-//    next site's blocks stream while the workgroup waits for the rest of the
-//    GPU and computes the next prologue.
-//  * A weight wavefront makes no global access but its weight loads, and
-//    every refill is the same 9 buffer loads (out of range, so without a
-//    memory access, past the end of the sequence).  The compiler's count of
-//    a wavefront's outstanding loads is therefore exact on every path, and
-//    the wait for one register set never waits for the other.  Outputs,
-//    error bits and the exported prologue vectors go through LDS.
-//  * A tile's 16 rows are complete when every wavefront holding one of its
-//    blocks has added its partial sums into an LDS slot; the wavefront that
-//    completes the count rounds, checks and applies the epilogue, then
-//    stages the outputs.  No workgroup barrier per tile.
-//  * The control wavefront does every other global access: it stores the
-//    staged outputs, signals this workgroup's completion of a site, waits for
-//    all workgroups (one flag per workgroup), and copies the next site's
-//    activation vector (and RMSNorm weights) into LDS.
+//    to a later site, since weights never depend on an activation.  Every
+//    refill is the same 9 buffer loads (out of range, so without a memory
+//    access, past the end of the sequence), and a weight wavefront makes no
+//    other global access, so the compiler's count of its outstanding loads
+//    is exact on every path and the wait for one set never waits for the
+//    other.  At its first block of a site it waits only for that site's
+//    activations (an LDS flag), never for the other wavefronts.
+//  * 3 prologue wavefronts compute each site's activations (RMSNorm, DYNQ8:
+//    x8, e_x and the offset corrections) ahead of the weight wavefronts,
+//    into a ring of 6 LDS buffers; a buffer is reused once every weight
+//    wavefront has moved past the site that used it.
+//  * 1 control wavefront stores the outputs, which the wavefront completing
+//    a tile stages in LDS, and at a fenced site waits until every workgroup
+//    has stored its outputs of all earlier sites (one flag per workgroup)
+//    before the prologue wavefronts may read that site's activations.
 //
-// The LDS flags and the workgroup barriers are inline assembly: the
-// compiler's own forms make a wavefront wait for all of its outstanding
-// loads (vmcnt(0)), which would drain the register pipeline.  The data
-// crossing a site boundary (outputs, activation vectors, flags) moves with
-// agent-coherent accesses (sc1), so no cache-wide writeback or invalidation
-// is needed.  Every result is bit-exact with the reference's integer law
-// (ref/w4a8_ref.py:254-289 and the epilogues of gen_layer_script.py:1397-1433,
-// seq_model.py:1027-1050).
+// A tile's 16 rows are complete when every weight wavefront holding one of
+// its blocks has added its partial sums into an LDS slot; the wavefront
+// that completes the count rounds, checks and applies the epilogue.  The LDS
+// flags are inline assembly (the compiler's own LDS synchronisation makes a
+// wavefront wait for all of its outstanding loads).  Data crossing a site
+// boundary (outputs, activation vectors, flags) moves with agent-coherent
+// accesses (sc1), so no cache-wide writeback or invalidation is needed.
+// Every result is bit-exact with the reference's integer law
+// (ref/w4a8_ref.py:254-289, fixedpoint.py:24-75, layer_fixed.py:1242-1278
+// and the epilogues of gen_layer_script.py:1397-1433, seq_model.py:1027-1050).
 #include "w4a8_device.h"
 
 namespace w4a8 {
 
 namespace {
 
-constexpr int kCW = 8;                      // weight wavefronts
-constexpr int kCtrl = kCW;                  // index of the control wavefront
-constexpr int kThreads = (kCW + 1) * 64;    // 576
-constexpr int kWThreads = kCW * 64;         // 512 threads run the prologue
-constexpr int kPiece = kWThreads * 8;       // 4096 elements per prologue piece
-constexpr int kXPieces = (kKMax + kPiece - 1) / kPiece;   // 3
-constexpr int kXBytes = 2 * kKMax;          // x16 (24 KiB) / x8 + corrections
+constexpr int kCW = 8;                      // weight wavefronts 0..7
+constexpr int kCtrl = kCW;                  // the control wavefront
+constexpr int kPW = 3;                      // prologue wavefronts
+constexpr int kPW0 = kCW + 1;               // ... 9..11
+constexpr int kThreads = (kPW0 + kPW) * 64; // 768
+constexpr int kNB = 6;                      // activation buffers
 constexpr int kXloOff = kKMax;              // int32 corrections after x8
-constexpr int kNormOff = 16384;             // RMSNorm weights (K <= 4096)
-constexpr int kTSlots = 8;                  // tiles being reduced at once
+constexpr int kXB = kKMax + kKMax / 8;      // x8 + corrections of one site
+constexpr int kTSlots = 32;                 // tiles being reduced at once
+constexpr int kChunk = 64 * 8;              // int16 elements per prologue chunk
+constexpr int kPC = (kKMax / kChunk + kPW - 1) / kPW;             // chunks per wavefront
+constexpr int kPN = (kStreamNormKMax / kChunk + kPW - 1) / kPW;   // RMSNorm chunks
+constexpr int kPX = (kKMax / 1024 + kPW - 1) / kPW;               // int8 chunks (1 KiB)
 constexpr uint32_t kGridSpin = 1u << 18;    // polls before a grid wait gives up
 constexpr int kBufDword3 = 0x00020000;      // raw buffer, 32-bit data format
+constexpr int kAuxSc1 = 16;                 // buffer-load cache policy: agent-coherent
 
-static_assert(kPiece % 32 == 0, "a DPP quad of threads covers one (group, quarter)");
-static_assert(kStreamNormKMax <= kPiece, "RMSNorm takes one piece per thread");
-static_assert(kNormOff + 2 * kStreamNormKMax <= kXBytes, "norm weights fit");
-static_assert(kXloOff + 4 * kKMax / 32 <= kNormOff, "corrections fit");
+static_assert(kKMax % kChunk == 0 && kStreamNormKMax % kChunk == 0, "whole chunks");
+static_assert((kTSlots & (kTSlots - 1)) == 0, "slot index is a mask");
+static_assert(kXB % 16 == 0, "buffers stay 16-byte aligned");
 
 // The site table is read-only for the whole launch.  Read through the
 // constant address space, every (uniform) field load is a scalar load, also
-// after barriers, so weight wavefronts never issue a vector load of their
+// after LDS waits, so weight wavefronts never issue a vector load of their
 // own besides the weight loads.
 typedef const __attribute__((address_space(4))) GemvParams CSite;
 typedef const __attribute__((address_space(4))) GemvJob CJob;
 
 struct __align__(16) Lds {
-  int8_t x[2][kXBytes];             // activations of site s in x[s & 1]
-  int16_t xn[kStreamNormKMax];      // the site's RMSNorm output (workgroup 0 exports it)
+  int8_t x[kNB][kXB];               // x8 and corrections of site s in x[s % kNB]
   int64_t tv[kTSlots][kTileRows];   // partial sums, then staged outputs
   int32_t tcnt[kTSlots];            // contributions added to the slot
   int32_t tgen[kTSlots];            // tile number the slot is open for
   int32_t tready[kTSlots];          // tile number + 1 once its outputs are staged
+  int32_t ready[kNB];               // site whose activations are in the buffer (-1: none)
+  int32_t ex[kNB];                  // ... and its e_x
+  int32_t wsite[kCW];               // site each weight wavefront works on (nsites: done)
+  int32_t gridok;                   // last fenced site whose grid-wide wait has passed
+  int32_t psync[kPW];               // prologue wavefronts' barrier phases
   int32_t abort;                    // set by the first LDS wait that gives up
-  int32_t err;                      // error bits found by the weight wavefronts
+  int32_t err;                      // error bits found inside the workgroup
   uint16_t rsqrt[512];
   uint16_t sig[264];
-  int64_t part[2][kCW];             // prologue partial reductions
+  int64_t pss[kPW];                 // prologue partial sums of squares
+  int32_t pmx[kPW];                 // prologue partial maxima
   uint64_t best;                    // argmax key of the head's rows seen here (0: none)
 };
 
 // ---------------------------------------------------------------------------
-// copies into LDS (control wavefront) and LDS synchronisation
+// LDS synchronisation
 // ---------------------------------------------------------------------------
-// lane l copies 16 bytes from src (its own address) to LDS lds_base + 16 * l;
-// lds_base must be uniform
-__device__ __forceinline__ void copy16_sc1(const void *src, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off sc1"
-               :: "v"(src), "s"(lds_base) : "memory", "m0");
-}
-__device__ __forceinline__ void copy16(const void *src, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
-               :: "v"(src), "s"(lds_base) : "memory", "m0");
-}
 __device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 __device__ __forceinline__ void lds_add_u64(int64_t *p, int64_t v) {
@@ -218,136 +217,6 @@ __device__ __forceinline__ void issue_block(BlockRegs &R, CSite *sites, int nsit
   }
 }
 
-// ------------------------------------------------------------- prologue
-// The site's activation vector is in LDS buffer xb (int16 x at xb[0, 2K),
-// int8 x at xb[0, K) for PRO_X8; RMSNorm weights at xb[kNormOff, +2K)).
-// Leaves x8 at xb[0, K) and the offset corrections at xb[kXloOff] (and, in
-// workgroup 0 when the site exports it, the RMSNorm output at L.xn); returns
-// e_x.  All 9 wavefronts call it (the same barriers); the control wavefront
-// computes nothing.
-__device__ int stream_prologue(CSite &P, Lds &L, int8_t *xb, int tid, bool ctrl) {
-  const int K = P.K;
-  const int lane = tid & 63, wave = tid >> 6;
-  int32_t *xlo = (int32_t *)(xb + kXloOff);
-  if (P.pro == PRO_X8) {
-    if (!ctrl) {
-      for (int c = tid; c < P.NG * 4; c += kWThreads) {
-        const int *xw = (const int *)(xb + 32 * c);
-        int s = 0;
-        s = __builtin_amdgcn_sdot4(xw[0], 0x01010101, s, false);
-        s = __builtin_amdgcn_sdot4(xw[2], 0x01010101, s, false);
-        s = __builtin_amdgcn_sdot4(xw[4], 0x01010101, s, false);
-        s = __builtin_amdgcn_sdot4(xw[6], 0x01010101, s, false);
-        xlo[c] = -8 * s;
-      }
-    }
-    lds_barrier();
-    return P.e_x_given;
-  }
-  const int np = (K + kPiece - 1) / kPiece;
-  int4 pc[kXPieces];
-#pragma unroll
-  for (int c = 0; c < kXPieces; ++c) {
-    const int base = c * kPiece + tid * 8;
-    pc[c] = make_int4(0, 0, 0, 0);
-    if (!ctrl && c < np && base < K) pc[c] = *(const int4 *)(xb + 2 * base);
-  }
-  if (P.pro == PRO_RMSNORM_DYNQ8) {
-    // layer_fixed.py:1262-1278 in sign-magnitude form (rshift_round rounds
-    // the magnitude); K <= kStreamNormKMax, so one piece per thread
-    const int base = tid * 8;
-    int4 wv = make_int4(0, 0, 0, 0);
-    if (!ctrl && base < K) wv = *(const int4 *)(xb + kNormOff + 2 * base);
-    uint64_t ss = 0;
-#pragma unroll
-    for (int j = 0; j < 8; j += 2) {
-      const int32_t a = piece_get(pc[0], j), b = piece_get(pc[0], j + 1);
-      ss += (uint64_t)((uint32_t)(a * a) + (uint32_t)(b * b));
-    }
-    ss = wave_sum_u64(ss);
-    if (!ctrl && lane == 0) L.part[0][wave] = (int64_t)ss;
-    lds_barrier();
-    ss = 0;
-#pragma unroll
-    for (int w = 0; w < kCW; ++w) ss += (uint64_t)L.part[0][w];
-    if (ss == 0) ss = 1;
-    int64_t r;
-    int e;
-    rsqrt_q(ss, 2 * P.in_f + (31 - __clz(K)), L.rsqrt, &r, &e);
-    const int s1 = 30 - e;
-    const int32_t one = P.one_plus ? (1 << 14) : 0;
-    const int rs = s1 < 0 ? 0 : (s1 > 63 ? 63 : s1);
-    const int ls = s1 < 0 ? (-s1 > 63 ? 63 : -s1) : 0;
-    const uint64_t half1 = rs > 0 ? ((uint64_t)1 << (rs - 1)) : 0;
-    const bool right = s1 >= 0;
-    // r < 2^31 (a Q30 reciprocal square root), |x| <= 2^15; for in_f within
-    // 0..40 (checked on the host) the left shift is at most 17, so |x| * r
-    // shifted stays below 2^63
-    const uint32_t r32 = (uint32_t)r;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int32_t xv = piece_get(pc[0], j);
-      const int32_t sc = (int32_t)piece_get(wv, j) + one;
-      const uint64_t mag = (uint64_t)(uint32_t)abs(xv) * (uint64_t)r32;
-      uint64_t ym = right ? ((mag + half1) >> rs) : (mag << ls);
-      // y is clipped to [-2^32, 2^32 - 1]; a magnitude of 2^32 or more
-      // saturates the int16 result below for any nonzero scale, exactly as
-      // 2^32 - 1 does, so the product can be formed in 32 x 32 bits
-      ym = ym < 0xFFFFFFFFull ? ym : 0xFFFFFFFFull;
-      const uint64_t q = ((uint64_t)(uint32_t)ym * (uint64_t)(uint32_t)abs(sc) + 8192u) >> 14;
-      const bool neg = (xv < 0) != (sc < 0);
-      const int32_t q32 = q > 65535u ? 65535 : (int32_t)q;
-      const int32_t qm = min(q32, 32767 + (int32_t)neg);
-      piece_set(pc[0], j, (int16_t)(neg ? -qm : qm));
-    }
-    if (!ctrl && blockIdx.x == 0 && P.xn_out && base < K) *(int4 *)(L.xn + base) = pc[0];
-  }
-  int32_t mx = 0;
-#pragma unroll
-  for (int c = 0; c < kXPieces; ++c)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) mx = max(mx, abs((int32_t)piece_get(pc[c], j)));
-  mx = wave_max_i32(mx);
-  if (!ctrl && lane == 0) L.part[1][wave] = mx;
-  lds_barrier();
-  mx = 0;
-#pragma unroll
-  for (int w = 0; w < kCW; ++w) mx = max(mx, (int32_t)L.part[1][w]);
-  // fixedpoint.py:24-33: the least e with rshift_round(max, e) <= 127 is
-  // bitlen(max) - 7, or one more when rounding carries past 127
-  int e = mx > 127 ? 25 - __clz(mx) : 0;
-  if (e > 0 && ((mx + (1 << (e - 1))) >> e) > 127) ++e;
-  const int32_t half = (1 << e) >> 1;
-  if (!ctrl) {
-#pragma unroll
-    for (int c = 0; c < kXPieces; ++c) {
-      const int base = c * kPiece + tid * 8;
-      if (c < np) {
-        uint32_t lo = 0, hi = 0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int32_t v = piece_get(pc[c], j);
-          const int32_t qm = min((abs(v) + half) >> e, 127);
-          const uint32_t b8 = (uint32_t)(uint8_t)(int8_t)(v < 0 ? -qm : qm);
-          if (j < 4) lo |= b8 << (8 * j);
-          else       hi |= b8 << (8 * (j - 4));
-        }
-        // -8 * sum of the x8 met by the offset-form low nibbles of one
-        // (group, quarter): 32 consecutive k = the 4 threads of a DPP quad
-        int t4 = __builtin_amdgcn_sdot4((int)lo, 0x01010101, 0, false);
-        t4 += __builtin_amdgcn_update_dpp(0, t4, 0xB1, 0xF, 0xF, false);
-        t4 += __builtin_amdgcn_update_dpp(0, t4, 0x4E, 0xF, 0xF, false);
-        if (base < K) {
-          *(uint2 *)(xb + base) = make_uint2(lo, hi);
-          if ((tid & 3) == 0) xlo[base / 32] = -8 * t4;
-        }
-      }
-    }
-  }
-  lds_barrier();
-  return e;
-}
-
 // ------------------------------------------------------------- tiles
 // Add this wavefront's share of tile kt; true if it completed the tile.
 __device__ __forceinline__ bool tile_add(Lds &L, int kt, int64_t p, int contributors,
@@ -407,45 +276,6 @@ __device__ __forceinline__ void tile_epilogue(Lds &L, int kt, CJob &J, int tl, i
 }
 
 // ------------------------------------------------------------- control
-// start copying the site's activation vector (agent-coherent) and RMSNorm
-// weights into LDS buffer xb; the caller waits (vmcnt) before the barrier
-// that hands the buffer to the weight wavefronts
-__device__ __forceinline__ void ctrl_issue_inputs(CSite &P, int8_t *xb, int lane) {
-  const uint8_t *x = (const uint8_t *)P.x;
-  const int nb = P.pro == PRO_X8 ? P.K : 2 * P.K;
-  for (int off = 0; off < nb; off += 1024)
-    if (off + 16 * lane < nb) copy16_sc1(x + off + 16 * lane, lds_off(xb + off));
-  if (P.pro == PRO_RMSNORM_DYNQ8) {
-    const uint8_t *w = (const uint8_t *)P.norm_w;
-    for (int off = 0; off < 2 * P.K; off += 1024)
-      if (off + 16 * lane < 2 * P.K) copy16(w + off + 16 * lane, lds_off(xb + kNormOff + off));
-  }
-}
-
-// workgroup 0: the prologue's exported vectors (x8, the RMSNorm output, e_x)
-__device__ void ctrl_export(CSite &P, Lds &L, const int8_t *xb, int e_x, int lane) {
-  const int K = P.K;
-  if (P.x8_out)
-    for (int off = 16 * lane; off < K; off += 1024) {
-      const int4 v = *(const int4 *)(xb + off);
-      int32_t *o = (int32_t *)(P.x8_out + off);
-      store_coherent(o, v.x);
-      store_coherent(o + 1, v.y);
-      store_coherent(o + 2, v.z);
-      store_coherent(o + 3, v.w);
-    }
-  if (P.pro == PRO_RMSNORM_DYNQ8 && P.xn_out)
-    for (int i = 8 * lane; i < K; i += 512) {
-      const int4 v = *(const int4 *)(L.xn + i);
-      int32_t *o = (int32_t *)(P.xn_out + i);
-      store_coherent(o, v.x);
-      store_coherent(o + 1, v.y);
-      store_coherent(o + 2, v.z);
-      store_coherent(o + 3, v.w);
-    }
-  if (P.e_x_out && lane == 0) store_coherent(P.e_x_out, (int32_t)e_x);
-}
-
 // Store the outputs of this CU's tiles of site P (tile numbers kt0, ...).
 // Argmax tiles stage nothing: their slot is freed by the wavefront that
 // completes them, which is waited for here too, so that no wavefront still
@@ -497,17 +327,175 @@ __device__ void grid_wait(uint32_t *flags, int G, uint32_t v, int lane, int32_t 
   }
 }
 
+
+// ------------------------------------------------------------- prologue
+// One 16-byte piece of a vector through a buffer whose range ends with the
+// vector: lanes past it read zero.  Agent-coherent, since an earlier site on
+// another CU may have written it.
+__device__ __forceinline__ int4 vec_load(__amdgpu_buffer_rsrc_t rs, int off) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kAuxSc1);
+  return make_int4((int)v.x, (int)v.y, (int)v.z, (int)v.w);
+}
+
+// The prologue of site P by the 3 prologue wavefronts (pw = 0..2; sync is
+// their barrier): x8 and the offset corrections into buffer xb, the exports
+// of workgroup 0 (x8, e_x, the RMSNorm output); returns e_x.  Prologue
+// wavefront pw takes the 512-element chunks g = pw, pw + 3, ... of x; lane l
+// of a chunk holds its elements 8l..8l+7, so the 4 lanes of a DPP quad hold
+// 32 consecutive elements -- one (group, k-quarter) of the weight layout.
+__device__ int group_prologue(CSite &P, Lds &L, int8_t *xb, int pw, int lane,
+                              GroupSync<kPW> &sync) {
+  const int K = P.K;
+  const bool exp = blockIdx.x == 0;
+  int32_t *xlo = (int32_t *)(xb + kXloOff);
+  if (P.pro == PRO_X8) {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)P.x, (short)0, K, kBufDword3);
+#pragma unroll
+    for (int c = 0; c < kPX; ++c) {
+      const int off = (c * kPW + pw) * 1024 + lane * 16;
+      const int4 v = vec_load(rs, off);
+      // -8 * sum of the x8 met by the offset-form low nibbles of a 32-byte
+      // (group, quarter): bytes 0-3 and 8-11 of each lane's 16, lane pairs
+      int t = __builtin_amdgcn_sdot4(v.x, 0x01010101, 0, false);
+      t = __builtin_amdgcn_sdot4(v.z, 0x01010101, t, false);
+      t += __builtin_amdgcn_update_dpp(0, t, 0xB1, 0xF, 0xF, false);
+      if (off < K) {
+        *(int4 *)(xb + off) = v;
+        if ((lane & 1) == 0) xlo[off / 32] = -8 * t;
+        if (exp && P.x8_out) *(int4 *)(P.x8_out + off) = v;
+      }
+    }
+    if (exp && P.e_x_out && pw == 0 && lane == 0) *P.e_x_out = P.e_x_given;
+    return P.e_x_given;
+  }
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc((void *)P.x, (short)0, 2 * K, kBufDword3);
+  int4 pc[kPC];
+#pragma unroll
+  for (int c = 0; c < kPC; ++c) pc[c] = vec_load(rx, ((c * kPW + pw) * kChunk + lane * 8) * 2);
+  if (P.pro == PRO_RMSNORM_DYNQ8) {
+    // layer_fixed.py:1262-1278 in sign-magnitude form (rshift_round rounds
+    // the magnitude); K <= kStreamNormKMax
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc((void *)P.norm_w, (short)0, 2 * K, kBufDword3);
+    int4 wv[kPN];
+#pragma unroll
+    for (int c = 0; c < kPN; ++c) wv[c] = vec_load(rw, ((c * kPW + pw) * kChunk + lane * 8) * 2);
+    uint64_t ss = 0;
+#pragma unroll
+    for (int c = 0; c < kPN; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        const int32_t a = piece_get(pc[c], j), b = piece_get(pc[c], j + 1);
+        ss += (uint64_t)((uint32_t)(a * a) + (uint32_t)(b * b));
+      }
+    ss = wave_sum_u64(ss);
+    if (lane == 0) L.pss[pw] = (int64_t)ss;
+    sync();
+    ss = 0;
+#pragma unroll
+    for (int w = 0; w < kPW; ++w) ss += (uint64_t)L.pss[w];
+    if (ss == 0) ss = 1;
+    int64_t r;
+    int e;
+    rsqrt_q(ss, 2 * P.in_f + (31 - __clz(K)), L.rsqrt, &r, &e);
+    const int s1 = 30 - e;
+    const int32_t one = P.one_plus ? (1 << 14) : 0;
+    const int rs = s1 < 0 ? 0 : (s1 > 63 ? 63 : s1);
+    const int ls = s1 < 0 ? (-s1 > 63 ? 63 : -s1) : 0;
+    const uint64_t half1 = rs > 0 ? ((uint64_t)1 << (rs - 1)) : 0;
+    const bool right = s1 >= 0;
+    // r < 2^31 (a Q30 reciprocal square root), |x| <= 2^15; for in_f within
+    // 0..40 (checked on the host) the left shift is at most 17, so |x| * r
+    // shifted stays below 2^63
+    const uint32_t r32 = (uint32_t)r;
+#pragma unroll
+    for (int c = 0; c < kPN; ++c) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int32_t xv = piece_get(pc[c], j);
+        const int32_t sc = (int32_t)piece_get(wv[c], j) + one;
+        const uint64_t mag = (uint64_t)(uint32_t)abs(xv) * (uint64_t)r32;
+        uint64_t ym = right ? ((mag + half1) >> rs) : (mag << ls);
+        // y is clipped to [-2^32, 2^32 - 1]; a magnitude of 2^32 or more
+        // saturates the int16 result below for any nonzero scale, exactly as
+        // 2^32 - 1 does, so the product can be formed in 32 x 32 bits
+        ym = ym < 0xFFFFFFFFull ? ym : 0xFFFFFFFFull;
+        const uint64_t q = ((uint64_t)(uint32_t)ym * (uint64_t)(uint32_t)abs(sc) + 8192u) >> 14;
+        const bool neg = (xv < 0) != (sc < 0);
+        const int32_t q32 = q > 65535u ? 65535 : (int32_t)q;
+        const int32_t qm = min(q32, 32767 + (int32_t)neg);
+        piece_set(pc[c], j, (int16_t)(neg ? -qm : qm));
+      }
+      const int base = (c * kPW + pw) * kChunk + lane * 8;
+      if (exp && P.xn_out && base < K) *(int4 *)(P.xn_out + base) = pc[c];
+    }
+  }
+  int32_t mx = 0;
+#pragma unroll
+  for (int c = 0; c < kPC; ++c)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mx = max(mx, abs((int32_t)piece_get(pc[c], j)));
+  mx = wave_max_i32(mx);
+  if (lane == 0) L.pmx[pw] = mx;
+  sync();
+  mx = 0;
+#pragma unroll
+  for (int w = 0; w < kPW; ++w) mx = max(mx, L.pmx[w]);
+  // fixedpoint.py:24-33: the least e with rshift_round(max, e) <= 127 is
+  // bitlen(max) - 7, or one more when rounding carries past 127
+  int e = mx > 127 ? 25 - __clz(mx) : 0;
+  if (e > 0 && ((mx + (1 << (e - 1))) >> e) > 127) ++e;
+  const int32_t half = (1 << e) >> 1;
+#pragma unroll
+  for (int c = 0; c < kPC; ++c) {
+    const int base = (c * kPW + pw) * kChunk + lane * 8;
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int32_t v = piece_get(pc[c], j);
+      const int32_t qm = min((abs(v) + half) >> e, 127);
+      const uint32_t b8 = (uint32_t)(uint8_t)(int8_t)(v < 0 ? -qm : qm);
+      if (j < 4) lo |= b8 << (8 * j);
+      else       hi |= b8 << (8 * (j - 4));
+    }
+    // -8 * sum of the x8 met by the offset-form low nibbles of one
+    // (group, quarter): 32 consecutive elements = the 4 lanes of a DPP quad
+    int t4 = __builtin_amdgcn_sdot4((int)lo, 0x01010101, 0, false);
+    t4 += __builtin_amdgcn_update_dpp(0, t4, 0xB1, 0xF, 0xF, false);
+    t4 += __builtin_amdgcn_update_dpp(0, t4, 0x4E, 0xF, 0xF, false);
+    if (base < K) {
+      *(uint2 *)(xb + base) = make_uint2(lo, hi);
+      if ((lane & 3) == 0) xlo[base / 32] = -8 * t4;
+      if (exp && P.x8_out) *(uint2 *)(P.x8_out + base) = make_uint2(lo, hi);
+    }
+  }
+  if (exp && P.e_x_out && pw == 0 && lane == 0) *P.e_x_out = e;
+  return e;
+}
+
+// the wavefront waits until every weight wavefront has moved past site t
+__device__ __forceinline__ bool wait_weights_past(Lds &L, int t, int lane) {
+  for (uint32_t n = 0; n < kLdsSpin; ++n) {
+    if (__all(lds_read_i32(&L.wsite[lane & (kCW - 1)]) > t)) return true;
+    if (lds_read_i32(&L.abort) != 0) return false;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return false;
+}
+
+
 __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
                                                           const GemvParams *__restrict__ sites_arg) {
   CSite *sites = (CSite *)sites_arg;
   __shared__ Lds L;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool ctrl = wave == kCtrl;
   const int G = gridDim.x, r = blockIdx.x;
   const int nsites = S.nsites;
 
-  // tables and reduction slots
+  // tables, reduction slots and flags
   const int32_t *tab = sites[0].tables;
   for (int i = tid; i < 512; i += kThreads) L.rsqrt[i] = (uint16_t)tab[kRsqrtOff + i];
   for (int i = tid; i < 257; i += kThreads) L.sig[i] = (uint16_t)tab[kSigmoidOff + i];
@@ -517,47 +505,54 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
     L.tgen[tid] = tid;
     L.tready[tid] = 0;
   }
+  if (tid < kNB) L.ready[tid] = -1;
+  if (tid < kCW) L.wsite[tid] = 0;
+  if (tid < kPW) L.psync[tid] = 0;
   if (tid == 0) {
+    L.gridok = 0;
     L.abort = 0;
     L.err = 0;
     L.best = 0;
   }
   wait_vm_all();   // the table loads, before any weight load is counted
+  lds_barrier();
 
-  if (ctrl) {
-    // Site s's activations go to x[s & 1].  Unless site s+1 is fenced, its
-    // activations are copied into the other buffer while site s computes
-    // (every weight wavefront is past site s-1, the buffer's last user); a
-    // fenced site first waits until every workgroup has stored its outputs
-    // of all earlier sites (flag value s+1), then copies.
+  if (wave == kCtrl) {
+    // outputs of every site in order; at a fenced site, the grid-wide wait
     int kt0 = 0;   // CU-local number of the site's first tile
-    if (nsites > 0) ctrl_issue_inputs(sites[0], L.x[0], lane);
-    wait_vm_all();
     for (int s = 0; s < nsites; ++s) {
       CSite &P = sites[s];
-      int8_t *xb = L.x[s & 1];
-      lds_barrier();   // site s's activation vector is in LDS
       if (S.trace && r == 0 && lane == 0) S.trace[s] = wall_clock64();
-      const bool ahead = s + 1 < nsites && !sites[s + 1].fence;
-      if (ahead) ctrl_issue_inputs(sites[s + 1], L.x[(s + 1) & 1], lane);
-      const int e_x = stream_prologue(P, L, xb, tid, true);
-      if (r == 0) ctrl_export(P, L, xb, e_x, lane);
-      // the next site's activations have landed (this site's output stores,
-      // issued below, are only waited for at a fence)
-      wait_vm_all();
       ctrl_serve(P, L, kt0, r, G, lane);
       {
         const int first = (r + P.tile_rot) % G;
         kt0 += first < P.total_tiles ? (P.total_tiles - 1 - first) / G + 1 : 0;
       }
-      if (s + 1 < nsites && !ahead) {
-        wait_vm_all();   // outputs stored
+      if (s + 1 < nsites && sites[s + 1].fence) {
+        wait_vm_all();   // this workgroup's outputs of sites <= s are stored
         if (lane == 0) store_coherent(S.done + r, (uint32_t)(s + 1));
         grid_wait(S.done, G, (uint32_t)(s + 1), lane, S.err);
-        ctrl_issue_inputs(sites[s + 1], L.x[(s + 1) & 1], lane);
-        wait_vm_all();
+        if (lane == 0) lds_write_i32(&L.gridok, s + 1);
       }
     }
+  } else if (wave >= kPW0) {
+    // prologues, in site order, into the buffer ring
+    const int pw = wave - kPW0;
+    GroupSync<kPW> sync{L.psync, kPW0, 0, true};
+    bool ok = true;
+    for (int s = 0; s < nsites; ++s) {
+      CSite &P = sites[s];
+      const int b = s % kNB;
+      if (s >= kNB) ok = wait_weights_past(L, s - kNB, lane) && ok;
+      if (P.fence_at > 0) ok = lds_wait_ge(&L.gridok, P.fence_at) && ok;
+      const int e = group_prologue(P, L, L.x[b], pw, lane, sync);
+      sync();   // the group's writes into buffer b are complete
+      if (pw == 0 && lane == 0) {
+        lds_write_i32(&L.ex[b], e);
+        lds_write_i32(&L.ready[b], s);
+      }
+    }
+    if (!(ok && sync.ok) && lane == 0) lds_or_i32(&L.err, 4);
   } else {
     // A holds item k of this wavefront's sequence, B item k + 1; cn is the
     // next item to put in flight
@@ -572,27 +567,26 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
     issue_block(B, sites, nsites, G, cb, lane);
     int s_cur = -1, e_x = 0, contributors = 0;
     int64_t p = 0;
-    // join site s's barriers and compute its prologue; the lane-derived
-    // addresses are recomputed from an opaque copy of the thread index, so
-    // the compiler does not keep them all live across the whole plan
-    auto enter = [&](int s) {
-      int tid_s = tid;
-      asm volatile("" : "+v"(tid_s));
-      lds_barrier();   // site s's activation vector is in LDS
-      e_x = stream_prologue(sites[s], L, L.x[s & 1], tid_s, false);
-      contributors = min(sites[s].nblk, kCW);
-    };
     // consume the block in R (item c; this wavefront's next item is nx),
     // refill R with the item two ahead, and add into the tile after this
     // wavefront's last block of it
     auto step = [&](BlockRegs &R, Cursor &c, const Cursor &nx) {
-      while (s_cur < c.s) enter(++s_cur);
+      // the lane-derived addresses are recomputed from an opaque copy of the
+      // thread index, so the compiler does not keep them all live
       int tid_s = tid;
       asm volatile("" : "+v"(tid_s));
       const int lane_s = tid_s & 63;
+      if (c.s != s_cur) {
+        // done with every earlier site; wait for this one's activations
+        s_cur = c.s;
+        lds_write_i32(&L.wsite[wave], s_cur);
+        lds_wait_eq(L, &L.ready[s_cur % kNB], s_cur, lane_s);
+        e_x = __builtin_amdgcn_readfirstlane(lds_read_i32(&L.ex[s_cur % kNB]));
+        contributors = min(sites[s_cur].nblk, kCW);
+      }
       CSite &P = sites[c.s];
       const int i = c.j / c.nblk, b = c.j - i * c.nblk;
-      const int8_t *xb = L.x[c.s & 1];
+      const int8_t *xb = L.x[c.s % kNB];
       p = dot_block(R, groups_in(P.NG, b), b * kGroupsPerBlock, lane_s & 3, xb,
                     (const int32_t *)(xb + kXloOff), p);
       const bool last = !(nx.s == c.s && nx.j / nx.nblk == i);
@@ -616,20 +610,19 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
       if (cb.s >= nsites) break;
       step(B, cb, ca);
     }
-    // sites after this wavefront's last block: it still joins their barriers
-    while (s_cur < nsites - 1) enter(++s_cur);
+    lds_write_i32(&L.wsite[wave], nsites);
   }
 
   int tid_e = tid;
   asm volatile("" : "+v"(tid_e));
   const int lane_e = tid_e & 63;
   lds_barrier();
-  if (ctrl && lane_e == 0) {
+  if (wave == kCtrl && lane_e == 0) {
     const int32_t e = lds_read_i32(&L.err);
     if (e) atomicOr(S.err, e);
     if (S.head_site >= 0) S.partials[r] = L.best;
+    if (S.trace && r == 0) S.trace[nsites] = wall_clock64();
   }
-  if (S.trace && r == 0 && ctrl && lane_e == 0) S.trace[nsites] = wall_clock64();
 }
 
 }  // namespace
