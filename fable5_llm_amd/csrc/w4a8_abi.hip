@@ -750,6 +750,7 @@ struct w4a8_plan {
   // persistent mode
   GemvParams *d_sites = nullptr;
   uint32_t *d_done = nullptr;
+  int8_t *d_stage = nullptr;
   uint64_t *d_pkeys = nullptr;
   int G = 0;
   int head_site = -1;
@@ -759,9 +760,11 @@ struct w4a8_plan {
 static void plan_drop_persistent(w4a8_plan *p) {
   if (p->d_sites) (void)hipFree(p->d_sites);
   if (p->d_done) (void)hipFree(p->d_done);
+  if (p->d_stage) (void)hipFree(p->d_stage);
   if (p->d_pkeys) (void)hipFree(p->d_pkeys);
   p->d_sites = nullptr;
   p->d_done = nullptr;
+  p->d_stage = nullptr;
   p->d_pkeys = nullptr;
   p->G = 0;
 }
@@ -853,7 +856,8 @@ static int plan_build_persistent(w4a8_plan *p) {
   }
   plan_fences(p, sites);
   HIP_TRY(hipMalloc(&p->d_sites, sizeof(GemvParams) * (size_t)n));
-  HIP_TRY(hipMalloc(&p->d_done, sizeof(uint32_t) * stream_counter_words(p->G)));
+  HIP_TRY(hipMalloc(&p->d_done, sizeof(uint32_t) * stream_counter_words(p->G, n)));
+  HIP_TRY(hipMalloc(&p->d_stage, (size_t)kStageBytes * (size_t)n));
   HIP_TRY(hipMalloc(&p->d_pkeys, sizeof(uint64_t) * (size_t)p->G));
   HIP_TRY(hipMemcpy(p->d_sites, sites.data(), sizeof(GemvParams) * (size_t)n,
                     hipMemcpyHostToDevice));
@@ -867,10 +871,12 @@ static int plan_launch_persistent(w4a8_plan *p, hipStream_t s, hipEvent_t e0,
   sp.nsites = (int32_t)p->steps.size();
   sp.head_site = p->head_site;
   sp.done = p->d_done;
+  sp.stage = p->d_stage;
   sp.err = p->ctx->d_err;
   sp.partials = p->d_pkeys;
   sp.trace = trace;
-  HIP_TRY(launch_fill_i32((int32_t *)p->d_done, 0, (int64_t)stream_counter_words(p->G), s));
+  HIP_TRY(launch_fill_i32((int32_t *)p->d_done, 0,
+                          (int64_t)stream_counter_words(p->G, (int)p->steps.size()), s));
   if (e0) HIP_TRY(hipEventRecord(e0, s));
   HIP_TRY(launch_stream(sp, p->G, s));
   if (e1) HIP_TRY(hipEventRecord(e1, s));

@@ -201,8 +201,8 @@ __device__ __forceinline__ bool lds_wait_ge(const int32_t *p, int32_t v) {
 // A barrier of wavefronts w0 .. w0+NW-1 only, in LDS: each posts its phase
 // and polls the others', so wavefronts outside the group -- stalled behind
 // their own weight loads -- are never waited for.  ok turns false if a poll
-// gave up.
-template <int NW>
+// gave up.  kSleep: back off between polls (for groups that wait long).
+template <int NW, bool kSleep = true>
 struct GroupSync {
   int32_t *flags;   // NW LDS words, zero before the first phase
   int w0;
@@ -216,7 +216,7 @@ struct GroupSync {
     bool done = false;
     for (uint32_t n = 0; n < kLdsSpin && !done; ++n) {
       done = __all(lds_read_i32(flags + lane % NW) >= phase);
-      if (!done) __builtin_amdgcn_s_sleep(1);
+      if (!done && kSleep) __builtin_amdgcn_s_sleep(1);
     }
     ok = ok && done;
   }

@@ -138,7 +138,10 @@ struct StreamParams {
   const GemvParams *sites;  // device array, nsites entries
   int32_t nsites;
   int32_t head_site;        // index of the LM-head site, or -1
-  uint32_t *done;           // stream_counter_words(grid) words, zero at launch
+  uint32_t *done;           // stream_counter_words(grid, nsites) words, zero at launch:
+                            // a completion flag per workgroup, then one per site whose
+                            // activations are staged
+  int8_t *stage;            // nsites * kStageBytes: each site's x8, corrections, e_x
   int32_t *err;             // bit 1: a completion wait gave up; bit 2: an LDS wait did
   uint64_t *partials;       // head: one key per workgroup
   uint64_t *trace;          // optional: nsites + 1 wall-clock stamps taken by
@@ -146,8 +149,14 @@ struct StreamParams {
 };
 hipError_t launch_stream(const StreamParams &sp, int grid, hipStream_t s);
 int stream_max_blocks_per_cu();
-// uint32 words of completion flags a grid of `grid` workgroups needs
-size_t stream_counter_words(int grid);
+// uint32 words of flags a grid of `grid` workgroups running nsites sites needs
+size_t stream_counter_words(int grid, int nsites);
+// index of the first site flag
+__host__ __device__ inline size_t stream_flag_site0(int grid) {
+  return (size_t)(grid + 63) / 64 * 64;
+}
+// one site's staged activations: x8[kKMax], int32 corrections[kKMax / 32], e_x
+constexpr int kStageBytes = kKMax + kKMax / 8 + 16;
 
 hipError_t launch_argmax_final(const uint64_t *partials, int n,
                                int32_t *result, hipStream_t s);

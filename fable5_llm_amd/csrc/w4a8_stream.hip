@@ -76,7 +76,8 @@ struct __align__(16) Lds {
   int32_t tcnt[kTSlots];            // contributions added to the slot
   int32_t tgen[kTSlots];            // tile number the slot is open for
   int32_t tready[kTSlots];          // tile number + 1 once its outputs are staged
-  int32_t ready[kNB];               // site whose activations are in the buffer (-1: none)
+  int32_t ready[kNB][kPW];          // per prologue wavefront: the site whose activations it
+                                    // has written into the buffer (-1: none)
   int32_t ex[kNB];                  // ... and its e_x
   int32_t wsite[kCW];               // site each weight wavefront works on (nsites: done)
   int32_t gridok;                   // last fenced site whose grid-wide wait has passed
@@ -94,6 +95,13 @@ struct __align__(16) Lds {
 // LDS synchronisation
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// lane l copies 16 bytes from src (its own address, agent-coherent) to LDS
+// lds_base + 16 * l; lds_base must be uniform
+__device__ __forceinline__ void copy16_sc1(const void *src, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off sc1"
+               :: "v"(src), "s"(lds_base) : "memory", "m0");
+}
 
 __device__ __forceinline__ void lds_add_u64(int64_t *p, int64_t v) {
   asm volatile("ds_add_u64 %0, %1" :: "v"(lds_off(p)), "v"(v) : "memory");
@@ -337,59 +345,87 @@ __device__ __forceinline__ int4 vec_load(__amdgpu_buffer_rsrc_t rs, int off) {
   return make_int4((int)v.x, (int)v.y, (int)v.z, (int)v.w);
 }
 
-// The prologue of site P by the 3 prologue wavefronts (pw = 0..2; sync is
-// their barrier): x8 and the offset corrections into buffer xb, the exports
-// of workgroup 0 (x8, e_x, the RMSNorm output); returns e_x.  Prologue
-// wavefront pw takes the 512-element chunks g = pw, pw + 3, ... of x; lane l
-// of a chunk holds its elements 8l..8l+7, so the 4 lanes of a DPP quad hold
-// 32 consecutive elements -- one (group, k-quarter) of the weight layout.
-__device__ int group_prologue(CSite &P, Lds &L, int8_t *xb, int pw, int lane,
-                              GroupSync<kPW> &sync) {
+// One prologue wavefront's share of a site's inputs, in registers: int16 x
+// in chunks g = pw, pw + 3, ... of 512 elements (lane l holds elements
+// 8l..8l+7 of a chunk, so the 4 lanes of a DPP quad hold 32 consecutive
+// elements -- one (group, k-quarter) of the weight layout), the RMSNorm
+// weights alike; for int8 x (PRO_X8), 1 KiB chunks of 16 bytes per lane.
+struct ProX {
+  int4 pc[kPC];
+  int4 wv[kPN];
+};
+
+// Put site P's inputs for prologue wavefront pw in flight: always the same
+// kPC + kPN buffer loads (out of range where there is nothing to load, or
+// when !real), so a wait for one register set never waits for the other.
+__device__ __forceinline__ void pro_issue(ProX &X, CSite &P, bool real, int pw, int lane) {
   const int K = P.K;
-  const bool exp = blockIdx.x == 0;
-  int32_t *xlo = (int32_t *)(xb + kXloOff);
+  const bool x8 = P.pro == PRO_X8;
+  const int xlen = real ? (x8 ? K : 2 * K) : 0;
+  const int wlen = real && P.pro == PRO_RMSNORM_DYNQ8 ? 2 * K : 0;
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc((void *)P.x, (short)0, xlen, kBufDword3);
+  const __amdgpu_buffer_rsrc_t rw =
+      __builtin_amdgcn_make_buffer_rsrc((void *)P.norm_w, (short)0, wlen, kBufDword3);
+#pragma unroll
+  for (int c = 0; c < kPC; ++c) {
+    const int off = x8 ? (c < kPX ? (c * kPW + pw) * 1024 + lane * 16 : 1 << 30)
+                       : ((c * kPW + pw) * kChunk + lane * 8) * 2;
+    X.pc[c] = vec_load(rx, off);
+  }
+#pragma unroll
+  for (int c = 0; c < kPN; ++c) X.wv[c] = vec_load(rw, ((c * kPW + pw) * kChunk + lane * 8) * 2);
+}
+
+// 8 bytes into the staging area, visible to every CU once waited for
+__device__ __forceinline__ void stage_u64(int8_t *p, uint32_t lo, uint32_t hi) {
+  store_coherent((uint64_t *)p, (uint64_t)lo | ((uint64_t)hi << 32));
+}
+
+// The prologue of site P by the 3 prologue wavefronts (pw = 0..2; sync is
+// their barrier) from the inputs in X: x8 and the offset corrections into
+// the site's staging area stg (agent-coherent stores), and the site's
+// exports (x8, e_x, the RMSNorm output); returns e_x.  Chunks past K are
+// skipped.
+__device__ int group_prologue(CSite &P, Lds &L, int8_t *stg, int pw, int lane,
+                              GroupSync<kPW, false> &sync, ProX &X) {
+  const int K = P.K;
+  int32_t *xlo = (int32_t *)(stg + kXloOff);
   if (P.pro == PRO_X8) {
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc((void *)P.x, (short)0, K, kBufDword3);
 #pragma unroll
     for (int c = 0; c < kPX; ++c) {
       const int off = (c * kPW + pw) * 1024 + lane * 16;
-      const int4 v = vec_load(rs, off);
-      // -8 * sum of the x8 met by the offset-form low nibbles of a 32-byte
-      // (group, quarter): bytes 0-3 and 8-11 of each lane's 16, lane pairs
-      int t = __builtin_amdgcn_sdot4(v.x, 0x01010101, 0, false);
-      t = __builtin_amdgcn_sdot4(v.z, 0x01010101, t, false);
-      t += __builtin_amdgcn_update_dpp(0, t, 0xB1, 0xF, 0xF, false);
-      if (off < K) {
-        *(int4 *)(xb + off) = v;
-        if ((lane & 1) == 0) xlo[off / 32] = -8 * t;
-        if (exp && P.x8_out) *(int4 *)(P.x8_out + off) = v;
+      if ((c * kPW + pw) * 1024 < K) {
+        const int4 v = X.pc[c];
+        // -8 * sum of the x8 met by the offset-form low nibbles of a
+        // 32-byte (group, quarter): bytes 0-3 and 8-11 of each lane's 16,
+        // lane pairs
+        int t = __builtin_amdgcn_sdot4(v.x, 0x01010101, 0, false);
+        t = __builtin_amdgcn_sdot4(v.z, 0x01010101, t, false);
+        t += __builtin_amdgcn_update_dpp(0, t, 0xB1, 0xF, 0xF, false);
+        if (off < K) {
+          stage_u64(stg + off, (uint32_t)v.x, (uint32_t)v.y);
+          stage_u64(stg + off + 8, (uint32_t)v.z, (uint32_t)v.w);
+          if ((lane & 1) == 0) store_coherent(&xlo[off / 32], -8 * t);
+          if (P.x8_out) *(int4 *)(P.x8_out + off) = v;
+        }
       }
     }
-    if (exp && P.e_x_out && pw == 0 && lane == 0) *P.e_x_out = P.e_x_given;
+    if (P.e_x_out && pw == 0 && lane == 0) *P.e_x_out = P.e_x_given;
     return P.e_x_given;
   }
-  const __amdgpu_buffer_rsrc_t rx =
-      __builtin_amdgcn_make_buffer_rsrc((void *)P.x, (short)0, 2 * K, kBufDword3);
-  int4 pc[kPC];
-#pragma unroll
-  for (int c = 0; c < kPC; ++c) pc[c] = vec_load(rx, ((c * kPW + pw) * kChunk + lane * 8) * 2);
   if (P.pro == PRO_RMSNORM_DYNQ8) {
     // layer_fixed.py:1262-1278 in sign-magnitude form (rshift_round rounds
     // the magnitude); K <= kStreamNormKMax
-    const __amdgpu_buffer_rsrc_t rw =
-        __builtin_amdgcn_make_buffer_rsrc((void *)P.norm_w, (short)0, 2 * K, kBufDword3);
-    int4 wv[kPN];
-#pragma unroll
-    for (int c = 0; c < kPN; ++c) wv[c] = vec_load(rw, ((c * kPW + pw) * kChunk + lane * 8) * 2);
     uint64_t ss = 0;
 #pragma unroll
     for (int c = 0; c < kPN; ++c)
+      if ((c * kPW + pw) * kChunk < K)
 #pragma unroll
-      for (int j = 0; j < 8; j += 2) {
-        const int32_t a = piece_get(pc[c], j), b = piece_get(pc[c], j + 1);
-        ss += (uint64_t)((uint32_t)(a * a) + (uint32_t)(b * b));
-      }
+        for (int j = 0; j < 8; j += 2) {
+          const int32_t a = piece_get(X.pc[c], j), b = piece_get(X.pc[c], j + 1);
+          ss += (uint64_t)((uint32_t)(a * a) + (uint32_t)(b * b));
+        }
     ss = wave_sum_u64(ss);
     if (lane == 0) L.pss[pw] = (int64_t)ss;
     sync();
@@ -412,31 +448,34 @@ __device__ int group_prologue(CSite &P, Lds &L, int8_t *xb, int pw, int lane,
     const uint32_t r32 = (uint32_t)r;
 #pragma unroll
     for (int c = 0; c < kPN; ++c) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int32_t xv = piece_get(pc[c], j);
-        const int32_t sc = (int32_t)piece_get(wv[c], j) + one;
-        const uint64_t mag = (uint64_t)(uint32_t)abs(xv) * (uint64_t)r32;
-        uint64_t ym = right ? ((mag + half1) >> rs) : (mag << ls);
-        // y is clipped to [-2^32, 2^32 - 1]; a magnitude of 2^32 or more
-        // saturates the int16 result below for any nonzero scale, exactly as
-        // 2^32 - 1 does, so the product can be formed in 32 x 32 bits
-        ym = ym < 0xFFFFFFFFull ? ym : 0xFFFFFFFFull;
-        const uint64_t q = ((uint64_t)(uint32_t)ym * (uint64_t)(uint32_t)abs(sc) + 8192u) >> 14;
-        const bool neg = (xv < 0) != (sc < 0);
-        const int32_t q32 = q > 65535u ? 65535 : (int32_t)q;
-        const int32_t qm = min(q32, 32767 + (int32_t)neg);
-        piece_set(pc[c], j, (int16_t)(neg ? -qm : qm));
-      }
       const int base = (c * kPW + pw) * kChunk + lane * 8;
-      if (exp && P.xn_out && base < K) *(int4 *)(P.xn_out + base) = pc[c];
+      if ((c * kPW + pw) * kChunk < K) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int32_t xv = piece_get(X.pc[c], j);
+          const int32_t sc = (int32_t)piece_get(X.wv[c], j) + one;
+          const uint64_t mag = (uint64_t)(uint32_t)abs(xv) * (uint64_t)r32;
+          uint64_t ym = right ? ((mag + half1) >> rs) : (mag << ls);
+          // y is clipped to [-2^32, 2^32 - 1]; a magnitude of 2^32 or more
+          // saturates the int16 result below for any nonzero scale, exactly
+          // as 2^32 - 1 does, so the product can be formed in 32 x 32 bits
+          ym = ym < 0xFFFFFFFFull ? ym : 0xFFFFFFFFull;
+          const uint64_t q = ((uint64_t)(uint32_t)ym * (uint64_t)(uint32_t)abs(sc) + 8192u) >> 14;
+          const bool neg = (xv < 0) != (sc < 0);
+          const int32_t q32 = q > 65535u ? 65535 : (int32_t)q;
+          const int32_t qm = min(q32, 32767 + (int32_t)neg);
+          piece_set(X.pc[c], j, (int16_t)(neg ? -qm : qm));
+        }
+        if (P.xn_out && base < K) *(int4 *)(P.xn_out + base) = X.pc[c];
+      }
     }
   }
   int32_t mx = 0;
 #pragma unroll
   for (int c = 0; c < kPC; ++c)
+    if ((c * kPW + pw) * kChunk < K)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) mx = max(mx, abs((int32_t)piece_get(pc[c], j)));
+      for (int j = 0; j < 8; ++j) mx = max(mx, abs((int32_t)piece_get(X.pc[c], j)));
   mx = wave_max_i32(mx);
   if (lane == 0) L.pmx[pw] = mx;
   sync();
@@ -451,28 +490,84 @@ __device__ int group_prologue(CSite &P, Lds &L, int8_t *xb, int pw, int lane,
 #pragma unroll
   for (int c = 0; c < kPC; ++c) {
     const int base = (c * kPW + pw) * kChunk + lane * 8;
-    uint32_t lo = 0, hi = 0;
+    if ((c * kPW + pw) * kChunk < K) {
+      uint32_t lo = 0, hi = 0;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int32_t v = piece_get(pc[c], j);
-      const int32_t qm = min((abs(v) + half) >> e, 127);
-      const uint32_t b8 = (uint32_t)(uint8_t)(int8_t)(v < 0 ? -qm : qm);
-      if (j < 4) lo |= b8 << (8 * j);
-      else       hi |= b8 << (8 * (j - 4));
-    }
-    // -8 * sum of the x8 met by the offset-form low nibbles of one
-    // (group, quarter): 32 consecutive elements = the 4 lanes of a DPP quad
-    int t4 = __builtin_amdgcn_sdot4((int)lo, 0x01010101, 0, false);
-    t4 += __builtin_amdgcn_update_dpp(0, t4, 0xB1, 0xF, 0xF, false);
-    t4 += __builtin_amdgcn_update_dpp(0, t4, 0x4E, 0xF, 0xF, false);
-    if (base < K) {
-      *(uint2 *)(xb + base) = make_uint2(lo, hi);
-      if ((lane & 3) == 0) xlo[base / 32] = -8 * t4;
-      if (exp && P.x8_out) *(uint2 *)(P.x8_out + base) = make_uint2(lo, hi);
+      for (int j = 0; j < 8; ++j) {
+        const int32_t v = piece_get(X.pc[c], j);
+        const int32_t qm = min((abs(v) + half) >> e, 127);
+        const uint32_t b8 = (uint32_t)(uint8_t)(int8_t)(v < 0 ? -qm : qm);
+        if (j < 4) lo |= b8 << (8 * j);
+        else       hi |= b8 << (8 * (j - 4));
+      }
+      // -8 * sum of the x8 met by the offset-form low nibbles of one
+      // (group, quarter): 32 consecutive elements = the 4 lanes of a DPP quad
+      int t4 = __builtin_amdgcn_sdot4((int)lo, 0x01010101, 0, false);
+      t4 += __builtin_amdgcn_update_dpp(0, t4, 0xB1, 0xF, 0xF, false);
+      t4 += __builtin_amdgcn_update_dpp(0, t4, 0x4E, 0xF, 0xF, false);
+      if (base < K) {
+        stage_u64(stg + base, lo, hi);
+        if ((lane & 3) == 0) store_coherent(&xlo[base / 32], -8 * t4);
+        if (P.x8_out) *(uint2 *)(P.x8_out + base) = make_uint2(lo, hi);
+      }
     }
   }
-  if (exp && P.e_x_out && pw == 0 && lane == 0) *P.e_x_out = e;
+  if (P.e_x_out && pw == 0 && lane == 0) *P.e_x_out = e;
   return e;
+}
+
+// Site s's prologue, by the CU that owns it: inputs, compute, then -- every
+// store of the three wavefronts complete -- e_x and the site's flag.
+__device__ void compute_publish(CSite &P, Lds &L, int8_t *stg, uint32_t *flag, int pw,
+                                int lane, GroupSync<kPW, false> &sync) {
+  ProX X;
+  pro_issue(X, P, true, pw, lane);
+  const int e = group_prologue(P, L, stg, pw, lane, sync, X);
+  if (pw == 0 && lane == 0) store_coherent((int32_t *)(stg + kXB), (int32_t)e);
+  wait_vm_all();
+  sync();
+  if (pw == 0 && lane == 0) store_coherent(flag, 1u);
+}
+
+// the wavefront waits until site s's activations are staged (bounded; bit 1
+// of err, as for the grid-wide wait)
+__device__ __forceinline__ bool wait_staged(const uint32_t *flag, int lane, int32_t *err) {
+  for (uint32_t n = 0; n < kGridSpin; ++n) {
+    if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) return true;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  if (lane == 0) atomicOr(err, 2);
+  return false;
+}
+
+// copy a staged site (x8 [0, K), corrections [kXloOff, + K/8)) into LDS
+// buffer xb: 1 KiB per copy instruction, split over the 3 wavefronts
+__device__ __forceinline__ void load_staged(const int8_t *stg, int8_t *xb, int K, int pw,
+                                            int lane) {
+  for (int off = pw * 1024; off < K; off += kPW * 1024)
+    if (off + 16 * lane < K) copy16_sc1(stg + off + 16 * lane, lds_off(xb + off));
+  const int nlo = K / 8;
+  for (int off = pw * 1024; off < nlo; off += kPW * 1024)
+    if (off + 16 * lane < nlo)
+      copy16_sc1(stg + kXloOff + off + 16 * lane, lds_off(xb + kXloOff + off));
+}
+
+// the wavefront waits until all prologue wavefronts have written site s's
+// activations into buffer b (bounded, like lds_wait_eq)
+__device__ __forceinline__ void wait_ready(Lds &L, int b, int s, int lane) {
+  for (uint32_t n = 0;; ++n) {
+    if (__all(lds_read_i32(&L.ready[b][lane % kPW]) == s)) break;
+    if (lds_read_i32(&L.abort) != 0) break;
+    if (n > kLdsSpin) {
+      if (lane == 0) {
+        lds_write_i32(&L.abort, 1);
+        lds_or_i32(&L.err, 4);
+      }
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  wait_lds();
 }
 
 // the wavefront waits until every weight wavefront has moved past site t
@@ -505,7 +600,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
     L.tgen[tid] = tid;
     L.tready[tid] = 0;
   }
-  if (tid < kNB) L.ready[tid] = -1;
+  if (tid < kNB * kPW) (&L.ready[0][0])[tid] = -1;
   if (tid < kCW) L.wsite[tid] = 0;
   if (tid < kPW) L.psync[tid] = 0;
   if (tid == 0) {
@@ -536,20 +631,46 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
       }
     }
   } else if (wave >= kPW0) {
-    // prologues, in site order, into the buffer ring
+    // Every site's prologue is computed once, by CU s % G, into the site's
+    // staging area (a site behind no fence at once, a fenced one after its
+    // grid-wide wait); every CU then copies the staged sites, in order, into
+    // its buffer ring ahead of the weight wavefronts.
     const int pw = wave - kPW0;
-    GroupSync<kPW> sync{L.psync, kPW0, 0, true};
+    // the SIMDs these wavefronts share with weight wavefronts issue their
+    // instructions first
+    __builtin_amdgcn_s_setprio(3);
+    GroupSync<kPW, false> sync{L.psync, kPW0, 0, true};
+    uint32_t *sflag = S.done + stream_flag_site0(G);
     bool ok = true;
+    for (int s = r; s < nsites; s += G)
+      if (sites[s].fence_at == 0)
+        compute_publish(sites[s], L, S.stage + (size_t)s * kStageBytes, sflag + s, pw, lane,
+                        sync);
     for (int s = 0; s < nsites; ++s) {
+      // lane-derived addresses are recomputed per site from an opaque copy
+      // of the thread index, so the compiler does not keep them live
+      int tid_s = tid;
+      asm volatile("" : "+v"(tid_s));
+      const int lane = tid_s & 63;
       CSite &P = sites[s];
+      const int8_t *stg = S.stage + (size_t)s * kStageBytes;
+      if (s % G == r && P.fence_at > 0) {
+        ok = lds_wait_ge(&L.gridok, P.fence_at) && ok;
+        compute_publish(P, L, S.stage + (size_t)s * kStageBytes, sflag + s, pw, lane, sync);
+      }
       const int b = s % kNB;
       if (s >= kNB) ok = wait_weights_past(L, s - kNB, lane) && ok;
-      if (P.fence_at > 0) ok = lds_wait_ge(&L.gridok, P.fence_at) && ok;
-      const int e = group_prologue(P, L, L.x[b], pw, lane, sync);
-      sync();   // the group's writes into buffer b are complete
-      if (pw == 0 && lane == 0) {
-        lds_write_i32(&L.ex[b], e);
-        lds_write_i32(&L.ready[b], s);
+      ok = wait_staged(sflag + s, lane, S.err) && ok;
+      load_staged(stg, L.x[b], P.K, pw, lane);
+      const int e = __hip_atomic_load((const int32_t *)(stg + kXB), __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+      wait_vm_all();
+      // this wavefront's copies into buffer b have landed (lds_write_i32
+      // waits for its LDS work first); the site is ready once all three
+      // have posted
+      if (lane == 0) {
+        if (pw == 0) lds_write_i32(&L.ex[b], e);
+        lds_write_i32(&L.ready[b][pw], s);
       }
     }
     if (!(ok && sync.ok) && lane == 0) lds_or_i32(&L.err, 4);
@@ -580,7 +701,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
         // done with every earlier site; wait for this one's activations
         s_cur = c.s;
         lds_write_i32(&L.wsite[wave], s_cur);
-        lds_wait_eq(L, &L.ready[s_cur % kNB], s_cur, lane_s);
+        wait_ready(L, s_cur % kNB, s_cur, lane_s);
         e_x = __builtin_amdgcn_readfirstlane(lds_read_i32(&L.ex[s_cur % kNB]));
         contributors = min(sites[s_cur].nblk, kCW);
       }
@@ -642,6 +763,8 @@ int stream_max_blocks_per_cu() {
   return n > 1 ? 1 : n;
 }
 
-size_t stream_counter_words(int grid) { return (size_t)(grid + 63) / 64 * 64; }
+size_t stream_counter_words(int grid, int nsites) {
+  return stream_flag_site0(grid) + (size_t)(nsites + 63) / 64 * 64;
+}
 
 }  // namespace w4a8
