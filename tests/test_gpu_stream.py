@@ -1,5 +1,7 @@
 """The full Qwen3.5-9B-shaped stream (249 matrices, 4.09 GB) on the device,
-replayed as a HIP graph, checked bit-exactly against the C/numpy oracle:
+replayed as a HIP graph and as one persistent launch (every site fenced, and
+fenced only where buffers are shared), checked bit-exactly against the
+C/numpy oracle:
 every site's DYNQ8 output and exponent, every MOVY / SILU32 output, and the
 LM-head argmax."""
 import numpy as np
@@ -12,9 +14,11 @@ from tests import stream_check as sc
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("mode", [N.PLAN_GRAPH, N.PLAN_PERSISTENT])
-def test_full_stream_bit_exact(engine, mode):
-    st = stream9b.Stream9B(engine, seed=7, mode=mode)
+@pytest.mark.parametrize("mode,fences", [(N.PLAN_GRAPH, N.FENCE_ALL),
+                                         (N.PLAN_PERSISTENT, N.FENCE_ALL),
+                                         (N.PLAN_PERSISTENT, N.FENCE_AUTO)])
+def test_full_stream_bit_exact(engine, mode, fences):
+    st = stream9b.Stream9B(engine, seed=7, mode=mode, fences=fences)
     try:
         st.run()
         st.run()                      # second replay of the same graph
