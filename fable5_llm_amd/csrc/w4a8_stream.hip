@@ -636,9 +636,8 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
     // grid-wide wait); every CU then copies the staged sites, in order, into
     // its buffer ring ahead of the weight wavefronts.
     const int pw = wave - kPW0;
-    // the SIMDs these wavefronts share with weight wavefronts issue their
-    // instructions first
-    __builtin_amdgcn_s_setprio(3);
+    // (default wave priority: these wavefronts mostly wait, and raised
+    // priority lets their polls outrank the weight wavefronts' work)
     GroupSync<kPW, false> sync{L.psync, kPW0, 0, true};
     uint32_t *sflag = S.done + stream_flag_site0(G);
     bool ok = true;
