@@ -93,7 +93,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=60,
-                    help="untimed steps first; the GPU needs about 40 steps of
+                    help="untimed steps first; the GPU needs about 40 steps of "
                          "continuous work to reach its steady clocks")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
