@@ -6,7 +6,8 @@ sites (65 with a fused RMSNorm), 249 matrices, 4,091,805,696 bytes of int4
 weights + uint16 scales, every matvec followed by its MOVY / SILU32 epilogue
 and the 248,320-row LM head by its argmax.  All inputs are synthetic, seeded
 and resident in HBM before the timed region.
---mode persistent (default) runs the whole step in one cooperative launch;
+--mode persistent (default) runs the whole step in one launch of one workgroup
+per CU (--mode cooperative: the same launch through the cooperative launch API);
 --fences auto (default) orders a site after an earlier one only where they
 share a buffer (the synthetic sites share none), --fences all after every
 earlier site.  --mode graph replays one GEMV launch per site as a HIP graph,
@@ -101,9 +102,10 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device copy (known bytes), the "
                          "reference point for rocprofv3 FETCH_SIZE/WRITE_SIZE")
-    ap.add_argument("--mode", choices=["persistent", "graph"], default="persistent",
-                    help="one cooperative launch per step, or one launch per "
-                         "site replayed as a HIP graph")
+    ap.add_argument("--mode", choices=["persistent", "cooperative", "graph"],
+                    default="persistent",
+                    help="one launch per step (plain, or through the cooperative "
+                         "launch API), or one launch per site replayed as a HIP graph")
     ap.add_argument("--fences", choices=["all", "auto"], default="auto",
                     help="persistent mode: every site waits for all earlier ones, "
                          "or only where it shares a buffer with one")
@@ -138,7 +140,9 @@ def main():
     ctx.set_stream(stream)
     t_build = time.perf_counter()
     from fable5_llm_amd import _native as N
-    mode = N.PLAN_PERSISTENT if args.mode == "persistent" else N.PLAN_GRAPH
+    mode = {"persistent": N.PLAN_PERSISTENT, "cooperative": N.PLAN_PERSISTENT_COOP,
+            "graph": N.PLAN_GRAPH}[args.mode]
+    persistent = mode != N.PLAN_GRAPH
     fences = N.FENCE_AUTO if args.fences == "auto" else N.FENCE_ALL
     st = stream9b.Stream9B(ctx, seed=args.seed, mode=mode, fences=fences)
     ctx.sync()
@@ -166,12 +170,12 @@ def main():
     # per-launch kernel time, ms (dispatch-recorded events; median of 5)
     prof = np.median(np.stack([st.profile() for _ in range(5)]), axis=0)
     kern_ms = float(prof.sum())
-    nlaunch = 1 if args.mode == "persistent" else int(prof.size)
+    nlaunch = 1 if persistent else int(prof.size)
     achieved = st.bytes / (kern_ms * 1e-3) / 1e9
-    kernel = "stream_kernel" if args.mode == "persistent" else "gemv_kernel"
+    kernel = "stream_kernel" if persistent else "gemv_kernel"
 
     ordered = None
-    if not args.no_ordered and args.mode == "persistent":
+    if not args.no_ordered and persistent:
         # the same plan with every site after the previous one: graph mode
         st.plan.set_mode(N.PLAN_GRAPH)
         for _ in range(max(3, args.warmup // 2)):
@@ -213,13 +217,15 @@ def main():
             "matrices": tot["matrices"], "dynq8_sites": tot["sites"],
             "rmsnorm_sites": tot["rmsnorm_sites"], "bytes_per_step": st.bytes,
             "reference_chunks": 1370, "batch": 1,
-            "fences": args.fences if args.mode == "persistent" else "all",
-            "launch": ("one cooperative launch per step; " +
+            "fences": args.fences if persistent else "all",
+            "launch": (("one launch per step, one workgroup per CU (" +
+                        ("cooperative launch API" if args.mode == "cooperative" else
+                         "plain launch") + "); " +
                        ("a site waits for earlier ones only where it shares a buffer "
                         "with them (the synthetic sites share none)"
                         if args.fences == "auto" else
-                        "every site waits for all earlier ones (per-workgroup flags)")
-                       if args.mode == "persistent"
+                        "every site waits for all earlier ones (per-workgroup flags)"))
+                       if persistent
                        else "HIP graph, one GEMV launch per site, in order"),
         },
         "roofline": {

@@ -17,7 +17,7 @@ PRO_X8, PRO_DYNQ8, PRO_RMSNORM_DYNQ8 = 0, 1, 2
 EPI_Y32, EPI_MOVY_I16, EPI_MOVY_P32, EPI_SILU32, EPI_SHIFT_I64 = 0, 1, 2, 3, 4
 ALU_SHIFT32, ALU_SILU32, ALU_EMUL32, ALU_SHIFT32W = 1, 6, 8, 9
 MOVY_PAIRS32, MOVY_INT16 = 0, 1
-PLAN_GRAPH, PLAN_PERSISTENT = 0, 1
+PLAN_GRAPH, PLAN_PERSISTENT, PLAN_PERSISTENT_COOP = 0, 1, 2
 FENCE_ALL, FENCE_AUTO = 0, 1
 
 _P = ctypes.c_void_p

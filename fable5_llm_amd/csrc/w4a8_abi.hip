@@ -136,7 +136,10 @@ int take_err(w4a8_ctx *c) {
     HIP_TRY(hipMemset(c->d_err, 0, sizeof(int32_t)));
     if (h & 1) return fail(W4A8_E_Y32_OVF, "y32 overflow — sh miscomputed");
     if (h & 2)
-      return fail(W4A8_E_HIP, "a persistent plan's site-completion wait timed out");
+      return fail(W4A8_E_HIP, "a persistent plan's wait for other workgroups timed out "
+                            "(are all of its workgroups resident? another long-running "
+                            "kernel on the GPU can hold CUs; W4A8_PLAN_PERSISTENT_COOP "
+                            "guarantees residency)");
     if (h & 4)
       return fail(W4A8_E_HIP, "a wait between wavefronts of one workgroup timed out");
   }
@@ -750,8 +753,8 @@ struct w4a8_plan {
   // persistent mode
   GemvParams *d_sites = nullptr;
   uint32_t *d_done = nullptr;
+  uint32_t epoch = 0;               // launches since d_done was zeroed
   int8_t *d_stage = nullptr;
-  uint64_t *d_pkeys = nullptr;
   int G = 0;
   int head_site = -1;
   int32_t *head_result = nullptr;
@@ -761,11 +764,10 @@ static void plan_drop_persistent(w4a8_plan *p) {
   if (p->d_sites) (void)hipFree(p->d_sites);
   if (p->d_done) (void)hipFree(p->d_done);
   if (p->d_stage) (void)hipFree(p->d_stage);
-  if (p->d_pkeys) (void)hipFree(p->d_pkeys);
   p->d_sites = nullptr;
   p->d_done = nullptr;
   p->d_stage = nullptr;
-  p->d_pkeys = nullptr;
+  p->epoch = 0;
   p->G = 0;
 }
 
@@ -858,7 +860,7 @@ static int plan_build_persistent(w4a8_plan *p) {
   HIP_TRY(hipMalloc(&p->d_sites, sizeof(GemvParams) * (size_t)n));
   HIP_TRY(hipMalloc(&p->d_done, sizeof(uint32_t) * stream_counter_words(p->G, n)));
   HIP_TRY(hipMalloc(&p->d_stage, (size_t)kStageBytes * (size_t)n));
-  HIP_TRY(hipMalloc(&p->d_pkeys, sizeof(uint64_t) * (size_t)p->G));
+  p->epoch = 0;
   HIP_TRY(hipMemcpy(p->d_sites, sites.data(), sizeof(GemvParams) * (size_t)n,
                     hipMemcpyHostToDevice));
   return W4A8_OK;
@@ -866,21 +868,30 @@ static int plan_build_persistent(w4a8_plan *p) {
 
 static int plan_launch_persistent(w4a8_plan *p, hipStream_t s, hipEvent_t e0,
                                   hipEvent_t e1, uint64_t *trace = nullptr) {
+  const int n = (int)p->steps.size();
+  // The flag words are zeroed once, not per launch: each launch's flag values
+  // exceed the previous launch's (they grow by n + 1 per launch), and the
+  // head's words are left zero by the launch that used them.  They are zeroed
+  // again before the values would pass 2^32, and in every launch a graph
+  // captures (each replay of the graph stores the same values).
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing(s, &cs));
+  if (p->epoch == 0 || cs != hipStreamCaptureStatusNone ||
+      (uint64_t)(p->epoch + 1) * (uint64_t)(n + 1) > 0xFFFFFFFFull) {
+    HIP_TRY(launch_fill_i32((int32_t *)p->d_done, 0, (int64_t)stream_counter_words(p->G, n), s));
+    p->epoch = 0;
+  }
   StreamParams sp{};
   sp.sites = p->d_sites;
-  sp.nsites = (int32_t)p->steps.size();
+  sp.nsites = (int32_t)n;
   sp.head_site = p->head_site;
   sp.done = p->d_done;
+  sp.epoch = ++p->epoch;
   sp.stage = p->d_stage;
   sp.err = p->ctx->d_err;
-  sp.partials = p->d_pkeys;
+  sp.result = p->head_result;
   sp.trace = trace;
-  HIP_TRY(launch_fill_i32((int32_t *)p->d_done, 0,
-                          (int64_t)stream_counter_words(p->G, (int)p->steps.size()), s));
-  if (e0) HIP_TRY(hipEventRecord(e0, s));
-  HIP_TRY(launch_stream(sp, p->G, s));
-  if (e1) HIP_TRY(hipEventRecord(e1, s));
-  if (p->head_site >= 0) HIP_TRY(launch_argmax_final(p->d_pkeys, p->G, p->head_result, s));
+  HIP_TRY(launch_stream(sp, p->G, s, p->mode == W4A8_PLAN_PERSISTENT_COOP, e0, e1));
   return W4A8_OK;
 }
 
@@ -960,7 +971,8 @@ int w4a8_plan_add_head(w4a8_plan *p, const w4a8_weights *w, int32_t prologue,
 }
 
 int w4a8_plan_set_mode(w4a8_plan *p, int32_t mode) {
-  if (!p || (mode != W4A8_PLAN_GRAPH && mode != W4A8_PLAN_PERSISTENT))
+  if (!p || (mode != W4A8_PLAN_GRAPH && mode != W4A8_PLAN_PERSISTENT &&
+             mode != W4A8_PLAN_PERSISTENT_COOP))
     return fail(W4A8_E_ARG, "unknown plan mode");
   if (mode != p->mode) plan_drop_graph(p);
   p->mode = mode;
@@ -980,7 +992,7 @@ int w4a8_plan_run(w4a8_plan *p) {
   if (p->steps.empty()) return W4A8_OK;
   w4a8_ctx *c = p->ctx;
   DeviceGuard g(c->device);
-  if (p->mode == W4A8_PLAN_PERSISTENT) {
+  if (p->mode != W4A8_PLAN_GRAPH) {
     if (!p->d_sites) {
       int rc = plan_build_persistent(p);
       if (rc) {
@@ -1016,7 +1028,7 @@ int w4a8_plan_profile(w4a8_plan *p, int32_t n, float *ms) {
     return fail(W4A8_E_ARG, "plan has " + std::to_string(p->steps.size()) + " steps");
   w4a8_ctx *c = p->ctx;
   DeviceGuard g(c->device);
-  if (p->mode == W4A8_PLAN_PERSISTENT) {
+  if (p->mode != W4A8_PLAN_GRAPH) {
     // one launch runs every step: its per-site times come from the
     // wall-clock stamps workgroup 0 takes as it starts each site, scaled so
     // that they sum to the launch's event-measured time

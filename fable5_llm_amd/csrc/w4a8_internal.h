@@ -129,31 +129,46 @@ hipError_t launch_gemv(const GemvParams &p, int grid, hipStream_t s);
 // same launch bracketed by events recorded by the dispatch itself
 hipError_t launch_gemv_timed(const GemvParams &p, int grid, hipStream_t s,
                              hipEvent_t start, hipEvent_t stop);
-// Persistent decode-step kernel: every site of a plan in one cooperative
-// launch of one workgroup per CU (8 weight wavefronts holding their next two
-// blocks in registers + 1 control wavefront); a site with `fence` set waits
-// for one completion flag per workgroup.
+// Persistent decode-step kernel: every site of a plan in one launch of one
+// workgroup per CU (8 weight wavefronts holding their next two blocks in
+// registers, 1 control wavefront, 3 prologue wavefronts); a site with
+// `fence` set waits for one completion flag per workgroup.
 constexpr int kStreamNormKMax = 4096;   // RMSNorm sites of a persistent plan
 struct StreamParams {
   const GemvParams *sites;  // device array, nsites entries
   int32_t nsites;
   int32_t head_site;        // index of the LM-head site, or -1
-  uint32_t *done;           // stream_counter_words(grid, nsites) words, zero at launch:
-                            // a completion flag per workgroup, then one per site whose
-                            // activations are staged
+  uint32_t *done;           // stream_counter_words(grid, nsites) words, zero when
+                            // allocated and never cleared between launches:
+                            // a completion flag per workgroup (launch `epoch` stores
+                            // (epoch - 1) * (nsites + 1) + s + 1 after site s), one flag
+                            // per site whose activations are staged (stores epoch), then
+                            // the head's key and arrival count (stream_head_word0)
+  uint32_t epoch;           // launches since `done` was zeroed, this one included:
+                            // every flag value it stores exceeds all earlier ones
   int8_t *stage;            // nsites * kStageBytes: each site's x8, corrections, e_x
   int32_t *err;             // bit 1: a completion wait gave up; bit 2: an LDS wait did
-  uint64_t *partials;       // head: one key per workgroup
+  int32_t *result;          // head: (index, value) of the maximum, written by the
+                            // workgroup that arrives last
   uint64_t *trace;          // optional: nsites + 1 wall-clock stamps taken by
                             // workgroup 0 as it starts each site, and at its end
 };
-hipError_t launch_stream(const StreamParams &sp, int grid, hipStream_t s);
+// one workgroup per CU; `cooperative`: through the cooperative launch API.
+// start / stop (optional) bracket the kernel: recorded by the dispatch itself
+// for the plain launch, around it for the cooperative one
+hipError_t launch_stream(const StreamParams &sp, int grid, hipStream_t s, bool cooperative,
+                         hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 int stream_max_blocks_per_cu();
 // uint32 words of flags a grid of `grid` workgroups running nsites sites needs
 size_t stream_counter_words(int grid, int nsites);
 // index of the first site flag
 __host__ __device__ inline size_t stream_flag_site0(int grid) {
   return (size_t)(grid + 63) / 64 * 64;
+}
+// index of the head's words: the uint64 key of the maximum so far (two words),
+// then the count of workgroups that have added theirs; both zero between launches
+__host__ __device__ inline size_t stream_head_word0(int grid, int nsites) {
+  return stream_flag_site0(grid) + (size_t)(nsites + 63) / 64 * 64;
 }
 // one site's staged activations: x8[kKMax], int32 corrections[kKMax / 32], e_x
 constexpr int kStageBytes = kKMax + kKMax / 8 + 16;

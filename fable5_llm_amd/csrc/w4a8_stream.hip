@@ -1,6 +1,6 @@
 // Persistent decode-step kernel (W4A8_PLAN_PERSISTENT) for gfx950.
 //
-// One cooperative launch runs every site of a plan, one workgroup per CU of
+// One launch runs every site of a plan, one workgroup per CU of
 // 12 wavefronts with three roles, which meet only through LDS flags -- no
 // workgroup barrier while the plan runs:
 //
@@ -36,6 +36,8 @@
 // Every result is bit-exact with the reference's integer law
 // (ref/w4a8_ref.py:254-289, fixedpoint.py:24-75, layer_fixed.py:1242-1278
 // and the epilogues of gen_layer_script.py:1397-1433, seq_model.py:1027-1050).
+#include <hip/hip_ext.h>
+
 #include "w4a8_device.h"
 
 namespace w4a8 {
@@ -518,22 +520,23 @@ __device__ int group_prologue(CSite &P, Lds &L, int8_t *stg, int pw, int lane,
 
 // Site s's prologue, by the CU that owns it: inputs, compute, then -- every
 // store of the three wavefronts complete -- e_x and the site's flag.
-__device__ void compute_publish(CSite &P, Lds &L, int8_t *stg, uint32_t *flag, int pw,
-                                int lane, GroupSync<kPW, false> &sync) {
+__device__ void compute_publish(CSite &P, Lds &L, int8_t *stg, uint32_t *flag, uint32_t epoch,
+                                int pw, int lane, GroupSync<kPW, false> &sync) {
   ProX X;
   pro_issue(X, P, true, pw, lane);
   const int e = group_prologue(P, L, stg, pw, lane, sync, X);
   if (pw == 0 && lane == 0) store_coherent((int32_t *)(stg + kXB), (int32_t)e);
   wait_vm_all();
   sync();
-  if (pw == 0 && lane == 0) store_coherent(flag, 1u);
+  if (pw == 0 && lane == 0) store_coherent(flag, epoch);
 }
 
-// the wavefront waits until site s's activations are staged (bounded; bit 1
-// of err, as for the grid-wide wait)
-__device__ __forceinline__ bool wait_staged(const uint32_t *flag, int lane, int32_t *err) {
+// the wavefront waits until site s's activations are staged in this launch
+// (bounded; bit 1 of err, as for the grid-wide wait)
+__device__ __forceinline__ bool wait_staged(const uint32_t *flag, uint32_t epoch, int lane,
+                                            int32_t *err) {
   for (uint32_t n = 0; n < kGridSpin; ++n) {
-    if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) return true;
+    if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= epoch) return true;
     __builtin_amdgcn_s_sleep(1);
   }
   if (lane == 0) atomicOr(err, 2);
@@ -581,6 +584,32 @@ __device__ __forceinline__ bool wait_weights_past(Lds &L, int t, int lane) {
 }
 
 
+// The head's maximum over workgroups: each adds its key with an atomic max,
+// waits for it to be performed, then counts itself in; the last to arrive
+// reads the key, writes (index, value) and zeroes both words for the next
+// launch, which the stream orders after this one.  The atomics are performed
+// at the device's coherence point, so, as for the completion flags, a wait
+// for the returned value orders them -- an acquire / release pair would add
+// an L2 write-back and invalidate to every workgroup's exit.
+// A key is (value ^ 2^31) << 32 | (2^32 - 1 - index): the unsigned maximum is
+// the largest value and, among equal values, the lowest index.
+__device__ void head_arrive(const StreamParams &S, int G, uint64_t best) {
+  const size_t w0 = stream_head_word0(G, S.nsites);
+  uint64_t *key = (uint64_t *)(S.done + w0);
+  uint32_t *count = S.done + w0 + 2;
+  uint64_t was = __hip_atomic_fetch_max(key, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  asm volatile("" : "+v"(was));   // a returning atomic ...
+  wait_vm_all();                   // ... that has returned
+  const uint32_t before =
+      __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (before != (uint32_t)G - 1u) return;
+  const uint64_t k = __hip_atomic_load(key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(key, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  S.result[0] = (int32_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFu));
+  S.result[1] = (int32_t)((uint32_t)(k >> 32) ^ 0x80000000u);
+}
+
 __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
                                                           const GemvParams *__restrict__ sites_arg) {
   CSite *sites = (CSite *)sites_arg;
@@ -589,6 +618,8 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = gridDim.x, r = blockIdx.x;
   const int nsites = S.nsites;
+  // this launch's completion-flag values are fbase + 1 .. fbase + nsites
+  const uint32_t fbase = (S.epoch - 1u) * (uint32_t)(nsites + 1);
 
   // tables, reduction slots and flags
   const int32_t *tab = sites[0].tables;
@@ -624,9 +655,10 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
         kt0 += first < P.total_tiles ? (P.total_tiles - 1 - first) / G + 1 : 0;
       }
       if (s + 1 < nsites && sites[s + 1].fence) {
+        const uint32_t v = fbase + (uint32_t)(s + 1);
         wait_vm_all();   // this workgroup's outputs of sites <= s are stored
-        if (lane == 0) store_coherent(S.done + r, (uint32_t)(s + 1));
-        grid_wait(S.done, G, (uint32_t)(s + 1), lane, S.err);
+        if (lane == 0) store_coherent(S.done + r, v);
+        grid_wait(S.done, G, v, lane, S.err);
         if (lane == 0) lds_write_i32(&L.gridok, s + 1);
       }
     }
@@ -643,8 +675,8 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
     bool ok = true;
     for (int s = r; s < nsites; s += G)
       if (sites[s].fence_at == 0)
-        compute_publish(sites[s], L, S.stage + (size_t)s * kStageBytes, sflag + s, pw, lane,
-                        sync);
+        compute_publish(sites[s], L, S.stage + (size_t)s * kStageBytes, sflag + s, S.epoch,
+                        pw, lane, sync);
     for (int s = 0; s < nsites; ++s) {
       // lane-derived addresses are recomputed per site from an opaque copy
       // of the thread index, so the compiler does not keep them live
@@ -655,11 +687,12 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
       const int8_t *stg = S.stage + (size_t)s * kStageBytes;
       if (s % G == r && P.fence_at > 0) {
         ok = lds_wait_ge(&L.gridok, P.fence_at) && ok;
-        compute_publish(P, L, S.stage + (size_t)s * kStageBytes, sflag + s, pw, lane, sync);
+        compute_publish(P, L, S.stage + (size_t)s * kStageBytes, sflag + s, S.epoch, pw, lane,
+                        sync);
       }
       const int b = s % kNB;
       if (s >= kNB) ok = wait_weights_past(L, s - kNB, lane) && ok;
-      ok = wait_staged(sflag + s, lane, S.err) && ok;
+      ok = wait_staged(sflag + s, S.epoch, lane, S.err) && ok;
       load_staged(stg, L.x[b], P.K, pw, lane);
       const int e = __hip_atomic_load((const int32_t *)(stg + kXB), __ATOMIC_RELAXED,
                                       __HIP_MEMORY_SCOPE_AGENT);
@@ -740,18 +773,29 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
   if (wave == kCtrl && lane_e == 0) {
     const int32_t e = lds_read_i32(&L.err);
     if (e) atomicOr(S.err, e);
-    if (S.head_site >= 0) S.partials[r] = L.best;
+    if (S.head_site >= 0) head_arrive(S, G, L.best);
     if (S.trace && r == 0) S.trace[nsites] = wall_clock64();
   }
 }
 
 }  // namespace
 
-hipError_t launch_stream(const StreamParams &sp, int grid, hipStream_t s) {
+hipError_t launch_stream(const StreamParams &sp, int grid, hipStream_t s, bool cooperative,
+                         hipEvent_t start, hipEvent_t stop) {
   const GemvParams *sites = sp.sites;
-  void *args[] = {(void *)&sp, (void *)&sites};
-  return hipLaunchCooperativeKernel((const void *)stream_kernel, dim3(grid), dim3(kThreads),
-                                    args, 0, s);
+  if (cooperative) {
+    void *args[] = {(void *)&sp, (void *)&sites};
+    hipError_t e = start ? hipEventRecord(start, s) : hipSuccess;
+    if (e == hipSuccess)
+      e = hipLaunchCooperativeKernel((const void *)stream_kernel, dim3(grid), dim3(kThreads),
+                                     args, 0, s);
+    if (e == hipSuccess && stop) e = hipEventRecord(stop, s);
+    return e;
+  }
+  // events, when given, are recorded by the dispatch itself
+  hipExtLaunchKernelGGL(stream_kernel, dim3(grid), dim3(kThreads), 0, s, start, stop, 0, sp,
+                        sites);
+  return hipGetLastError();
 }
 
 int stream_max_blocks_per_cu() {
@@ -763,7 +807,7 @@ int stream_max_blocks_per_cu() {
 }
 
 size_t stream_counter_words(int grid, int nsites) {
-  return stream_flag_site0(grid) + (size_t)(nsites + 63) / 64 * 64;
+  return stream_head_word0(grid, nsites) + 64;
 }
 
 }  // namespace w4a8

@@ -175,11 +175,24 @@ int w4a8_matmul_y32_async(w4a8_ctx *ctx, const w4a8_weights *w,
  *      captured at add time. -------------------------------------------- */
 #define W4A8_PLAN_GRAPH       0 /* one launch per site, replayed as a HIP graph;
                                    site s+1 starts after site s has completed */
-#define W4A8_PLAN_PERSISTENT  1 /* one cooperative launch for every site; a
-                                   fenced site waits for per-workgroup
-                                   completion flags, and each wavefront keeps
-                                   its next weight blocks in flight across the
-                                   wait */
+#define W4A8_PLAN_PERSISTENT  1 /* one launch for every site, one workgroup
+                                   per CU; a fenced site waits for
+                                   per-workgroup completion flags, and each
+                                   wavefront keeps its next weight blocks in
+                                   flight across the wait.  The grid is the
+                                   device's CU count and the kernel's LDS
+                                   admits one workgroup per CU, so on a GPU
+                                   not running other long kernels every
+                                   workgroup is resident at once; the waits
+                                   between workgroups are bounded, and report
+                                   an error (W4A8_E_HIP at the next sync)
+                                   instead of hanging where one is not */
+#define W4A8_PLAN_PERSISTENT_COOP 2 /* the same launch through the cooperative
+                                   launch API, which guarantees that every
+                                   workgroup is resident (for a GPU shared
+                                   with other long-running kernels); the
+                                   runtime's cooperative dispatch costs about
+                                   17 us per launch on MI355X */
 /* fences of a persistent plan */
 #define W4A8_FENCE_ALL   0 /* (default) every site waits for all earlier ones */
 #define W4A8_FENCE_AUTO  1 /* a site waits only when it reads a buffer an

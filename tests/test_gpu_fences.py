@@ -35,7 +35,8 @@ def _site_ref(img, nrows, x16, prologue, in_f, p0, norm_w=None, one_plus=True):
 
 @pytest.mark.parametrize("mode,fences", [(N.PLAN_GRAPH, N.FENCE_ALL),
                                          (N.PLAN_PERSISTENT, N.FENCE_ALL),
-                                         (N.PLAN_PERSISTENT, N.FENCE_AUTO)])
+                                         (N.PLAN_PERSISTENT, N.FENCE_AUTO),
+                                         (N.PLAN_PERSISTENT_COOP, N.FENCE_AUTO)])
 def test_dependent_sites(engine, mode, fences):
     from fable5_llm_amd.engine import Plan
     dev = torch.device("cuda", 0)

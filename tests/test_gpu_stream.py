@@ -16,7 +16,8 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("mode,fences", [(N.PLAN_GRAPH, N.FENCE_ALL),
                                          (N.PLAN_PERSISTENT, N.FENCE_ALL),
-                                         (N.PLAN_PERSISTENT, N.FENCE_AUTO)])
+                                         (N.PLAN_PERSISTENT, N.FENCE_AUTO),
+                                         (N.PLAN_PERSISTENT_COOP, N.FENCE_AUTO)])
 def test_full_stream_bit_exact(engine, mode, fences):
     st = stream9b.Stream9B(engine, seed=7, mode=mode, fences=fences)
     try:
