@@ -18,8 +18,11 @@ chain of dependent sites).
 Prints one JSON line.  `value` = stream bytes / wall time per step.
 `roofline` = the dominant kernel alone: stream bytes / sum of its per-launch
 durations, each launch bracketed by dispatch-recorded HIP events.
+`batched` = the int8-MFMA kernel over the stream's 96 FFN matrices at B
+tokens per pass (--batch), with its GB/s and MFMA utilisation.
 `cpu_baseline` = the C oracle (oracle/law_c.c, OpenMP) over the same stream
-on the host cores, which also checks every GPU output bit-exactly.
+on the host cores, which also checks every GPU output bit-exactly (and the
+batched leg's outputs for layer 0's FFN matrices, every token).
 """
 import argparse
 import json
@@ -31,6 +34,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
+PEAK_INT8_TOPS = 5000.0   # dense int8 MFMA, MI355X
 
 
 def traffic_profile(kernel):
@@ -51,9 +55,90 @@ def pmc_traffic(kernel):
 METRIC = "achieved HBM GB/s (% of peak) on W4A8 GEMV; ms per 9B-shape weight stream"
 
 
-def cpu_baseline(st, min_seconds):
+def batched_leg(st, ctx, batches, steps, warmup, seed):
+    """The FFN matrices of the stream (32 x gate, up: 12288 x 4096; down:
+    4096 x 12288; 2.49 GB, far beyond the 256 MB Infinity Cache) through the
+    batched int8-MFMA kernel, B tokens per pass: per-token x16 in Q8.7
+    (N(0,1), 1 % outliers), DYNQ8 per token on the GPU, then one
+    w4a8_matmul_y32 per matrix.  Returns the timings and, for the checker,
+    layer 0's inputs and outputs."""
+    import numpy as np
+    import torch
+    from fable5_llm_amd import stream9b
+    dev = torch.device("cuda", ctx.device)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed + 7)
+    ffn = [(si, mi) for si, s in enumerate(st.sites) for mi, m in enumerate(s.mats)
+           if m.name.split(".")[-1] in ("gate", "up", "down")]
+    stream = torch.cuda.current_stream(dev)
+    out, keep = [], []
+    for B in batches:
+        x8 = {}
+        for K in sorted({st.sites[si].mats[mi].K for si, mi in ffn}):
+            rows = [ctx.dynq8(stream9b.synth_x16(gen, K, stream9b.RS_F).cpu().numpy())[0]
+                    for _ in range(B)]
+            x8[K] = torch.from_numpy(np.stack(rows)).to(dev)
+        y = {n: torch.empty((B, n), dtype=torch.int32, device=dev)
+             for n in {st.sites[si].mats[mi].nrows for si, mi in ffn}}
+        nbytes = ops = 0
+        for si, mi in ffn:
+            m = st.sites[si].mats[mi]
+            nbytes += m.bytes + B * m.K + 4 * B * m.nrows
+            ops += 2 * m.nrows * m.K * B
+
+        def one_pass():
+            for si, mi in ffn:
+                m = st.sites[si].mats[mi]
+                ctx.matmul_async(st.weights[si][mi], x8[m.K], y[m.nrows])
+
+        for _ in range(warmup):
+            one_pass()
+        ctx.sync()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            one_pass()
+        e1.record(stream)
+        ctx.sync()
+        torch.cuda.synchronize(dev)
+        ms = e0.elapsed_time(e1) / steps
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        tops = ops / (ms * 1e-3) / 1e12
+        out.append({"B": B, "matrices": len(ffn), "ms_per_pass": round(ms, 4),
+                    "value": round(gbs, 1), "unit": "GB/s",
+                    "pct_of_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 1),
+                    "tops": round(tops, 2),
+                    "mfma_util_pct": round(100.0 * tops / PEAK_INT8_TOPS, 2),
+                    "bytes_per_pass": nbytes, "kernel": "matmul_kernel"})
+        # layer 0's gate, up and down with their outputs, for the checker
+        for si, mi in ffn[:3]:
+            m = st.sites[si].mats[mi]
+            ctx.matmul_async(st.weights[si][mi], x8[m.K], y[m.nrows])
+            ctx.sync()
+            keep.append((B, si, mi, x8[m.K].cpu().numpy(), y[m.nrows].cpu().numpy()))
+    return out, keep
+
+
+def batched_check(st, keep):
+    """Every kept batched output against B oracle matvec_y32 calls."""
+    import numpy as np
+    from fable5_llm_amd.stream9b import sh_for_k
+    from oracle import cfast
+    bad = 0
+    for B, si, mi, x8, y in keep:
+        m = st.sites[si].mats[mi]
+        img = np.frombuffer(st.weights[si][mi].download(), dtype=np.uint8)
+        for b in range(B):
+            ref = cfast.matvec_y32_img(img, m.nrows, m.K, sh_for_k(m.K), x8[b], 0)
+            bad += int(not np.array_equal(ref, y[b]))
+    return "bit-exact" if bad == 0 else f"MISMATCH in {bad} token rows"
+
+
+def cpu_baseline(st, min_seconds, keep=()):
     """Oracle leg: the C restatement over the full stream, repeated until
-    `min_seconds` of matvec work; returns its rate and the parity check."""
+    `min_seconds` of matvec work; returns its rate and the parity check (of
+    the stream and of the batched leg's kept outputs)."""
     import numpy as np
     from oracle import cfast
     from tests import stream_check as sc
@@ -86,6 +171,7 @@ def cpu_baseline(st, min_seconds):
         "host_cpus": os.cpu_count(),
         "numpy": np.__version__,
         "parity": "bit-exact" if not bad else f"MISMATCH {len(bad)}: {bad[:5]}",
+        "batched_parity": batched_check(st, keep) if keep else None,
     }
 
 
@@ -111,6 +197,9 @@ def main():
                          "or only where it shares a buffer with one")
     ap.add_argument("--no-ordered", action="store_true",
                     help="skip timing the same plan strictly in order (graph mode)")
+    ap.add_argument("--batch", default="8,32",
+                    help="token counts B for the batched int8-MFMA leg over the FFN "
+                         "matrices (comma-separated, each <= 64; empty: skip)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -249,8 +338,13 @@ def main():
     }
     if ordered:
         line["ordered"] = ordered
+    batches = [int(b) for b in args.batch.split(",") if b.strip()]
+    keep = ()
+    if batches:
+        line["batched"], keep = batched_leg(st, ctx, batches, min(args.steps, 50),
+                                            max(3, args.warmup // 10), args.seed)
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(st, args.cpu_seconds)
+        line["cpu_baseline"] = cpu_baseline(st, args.cpu_seconds, keep)
     st.close()
     ctx.close()
     print(json.dumps(line), flush=True)
