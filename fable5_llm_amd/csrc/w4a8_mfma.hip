@@ -8,12 +8,75 @@
 // of A and B alike, so A and B share one lane->k mapping and the dot product
 // does not depend on the order in which the hardware walks k.  D element
 // (4 * (l / 16) + r, l % 16) lands in lane l, register r.
-#include "w4a8_internal.h"
+//
+// One workgroup per CU, 12 wavefronts:
+//
+//  * 8 group wavefronts.  A tile's scale block b covers groups 8b..8b+7;
+//    wavefront w takes group 8b + w of every block, so the 8 read one
+//    block's 8 KiB of weights together.  Each keeps its next kMD 16-byte
+//    weight pieces in flight (uniform buffer loads: the compiler's count of
+//    its outstanding loads is exact, and a wait is for the oldest piece
+//    only).
+//  * up to 3 loader wavefronts copy, with LDS DMA, each block's activations
+//    (B tokens x 1 KiB) and the scale rows of the round's tiles into a ring
+//    of LDS slots, ahead of the group wavefronts, and flag each slot once its
+//    copies have landed.
+//  * 1 store wavefront: at the end of a round the 8 group wavefronts add
+//    their int64 sums into an LDS table (two tables, alternating by round);
+//    the store wavefront rounds, checks and stores the round's y32 and frees
+//    the table.  Group wavefronts thus issue no stores, which would make the
+//    compiler's count of their outstanding loads unknown.
+//
+// A workgroup works through its tiles in rounds of up to TM tiles (TM * CT
+// <= 4, CT = column tiles of 16 tokens), block-major within a round, so that
+// each block's activations serve every tile of the round.  Every wait between wavefronts is bounded: a wait that gives
+// up sets bit 2 of the error word and an abort word, after which no wait of
+// the workgroup polls again, so a launch always drains.
+#include "w4a8_device.h"
 
 namespace w4a8 {
 
+namespace {
+
 typedef int v4i __attribute__((ext_vector_type(4)));
-constexpr int kMaxColTiles = 4;   // B <= 64
+
+constexpr int kMW = 8;                     // group wavefronts 0..7
+constexpr int kML = 3;                     // loader wavefronts 8..10 (at most)
+constexpr int kMStore = kMW + kML;         // the store wavefront, 11
+constexpr int kMThreads = (kMW + kML + 1) * 64;
+constexpr int kMD = 8;                     // weight pieces in flight per group wavefront
+constexpr int kXRow = 1024 + 16;           // LDS bytes per token of a block's activations
+constexpr int kMBufDword3 = 0x00020000;    // raw buffer, 32-bit data format
+constexpr int kMAuxNt = 2;                 // buffer-load cache policy: non-temporal
+constexpr int kRingMax = 8;
+constexpr int kLdsBytes = 160 * 1024;
+
+static_assert(kXRow % 16 == 0, "token rows stay 16-byte aligned");
+
+struct MmParams {
+  const uint8_t *W;     // tile layout
+  const int8_t *x8;     // [B][K]
+  int32_t *y32;         // [B][nrows]
+  int32_t *err;
+  int64_t tile_bytes;
+  int32_t nrows, ntiles, NG, nblk, sh, K, B, CT;
+  int32_t tm;           // tiles per round
+  int32_t R;            // LDS slots
+  int32_t nl;           // loader wavefronts in use
+  int32_t slot_bytes;   // 16 * CT token rows of kXRow, then tm scale rows of 256 B
+};
+
+// LDS: flags, then the reduction tables, then the ring of slots
+struct MmFlags {
+  int32_t ready[kRingMax];   // step whose copies have landed in the slot (-1: none)
+  int32_t done[kMW];         // last step each group wavefront has finished (-1: none)
+  int32_t tgen[2];           // round allowed to add into each table next
+  int32_t tcnt[2];           // group wavefronts that have added this round
+  int32_t abort;
+  int32_t err;
+  int32_t pad[2];
+};
+constexpr int kFlagBytes = (int)((sizeof(MmFlags) + 255) / 256 * 256);
 
 __device__ __forceinline__ int cvt_lo16(uint32_t w) {
   // offset-form low nibbles u = w + 8 -> bytes 16*w (exact int8)
@@ -29,103 +92,347 @@ __device__ __forceinline__ int64_t rshr64_mm(int64_t v, int s) {
   return v >= 0 ? ((v + half) >> s) : -((-v + half) >> s);
 }
 
-__global__ __launch_bounds__(kWG) void matmul_kernel(
-    const uint8_t *W, int32_t nrows, int64_t ntiles, int64_t tile_bytes, int NG,
-    int nblk, int sh, const int8_t *x8, int B, int K, int32_t *y32,
-    int32_t *err) {
-  __shared__ int64_t red[kWaves - 1][kMaxColTiles][4][64];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int q = lane >> 4, c = lane & 15;
-  const int CT = (B + 15) / 16;
-  for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
-    const uint8_t *tb = W + t * tile_bytes;
-    int64_t p[kMaxColTiles][4];
-#pragma unroll
-    for (int ct = 0; ct < kMaxColTiles; ++ct)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) p[ct][r] = 0;
-    for (int b = wave; b < nblk; b += kWaves) {
-      const uint8_t *bb = tb + (int64_t)b * kBlockBytes;
-      uint4 sc[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sc[r] = ldg16_nt(bb + (4 * q + r) * 16);
-      const int ng = min(kGroupsPerBlock, NG - b * kGroupsPerBlock);
-      for (int i = 0; i < ng; ++i) {
-        const int g = b * kGroupsPerBlock + i;
-        const uint4 wp = ldg16_nt(bb + kScaleChunk + i * kGroupChunk + (c * 4 + q) * 16);
-        const v4i a0 = {cvt_lo16(wp.x), cvt_hi16(wp.x), cvt_lo16(wp.y), cvt_hi16(wp.y)};
-        const v4i a1 = {cvt_lo16(wp.z), cvt_hi16(wp.z), cvt_lo16(wp.w), cvt_hi16(wp.w)};
-        uint32_t m[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const uint32_t w = (i >> 1) == 0 ? sc[r].x
-                           : (i >> 1) == 1 ? sc[r].y
-                           : (i >> 1) == 2 ? sc[r].z : sc[r].w;
-          m[r] = (i & 1) ? (w >> 16) : (w & 0xFFFFu);
-        }
-#pragma unroll
-        for (int ct = 0; ct < kMaxColTiles; ++ct) {
-          if (ct < CT) {
-            const int tok = ct * 16 + c;
-            v4i b0 = {0, 0, 0, 0}, b1 = {0, 0, 0, 0};
-            if (tok < B) {
-              const int8_t *xp = x8 + (int64_t)tok * K + kGroup * g + 32 * q;
-              const int4 u0 = *(const int4 *)xp, u1 = *(const int4 *)(xp + 16);
-              b0 = v4i{u0.x, u0.y, u0.z, u0.w};
-              b1 = v4i{u1.x, u1.y, u1.z, u1.w};
-            }
-            v4i acc = {0, 0, 0, 0};
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, acc, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              p[ct][r] += (int64_t)(int32_t)m[r] * (int64_t)acc[r];
-          }
-        }
+__device__ __forceinline__ void mm_wait_vm_all() {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+__device__ __forceinline__ void mm_lds_add_u64(int64_t *p, int64_t v) {
+  asm volatile("ds_add_u64 %0, %1" :: "v"(lds_off(p)), "v"(v) : "memory");
+}
+__device__ __forceinline__ int32_t mm_lds_add_rtn(int32_t *p, int32_t v) {
+  int32_t old;
+  asm volatile("s_waitcnt lgkmcnt(0)\n\tds_add_rtn_u32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)"
+               : "=v"(old) : "v"(lds_off(p)), "v"(v) : "memory");
+  return old;
+}
+__device__ __forceinline__ void mm_lds_or(int32_t *p, int32_t v) {
+  asm volatile("ds_or_b32 %0, %1" :: "v"(lds_off(p)), "v"(v) : "memory");
+}
+// lane l copies 16 (or 4) bytes from its own address to LDS lds_base + 16 l
+// (4 l); lds_base must be uniform
+__device__ __forceinline__ void dma16(const void *src, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(src), "s"(lds_base) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void *src, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off"
+               :: "v"(src), "s"(lds_base) : "memory", "m0");
+}
+
+// Bounded LDS wait of one wavefront: until every lane's predicate holds,
+// the workgroup aborts, or kLdsSpin polls (then bit 2 of err and abort).
+template <typename Pred>
+__device__ __forceinline__ bool mm_wait(MmFlags &F, Pred pred) {
+  for (uint32_t n = 0;; ++n) {
+    if (__all(pred())) return true;
+    if (lds_read_i32(&F.abort) != 0) return false;
+    if (n > kLdsSpin) {
+      if ((threadIdx.x & 63) == 0) {
+        lds_write_i32(&F.abort, 1);
+        mm_lds_or(&F.err, 4);
       }
+      return false;
     }
-    if (wave > 0) {
-#pragma unroll
-      for (int ct = 0; ct < kMaxColTiles; ++ct)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) red[wave - 1][ct][r][lane] = p[ct][r];
-    }
-    __syncthreads();
-    if (wave == 0) {
-#pragma unroll
-      for (int ct = 0; ct < kMaxColTiles; ++ct) {
-        if (ct < CT) {
-          const int tok = ct * 16 + c;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            int64_t tot = p[ct][r];
-#pragma unroll
-            for (int w = 0; w < kWaves - 1; ++w) tot += red[w][ct][r][lane];
-            const int64_t row = t * kTileRows + 4 * q + r;
-            if (tok < B && row < nrows) {
-              const int64_t y = rshr64_mm(tot >> 4, sh);
-              if (y > 2147483647LL || y < -2147483647LL) atomicOr(err, 1);
-              y32[(int64_t)tok * nrows + row] = (int32_t)y;
-            }
-          }
-        }
-      }
-    }
-    __syncthreads();
+    __builtin_amdgcn_s_sleep(1);
   }
 }
+
+// The same wait for a group wavefront, as a loop of plain exits (the form
+// in which the compiler keeps its count of outstanding weight loads across
+// it): until the LDS word at p is at least v (kAtLeast) or equal to v.
+template <bool kAtLeast>
+__device__ __forceinline__ void mm_wait_word(MmFlags &F, const int32_t *p, int v, int lane) {
+  for (uint32_t n = 0;; ++n) {
+    const int32_t cur = lds_read_i32(p);
+    if (__all(kAtLeast ? cur >= v : cur == v)) break;
+    if (lds_read_i32(&F.abort) != 0) break;
+    if (n > kLdsSpin) {
+      if (lane == 0) {
+        lds_write_i32(&F.abort, 1);
+        mm_lds_or(&F.err, 4);
+      }
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// A workgroup's items: round rho (tiles rho*tm .. of its own tiles r, r+G,
+// ...), block kb, tile j of the round.  Step = rho * nblk + kb.
+struct MCur {
+  int rho, kb, j, nt;
+};
+__device__ __forceinline__ int round_tiles(const MmParams &P, int nmine, int rho) {
+  return min(P.tm, nmine - rho * P.tm);
+}
+__device__ __forceinline__ void mcur_next(const MmParams &P, int nmine, MCur &c) {
+  if (++c.j < c.nt) return;
+  c.j = 0;
+  if (++c.kb < P.nblk) return;
+  c.kb = 0;
+  ++c.rho;
+  c.nt = c.rho * P.tm < nmine ? round_tiles(P, nmine, c.rho) : 0;
+}
+
+// Put item c's piece of group 8 kb + w in flight (a buffer load whose range
+// is empty past the end, or for a group past NG: no memory access).
+__device__ __forceinline__ uint4 mm_issue(const MmParams &P, int r, int G, int w, int lane,
+                                          const MCur &c) {
+  const uint8_t *base = P.W;
+  int len = 0;
+  if (c.nt > 0 && 8 * c.kb + w < P.NG) {
+    const int64_t t = (int64_t)r + (int64_t)G * (c.rho * P.tm + c.j);
+    base = P.W + t * P.tile_bytes + (int64_t)c.kb * kBlockBytes + kScaleChunk +
+           (int64_t)w * kGroupChunk;
+    len = kGroupChunk;
+  }
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, len, kMBufDword3);
+  // lane (c = l % 16, q = l / 16) takes row c's quarter q: bytes (4c + q) * 16
+  const int piece = ((lane & 15) * 4 + (lane >> 4)) * 16;
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  const u4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, piece, 0, kMAuxNt);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+template <int TMX, int CTX>
+__global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  MmFlags &F = *(MmFlags *)smem;
+  int64_t *tables = (int64_t *)(smem + kFlagBytes);   // [2][TMX][CTX][4][64]
+  uint8_t *ring = smem + kFlagBytes + 2 * TMX * CTX * 4 * 64 * 8;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = gridDim.x, r = blockIdx.x;
+  const int nmine = r < P.ntiles ? (P.ntiles - 1 - r) / G + 1 : 0;
+  const int nrounds = (nmine + P.tm - 1) / P.tm;
+  const int nsteps = nrounds * P.nblk;
+
+  if (tid < kRingMax) F.ready[tid] = -1;
+  if (tid < kMW) F.done[tid] = -1;
+  if (tid < 2) {
+    F.tgen[tid] = tid;
+    F.tcnt[tid] = 0;
+  }
+  if (tid == 0) {
+    F.abort = 0;
+    F.err = 0;
+  }
+  for (int i = tid; i < 2 * TMX * CTX * 4 * 64; i += kMThreads) tables[i] = 0;
+  __syncthreads();
+
+  if (wave == kMStore) {
+    // round rho's sums are complete once all 8 group wavefronts have added
+    bool ok = true;
+    for (int rho = 0; rho < nrounds; ++rho) {
+      const int tb = rho & 1, nt = round_tiles(P, nmine, rho);
+      int64_t *tbl = tables + tb * (TMX * CTX * 4 * 64);
+      if (!mm_wait(F, [&] { return lds_read_i32(&F.tcnt[tb]) == kMW; })) {
+        ok = false;
+        break;
+      }
+      const int q = lane >> 4, c = lane & 15;
+      for (int jj = 0; jj < nt; ++jj) {
+        const int64_t t = (int64_t)r + (int64_t)G * (rho * P.tm + jj);
+        for (int ct = 0; ct < P.CT; ++ct) {
+          for (int e = 0; e < 4; ++e) {
+            int64_t &v = tbl[((jj * CTX + ct) * 4 + e) * 64 + lane];
+            const int64_t tot = v;
+            v = 0;
+            const int64_t row = t * kTileRows + 4 * q + e;
+            const int tok = ct * 16 + c;
+            if (tok < P.B && row < P.nrows) {
+              const int64_t y = rshr64_mm(tot >> 4, P.sh);   // tot = 16 p
+              if (y > 2147483647LL || y < -2147483647LL) mm_lds_or(&F.err, 1);
+              P.y32[(int64_t)tok * P.nrows + row] = (int32_t)y;
+            }
+          }
+        }
+      }
+      wait_lds();
+      if (lane == 0) {
+        lds_write_i32(&F.tcnt[tb], 0);
+        lds_write_i32(&F.tgen[tb], rho + 2);
+      }
+    }
+    if (!ok && lane == 0) mm_lds_or(&F.err, 4);
+  } else if (wave >= kMW) {
+    // loader l: steps l, l + nl, ...
+    const int l = wave - kMW;
+    if (l < P.nl) {
+      for (int s = l; s < nsteps; s += P.nl) {
+        const int rho = s / P.nblk, kb = s - rho * P.nblk;
+        const int slot = s % P.R;
+        // the slot's previous step has been consumed by every group wavefront
+        if (s >= P.R &&
+            !mm_wait(F, [&] { return lds_read_i32(&F.done[lane & (kMW - 1)]) >= s - P.R; }))
+          break;
+        uint8_t *sb = ring + (size_t)slot * P.slot_bytes;
+        const int kbytes = min(1024, P.K - kb * 1024);   // multiple of 128
+        for (int tok = 0; tok < P.B; ++tok) {
+          const int8_t *src = 16 * lane < kbytes
+                                  ? P.x8 + (int64_t)tok * P.K + kb * 1024 + 16 * lane
+                                  : P.x8;   // nothing to copy: any mapped address
+          dma16(src, lds_off(sb + tok * kXRow));
+        }
+        const int nt = round_tiles(P, nmine, rho);
+        for (int j = 0; j < nt; ++j) {
+          const int64_t t = (int64_t)r + (int64_t)G * (rho * P.tm + j);
+          dma4(P.W + t * P.tile_bytes + (int64_t)kb * kBlockBytes + 4 * lane,
+               lds_off(sb + 16 * P.CT * kXRow + 256 * j));
+        }
+        mm_wait_vm_all();
+        if (lane == 0) lds_write_i32(&F.ready[slot], s);
+      }
+    }
+  } else {
+    const int w = wave;
+    const int q = lane >> 4, c = lane & 15;
+    int64_t p[TMX][CTX][4];
+#pragma unroll
+    for (int a = 0; a < TMX; ++a)
+#pragma unroll
+      for (int b = 0; b < CTX; ++b)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) p[a][b][e] = 0;
+    MCur cur{0, 0, 0, nmine > 0 ? round_tiles(P, nmine, 0) : 0};
+    MCur fill = cur;
+    uint4 wr[kMD];
+#pragma unroll
+    for (int d = 0; d < kMD; ++d) {
+      wr[d] = mm_issue(P, r, G, w, lane, fill);
+      mcur_next(P, nmine, fill);
+    }
+    for (;;) {
+#pragma unroll
+      for (int d = 0; d < kMD; ++d) {
+        if (cur.nt == 0) goto finished;
+        const int s = cur.rho * P.nblk + cur.kb;
+        const int slot = s % P.R;
+        if (cur.j == 0) mm_wait_word<false>(F, &F.ready[slot], s, lane);
+        const uint8_t *sb = ring + (size_t)slot * P.slot_bytes;
+        {
+          const uint4 wp = wr[d];
+          const v4i a0 = {cvt_lo16(wp.x), cvt_hi16(wp.x), cvt_lo16(wp.y), cvt_hi16(wp.y)};
+          const v4i a1 = {cvt_lo16(wp.z), cvt_hi16(wp.z), cvt_lo16(wp.w), cvt_hi16(wp.w)};
+          // this group's scales of rows 4q .. 4q+3 (row rr's 16 bytes hold
+          // the block's 8 uint16 scales)
+          const uint8_t *scl = sb + 16 * P.CT * kXRow + 256 * cur.j;
+          int32_t m[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            m[e] = *(const uint16_t *)(scl + (4 * q + e) * 16 + 2 * w);
+#pragma unroll
+          for (int ct = 0; ct < CTX; ++ct) {
+            if (ct < P.CT) {
+              const int8_t *xr = (const int8_t *)sb + (16 * ct + c) * kXRow + w * 128 + 32 * q;
+              const int4 u0 = *(const int4 *)xr, u1 = *(const int4 *)(xr + 16);
+              const v4i b0 = {u0.x, u0.y, u0.z, u0.w}, b1 = {u1.x, u1.y, u1.z, u1.w};
+              v4i acc = {0, 0, 0, 0};
+              acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, acc, 0, 0, 0);
+              acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, acc, 0, 0, 0);
+#pragma unroll
+              for (int jj = 0; jj < TMX; ++jj)
+                if (jj == cur.j)
+#pragma unroll
+                  for (int e = 0; e < 4; ++e)
+                    p[jj][ct][e] += (int64_t)m[e] * (int64_t)acc[e];
+            }
+          }
+        }
+        // refill this register with the item kMD ahead
+        wr[d] = mm_issue(P, r, G, w, lane, fill);
+        mcur_next(P, nmine, fill);
+        const bool step_end = cur.j == cur.nt - 1;
+        const bool round_end = step_end && cur.kb == P.nblk - 1;
+        if (step_end) {
+          wait_lds();   // this wavefront's reads of the slot are done
+          if (lane == 0) lds_write_i32(&F.done[w], s);
+        }
+        if (round_end) {
+          const int rho = cur.rho, nt = cur.nt, tb = rho & 1;
+          int64_t *tbl = tables + tb * (TMX * CTX * 4 * 64);
+          mm_wait_word<true>(F, &F.tgen[tb], rho, lane);
+#pragma unroll
+          for (int jj = 0; jj < TMX; ++jj)
+#pragma unroll
+            for (int ct = 0; ct < CTX; ++ct)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                if (jj < nt && ct < P.CT)
+                  mm_lds_add_u64(&tbl[((jj * CTX + ct) * 4 + e) * 64 + lane], p[jj][ct][e]);
+                p[jj][ct][e] = 0;
+              }
+          wait_lds();   // the adds are done before the count
+          if (lane == 0) mm_lds_add_rtn(&F.tcnt[tb], 1);
+        }
+        mcur_next(P, nmine, cur);
+      }
+    }
+  finished:;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    const int32_t e = lds_read_i32(&F.err);
+    if (e) atomicOr(P.err, e);
+  }
+}
+
+}  // namespace
 
 hipError_t launch_matmul(const uint8_t *w, int32_t nrows, const Layout &L, int32_t sh,
                          const int8_t *x8, int32_t B, int32_t *y32, int32_t *err,
                          hipStream_t s) {
-  const int64_t ntiles = (nrows + kTileRows - 1) / kTileRows;
+  MmParams P{};
+  P.W = w;
+  P.x8 = x8;
+  P.y32 = y32;
+  P.err = err;
+  P.tile_bytes = L.tile_bytes;
+  P.nrows = nrows;
+  P.ntiles = (nrows + kTileRows - 1) / kTileRows;
+  P.NG = L.NG;
+  P.nblk = L.nblk;
+  P.sh = sh;
+  P.K = L.K;
+  P.B = B;
+  P.CT = (B + 15) / 16;
+  const int tmx = P.CT == 1 ? 4 : (P.CT == 2 ? 2 : 1);
+  const int table_bytes = 2 * tmx * (tmx == 4 ? 1 : (tmx == 2 ? 2 : 4)) * 4 * 64 * 8;
+  P.slot_bytes = 16 * P.CT * kXRow + tmx * 256;
+  const int avail = kLdsBytes - kFlagBytes - table_bytes;
+  P.R = avail / P.slot_bytes;
+  if (P.R > kRingMax) P.R = kRingMax;
+  if (P.R < 2) return hipErrorInvalidValue;
+  P.nl = P.R - 1 < kML ? P.R - 1 : kML;   // >= 1: R >= 2
   int dev = 0, ncu = 256;
   if (hipGetDevice(&dev) == hipSuccess)
     (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
-  const int64_t cap = (int64_t)ncu * 4;
-  const int grid = (int)(ntiles < cap ? ntiles : cap);
-  hipLaunchKernelGGL(matmul_kernel, dim3(grid), dim3(kWG), 0, s, w, nrows, ntiles,
-                     L.tile_bytes, L.NG, L.nblk, sh, x8, B, L.K, y32, err);
+  // rounds of tm tiles: as many tiles per round as the workgroups' shares
+  // allow, at most tmx
+  const int G = P.ntiles < ncu ? P.ntiles : ncu;
+  const int per = (P.ntiles + G - 1) / G;
+  P.tm = per < tmx ? per : tmx;
+  const size_t lds = (size_t)kFlagBytes + table_bytes + (size_t)P.R * P.slot_bytes;
+  // dynamic LDS beyond the default limit: allowed once per process
+  static const hipError_t attr = [] {
+    hipError_t e = hipFuncSetAttribute((const void *)matmul_kernel<4, 1>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute((const void *)matmul_kernel<2, 2>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute((const void *)matmul_kernel<1, 4>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    return e;
+  }();
+  if (attr != hipSuccess) return attr;
+  if (P.CT == 1) {
+    hipLaunchKernelGGL((matmul_kernel<4, 1>), dim3(G), dim3(kMThreads), lds, s, P);
+  } else if (P.CT == 2) {
+    hipLaunchKernelGGL((matmul_kernel<2, 2>), dim3(G), dim3(kMThreads), lds, s, P);
+  } else {
+    hipLaunchKernelGGL((matmul_kernel<1, 4>), dim3(G), dim3(kMThreads), lds, s, P);
+  }
   return hipGetLastError();
 }
 
