@@ -44,7 +44,7 @@ constexpr int kMW = 8;                     // group wavefronts 0..7
 constexpr int kML = 3;                     // loader wavefronts 8..10 (at most)
 constexpr int kMStore = kMW + kML;         // the store wavefront, 11
 constexpr int kMThreads = (kMW + kML + 1) * 64;
-constexpr int kMD = 8;                     // weight pieces in flight per group wavefront
+constexpr int kMD = 16;                    // weight pieces in flight per group wavefront
 constexpr int kXRow = 1024 + 16;           // LDS bytes per token of a block's activations
 constexpr int kMBufDword3 = 0x00020000;    // raw buffer, 32-bit data format
 constexpr int kMAuxNt = 2;                 // buffer-load cache policy: non-temporal
@@ -156,32 +156,23 @@ __device__ __forceinline__ void mm_wait_word(MmFlags &F, const int32_t *p, int v
   }
 }
 
-// A workgroup's items: round rho (tiles rho*tm .. of its own tiles r, r+G,
-// ...), block kb, tile j of the round.  Step = rho * nblk + kb.
-struct MCur {
-  int rho, kb, j, nt;
-};
+// A workgroup's tiles are r, r + G, ...; round rho takes tiles rho*tm ..
+// rho*tm + nt - 1 of them, and step s = rho * nblk + kb covers block kb of
+// every tile of round rho.
 __device__ __forceinline__ int round_tiles(const MmParams &P, int nmine, int rho) {
   return min(P.tm, nmine - rho * P.tm);
 }
-__device__ __forceinline__ void mcur_next(const MmParams &P, int nmine, MCur &c) {
-  if (++c.j < c.nt) return;
-  c.j = 0;
-  if (++c.kb < P.nblk) return;
-  c.kb = 0;
-  ++c.rho;
-  c.nt = c.rho * P.tm < nmine ? round_tiles(P, nmine, c.rho) : 0;
-}
 
-// Put item c's piece of group 8 kb + w in flight (a buffer load whose range
-// is empty past the end, or for a group past NG: no memory access).
+// Put group 8 kb + w of tile j of round rho in flight: a buffer load whose
+// range is empty (no memory access, zeros) when there is no such tile or
+// group, so every step issues the same loads.
 __device__ __forceinline__ uint4 mm_issue(const MmParams &P, int r, int G, int w, int lane,
-                                          const MCur &c) {
+                                          int rho, int kb, int j, bool real) {
   const uint8_t *base = P.W;
   int len = 0;
-  if (c.nt > 0 && 8 * c.kb + w < P.NG) {
-    const int64_t t = (int64_t)r + (int64_t)G * (c.rho * P.tm + c.j);
-    base = P.W + t * P.tile_bytes + (int64_t)c.kb * kBlockBytes + kScaleChunk +
+  if (real && 8 * kb + w < P.NG) {
+    const int64_t t = (int64_t)r + (int64_t)G * (rho * P.tm + j);
+    base = P.W + t * P.tile_bytes + (int64_t)kb * kBlockBytes + kScaleChunk +
            (int64_t)w * kGroupChunk;
     len = kGroupChunk;
   }
@@ -193,6 +184,10 @@ __device__ __forceinline__ uint4 mm_issue(const MmParams &P, int r, int G, int w
   const u4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, piece, 0, kMAuxNt);
   return make_uint4(v.x, v.y, v.z, v.w);
 }
+
+// steps in flight per group wavefront: TMX pieces each
+template <int TMX>
+constexpr int mm_depth() { return TMX >= 4 ? 4 : 8; }
 
 template <int TMX, int CTX>
 __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
@@ -287,6 +282,7 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
   } else {
     const int w = wave;
     const int q = lane >> 4, c = lane & 15;
+    constexpr int D = mm_depth<TMX>();
     int64_t p[TMX][CTX][4];
 #pragma unroll
     for (int a = 0; a < TMX; ++a)
@@ -294,62 +290,72 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
       for (int b = 0; b < CTX; ++b)
 #pragma unroll
         for (int e = 0; e < 4; ++e) p[a][b][e] = 0;
-    MCur cur{0, 0, 0, nmine > 0 ? round_tiles(P, nmine, 0) : 0};
-    MCur fill = cur;
-    uint4 wr[kMD];
+    // wr[j][d]: tile j's piece of the step s with s % D == d
+    uint4 wr[TMX][D];
+    int f_rho = 0, f_kb = 0;   // next step to put in flight
+    auto fill = [&](uint4 (&slot)[TMX][D], const int d) {
+      const int nt = f_rho < nrounds ? round_tiles(P, nmine, f_rho) : 0;
 #pragma unroll
-    for (int d = 0; d < kMD; ++d) {
-      wr[d] = mm_issue(P, r, G, w, lane, fill);
-      mcur_next(P, nmine, fill);
-    }
+      for (int j = 0; j < TMX; ++j)
+        slot[j][d] = mm_issue(P, r, G, w, lane, f_rho, f_kb, j, j < nt);
+      if (++f_kb == P.nblk) {
+        f_kb = 0;
+        ++f_rho;
+      }
+    };
+#pragma unroll
+    for (int d = 0; d < D; ++d) fill(wr, d);
+    int s = 0, rho = 0, kb = 0;
     for (;;) {
 #pragma unroll
-      for (int d = 0; d < kMD; ++d) {
-        if (cur.nt == 0) goto finished;
-        const int s = cur.rho * P.nblk + cur.kb;
+      for (int d = 0; d < D; ++d) {
+        if (s >= nsteps) goto finished;
+        const int nt = round_tiles(P, nmine, rho);
         const int slot = s % P.R;
-        if (cur.j == 0) mm_wait_word<false>(F, &F.ready[slot], s, lane);
+        mm_wait_word<false>(F, &F.ready[slot], s, lane);
         const uint8_t *sb = ring + (size_t)slot * P.slot_bytes;
-        {
-          const uint4 wp = wr[d];
-          const v4i a0 = {cvt_lo16(wp.x), cvt_hi16(wp.x), cvt_lo16(wp.y), cvt_hi16(wp.y)};
-          const v4i a1 = {cvt_lo16(wp.z), cvt_hi16(wp.z), cvt_lo16(wp.w), cvt_hi16(wp.w)};
-          // this group's scales of rows 4q .. 4q+3 (row rr's 16 bytes hold
-          // the block's 8 uint16 scales)
-          const uint8_t *scl = sb + 16 * P.CT * kXRow + 256 * cur.j;
-          int32_t m[4];
+        // this group's activations for the step's tokens: lane (c, q) feeds
+        // token 16 ct + c, k = 128 w + 32 q + [0, 32)
+        v4i bx[CTX][2];
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            m[e] = *(const uint16_t *)(scl + (4 * q + e) * 16 + 2 * w);
+        for (int ct = 0; ct < CTX; ++ct) {
+          const int8_t *xr = (const int8_t *)sb + (16 * ct + c) * kXRow + w * 128 + 32 * q;
+          const int4 u0 = *(const int4 *)xr, u1 = *(const int4 *)(xr + 16);
+          bx[ct][0] = v4i{u0.x, u0.y, u0.z, u0.w};
+          bx[ct][1] = v4i{u1.x, u1.y, u1.z, u1.w};
+        }
 #pragma unroll
-          for (int ct = 0; ct < CTX; ++ct) {
-            if (ct < P.CT) {
-              const int8_t *xr = (const int8_t *)sb + (16 * ct + c) * kXRow + w * 128 + 32 * q;
-              const int4 u0 = *(const int4 *)xr, u1 = *(const int4 *)(xr + 16);
-              const v4i b0 = {u0.x, u0.y, u0.z, u0.w}, b1 = {u1.x, u1.y, u1.z, u1.w};
-              v4i acc = {0, 0, 0, 0};
-              acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, acc, 0, 0, 0);
-              acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, acc, 0, 0, 0);
+        for (int j = 0; j < TMX; ++j) {
+          if (j < nt) {
+            const uint4 wp = wr[j][d];
+            const v4i a0 = {cvt_lo16(wp.x), cvt_hi16(wp.x), cvt_lo16(wp.y), cvt_hi16(wp.y)};
+            const v4i a1 = {cvt_lo16(wp.z), cvt_hi16(wp.z), cvt_lo16(wp.w), cvt_hi16(wp.w)};
+            // this group's scales of rows 4q .. 4q+3 (row rr's 16 bytes hold
+            // the block's 8 uint16 scales)
+            const uint8_t *scl = sb + 16 * P.CT * kXRow + 256 * j;
+            int32_t m[4];
 #pragma unroll
-              for (int jj = 0; jj < TMX; ++jj)
-                if (jj == cur.j)
+            for (int e = 0; e < 4; ++e)
+              m[e] = *(const uint16_t *)(scl + (4 * q + e) * 16 + 2 * w);
 #pragma unroll
-                  for (int e = 0; e < 4; ++e)
-                    p[jj][ct][e] += (int64_t)m[e] * (int64_t)acc[e];
+            for (int ct = 0; ct < CTX; ++ct) {
+              if (ct < P.CT) {
+                v4i acc = {0, 0, 0, 0};
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bx[ct][0], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bx[ct][1], acc, 0, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) p[j][ct][e] += (int64_t)m[e] * (int64_t)acc[e];
+              }
             }
           }
         }
-        // refill this register with the item kMD ahead
-        wr[d] = mm_issue(P, r, G, w, lane, fill);
-        mcur_next(P, nmine, fill);
-        const bool step_end = cur.j == cur.nt - 1;
-        const bool round_end = step_end && cur.kb == P.nblk - 1;
-        if (step_end) {
-          wait_lds();   // this wavefront's reads of the slot are done
-          if (lane == 0) lds_write_i32(&F.done[w], s);
-        }
-        if (round_end) {
-          const int rho = cur.rho, nt = cur.nt, tb = rho & 1;
+        // refill this step's registers with the step D ahead
+        fill(wr, d);
+        wait_lds();   // this wavefront's reads of the slot are done
+        if (lane == 0) lds_write_i32(&F.done[w], s);
+        if (kb == P.nblk - 1) {
+          // end of round rho: add this wavefront's sums into its table
+          const int tb = rho & 1;
           int64_t *tbl = tables + tb * (TMX * CTX * 4 * 64);
           mm_wait_word<true>(F, &F.tgen[tb], rho, lane);
 #pragma unroll
@@ -364,8 +370,12 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
               }
           wait_lds();   // the adds are done before the count
           if (lane == 0) mm_lds_add_rtn(&F.tcnt[tb], 1);
+          kb = 0;
+          ++rho;
+        } else {
+          ++kb;
         }
-        mcur_next(P, nmine, cur);
+        ++s;
       }
     }
   finished:;
