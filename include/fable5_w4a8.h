@@ -192,7 +192,7 @@ int w4a8_matmul_y32_async(w4a8_ctx *ctx, const w4a8_weights *w,
                                    workgroup is resident (for a GPU shared
                                    with other long-running kernels); the
                                    runtime's cooperative dispatch costs about
-                                   17 us per launch on MI355X */
+                                   23 us per launch on MI355X */
 /* fences of a persistent plan */
 #define W4A8_FENCE_ALL   0 /* (default) every site waits for all earlier ones */
 #define W4A8_FENCE_AUTO  1 /* a site waits only when it reads a buffer an
