@@ -18,6 +18,8 @@ chain of dependent sites).
 Prints one JSON line.  `value` = stream bytes / wall time per step.
 `roofline` = the dominant kernel alone: stream bytes / sum of its per-launch
 durations, each launch bracketed by dispatch-recorded HIP events.
+`ffn` = one layer's SwiGLU block per call (w4a8_mlp_async) over the 32
+layers, with the residual add.
 `batched` = the int8-MFMA kernel over the stream's 96 FFN matrices at B
 tokens per pass (--batch), with its GB/s and MFMA utilisation.
 `cpu_baseline` = the C oracle (oracle/law_c.c, OpenMP) over the same stream
@@ -120,6 +122,87 @@ def batched_leg(st, ctx, batches, steps, warmup, seed):
     return out, keep
 
 
+def ffn_leg(st, ctx, steps, warmup):
+    """One decoder layer's FFN block per call (w4a8_mlp_async: RMSNorm ->
+    DYNQ8 -> gate SILU32 / up SHIFT32W -> EMUL32 -> DYNQ8 -> down -> residual
+    ADD) for each of the stream's 32 layers in turn: 77.9 MB of weights per
+    call, 2.49 GB per pass.  Returns the timing and, for the checker, layer
+    0's input and outputs."""
+    import torch
+    dev = torch.device("cuda", ctx.device)
+    stream = torch.cuda.current_stream(dev)
+    layers = []
+    for si, s in enumerate(st.sites):
+        if s.name.endswith(".ln2"):
+            down = st.sites[si + 1]
+            assert down.name.endswith(".swiglu")
+            g, u = s.mats
+            d = down.mats[0]
+            p0s = [g.p0(s.in_f), u.p0(s.in_f), d.p0(down.in_f)]
+            x, nw = st.inputs[si]
+            y = torch.empty(d.nrows, dtype=torch.int16, device=dev)
+            res = torch.empty(d.nrows, dtype=torch.int16, device=dev)
+            nbytes = g.bytes + u.bytes + d.bytes
+            layers.append((si, st.weights[si][0], st.weights[si][1], st.weights[si + 1][0],
+                           p0s, x, nw, s, y, res, nbytes))
+
+    def one_pass():
+        for (_si, wg, wu, wd, p0s, x, nw, s, y, res, _b) in layers:
+            ctx.mlp_async(wg, wu, wd, p0s, x, norm_w=nw, in_f=s.in_f,
+                          one_plus=s.one_plus, mlp_out=y, res_out=res)
+
+    for _ in range(warmup):
+        one_pass()
+    ctx.sync()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        one_pass()
+    e1.record(stream)
+    ctx.sync()
+    torch.cuda.synchronize(dev)
+    ms = e0.elapsed_time(e1) / steps
+    nbytes = sum(l[-1] for l in layers)
+    si, wg, wu, wd, p0s, x, nw, s, y, res, _ = layers[0]
+    keep = (si, p0s, x.cpu().numpy(), nw.cpu().numpy(), y.cpu().numpy(), res.cpu().numpy())
+    return {"layers": len(layers), "ms_per_pass": round(ms, 4),
+            "us_per_layer": round(ms * 1e3 / len(layers), 2),
+            "value": round(nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s",
+            "pct_of_peak_hbm": round(100.0 * nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 1),
+            "bytes_per_pass": nbytes, "launches_per_layer": 4,
+            "chain": "RMSNorm->DYNQ8->gate SILU32 + up SHIFT32W (one launch), EMUL32, "
+                     "DYNQ8->down SHIFT32, residual ADD"}, keep
+
+
+def ffn_check(st, keep):
+    """Layer 0's FFN block against the oracle: law.py for RMSNorm, DYNQ8,
+    SILU32, EMUL32 and the shifts, oracle/law_c.c for the matvecs."""
+    import numpy as np
+    from fable5_llm_amd.stream9b import sh_for_k
+    from oracle import cfast, law
+    si, p0s, x16, nw, y, res = keep
+    s, d = st.sites[si], st.sites[si + 1]
+    imgs = [np.frombuffer(w.download(), dtype=np.uint8) for w in
+            (st.weights[si][0], st.weights[si][1], st.weights[si + 1][0])]
+    mats = (s.mats[0], s.mats[1], d.mats[0])
+
+    def mv(k, x):
+        m = mats[k]
+        x8, e_x = law.dyn_quant_i8(x)
+        yy = cfast.matvec_y32_img(imgs[k], m.nrows, m.K, sh_for_k(m.K), x8, 0)
+        return law.rs_s(yy.astype(np.int64), p0s[k] - e_x)
+    xn = law.rmsnorm_fx(x16, nw, s.in_f, s.one_plus)
+    g, u = mv(0, xn), mv(1, xn)
+    sg = law.clip16(np.array([law.silu_q(int(np.clip(v, -(1 << 20), (1 << 20) - 1)))
+                              for v in g], dtype=np.int64))
+    prod = law.clip16(law.rshift_round(sg * law.clip32(u), 12))
+    ref_y = law.clip16(mv(2, prod))
+    ok = np.array_equal(y.astype(np.int64), ref_y) and np.array_equal(
+        res.astype(np.int64), law.clip16(x16.astype(np.int64) + ref_y))
+    return "bit-exact" if ok else "MISMATCH"
+
+
 def batched_check(st, keep):
     """Every kept batched output against B oracle matvec_y32 calls."""
     import numpy as np
@@ -135,7 +218,7 @@ def batched_check(st, keep):
     return "bit-exact" if bad == 0 else f"MISMATCH in {bad} token rows"
 
 
-def cpu_baseline(st, min_seconds, keep=()):
+def cpu_baseline(st, min_seconds, keep=(), keep_ffn=None):
     """Oracle leg: the C restatement over the full stream, repeated until
     `min_seconds` of matvec work; returns its rate and the parity check (of
     the stream and of the batched leg's kept outputs)."""
@@ -172,6 +255,7 @@ def cpu_baseline(st, min_seconds, keep=()):
         "numpy": np.__version__,
         "parity": "bit-exact" if not bad else f"MISMATCH {len(bad)}: {bad[:5]}",
         "batched_parity": batched_check(st, keep) if keep else None,
+        "ffn_parity": ffn_check(st, keep_ffn) if keep_ffn else None,
     }
 
 
@@ -197,6 +281,8 @@ def main():
                          "or only where it shares a buffer with one")
     ap.add_argument("--no-ordered", action="store_true",
                     help="skip timing the same plan strictly in order (graph mode)")
+    ap.add_argument("--no-ffn", action="store_true",
+                    help="skip the FFN-block leg (w4a8_mlp_async per layer)")
     ap.add_argument("--batch", default="8,32",
                     help="token counts B for the batched int8-MFMA leg over the FFN "
                          "matrices (comma-separated, each <= 64; empty: skip)")
@@ -343,8 +429,12 @@ def main():
     if batches:
         line["batched"], keep = batched_leg(st, ctx, batches, min(args.steps, 50),
                                             max(3, args.warmup // 10), args.seed)
+    keep_ffn = None
+    if not args.no_ffn:
+        line["ffn"], keep_ffn = ffn_leg(st, ctx, min(args.steps, 50),
+                                        max(3, args.warmup // 10))
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(st, args.cpu_seconds, keep)
+        line["cpu_baseline"] = cpu_baseline(st, args.cpu_seconds, keep, keep_ffn)
     st.close()
     ctx.close()
     print(json.dumps(line), flush=True)

@@ -29,6 +29,8 @@ struct w4a8_ctx {
   int32_t *d_result = nullptr;   // head argmax {idx, val}
   uint8_t *d_stage = nullptr;
   size_t stage_cap = 0;
+  uint8_t *d_chain = nullptr;   // temporaries of device-side chains (w4a8_mlp_async)
+  size_t chain_cap = 0;
   int32_t h_tables[kTableLen];
 };
 
@@ -347,6 +349,7 @@ int w4a8_ctx_destroy(w4a8_ctx *c) {
   (void)hipFree(c->d_partials);
   (void)hipFree(c->d_result);
   (void)hipFree(c->d_stage);
+  (void)hipFree(c->d_chain);
   if (c->own) (void)hipStreamDestroy(c->own);
   delete c;
   return W4A8_OK;
@@ -730,6 +733,61 @@ int w4a8_matmul_y32_async(w4a8_ctx *c, const w4a8_weights *w, const int8_t *d_x8
   DeviceGuard g(c->device);
   HIP_TRY(launch_matmul(w->d, (int32_t)w->nrows, w->L, w->sh, d_x8, B, d_y32, c->d_err,
                         c->stream));
+  return W4A8_OK;
+}
+
+// ------------------------------------------------------------ FFN block
+int w4a8_mlp_async(w4a8_ctx *c, const w4a8_weights *gate, const w4a8_weights *up,
+                   const w4a8_weights *down, int32_t p0_gate, int32_t p0_up,
+                   int32_t p0_down, const int16_t *d_x16, const int16_t *d_norm_w,
+                   int32_t in_f, int32_t one_plus, int16_t *d_mlp_out,
+                   int16_t *d_res_out) {
+  if (!c || !gate || !up || !down || !d_x16) return fail(W4A8_E_ARG, "null argument");
+  const int64_t H = gate->L.K, FFN = gate->nrows;
+  if (up->L.K != H || up->nrows != FFN || down->L.K != FFN || down->nrows != H)
+    return fail(W4A8_E_ARG, "gate and up must be FFN x H and down H x FFN (gate " +
+                                std::to_string(gate->nrows) + "x" + std::to_string(H) +
+                                ", up " + std::to_string(up->nrows) + "x" +
+                                std::to_string(up->L.K) + ", down " +
+                                std::to_string(down->nrows) + "x" +
+                                std::to_string(down->L.K) + ")");
+  if (FFN > 16383)
+    return fail(W4A8_E_RANGE, "FFN width " + std::to_string(FFN) +
+                                  " does not fit an ALU count (max 16383)");
+  // temporaries: sg int16[FFN], u int32[FFN], prod int16[FFN], y int16[H]
+  auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
+  const size_t o_u = al(2 * FFN), o_p = o_u + al(4 * FFN), o_y = o_p + al(2 * FFN);
+  const size_t need = o_y + al(2 * H);
+  DeviceGuard g(c->device);
+  if (need > c->chain_cap) {
+    HIP_TRY(hipStreamSynchronize(c->stream));   // earlier chains may still read it
+    if (c->d_chain) HIP_TRY(hipFree(c->d_chain));
+    c->d_chain = nullptr;
+    c->chain_cap = 0;
+    HIP_TRY(hipMalloc(&c->d_chain, need));
+    c->chain_cap = need;
+  }
+  int16_t *sg = (int16_t *)c->d_chain;
+  int32_t *u = (int32_t *)(c->d_chain + o_u);
+  int16_t *prod = (int16_t *)(c->d_chain + o_p);
+  int16_t *y = d_mlp_out ? d_mlp_out : (int16_t *)(c->d_chain + o_y);
+  // gate and up share the input: one launch, RMSNorm (or not) -> DYNQ8
+  const w4a8_weights *gu[2] = {gate, up};
+  const int32_t epi_gu[2] = {EPI_SILU32, EPI_MOVY_P32};
+  const int32_t p0_gu[2] = {p0_gate, p0_up};
+  void *out_gu[2] = {sg, u};
+  int rc = site_launch(c, 2, gu, epi_gu, p0_gu, out_gu,
+                       d_norm_w ? PRO_RMSNORM_DYNQ8 : PRO_DYNQ8, d_x16, d_norm_w, in_f,
+                       one_plus, 0, nullptr, nullptr, nullptr);
+  if (rc) return rc;
+  // EMUL32 at p0 = 12 (gen_layer_script.py:2182-2184)
+  HIP_TRY(launch_alu(W4A8_ALU_EMUL32, u, sg, FFN, 12, c->d_tables, prod, c->stream));
+  const int32_t epi_d = EPI_MOVY_I16;
+  void *out_d = y;
+  rc = site_launch(c, 1, &down, &epi_d, &p0_down, &out_d, PRO_DYNQ8, prod, nullptr, 0, 0,
+                   0, nullptr, nullptr, nullptr);
+  if (rc) return rc;
+  if (d_res_out) HIP_TRY(launch_add16(d_x16, y, H, d_res_out, c->stream));
   return W4A8_OK;
 }
 

@@ -181,6 +181,9 @@ hipError_t launch_movy(const int32_t *y, int64_t n, int shift, int mode,
                        void *out, hipStream_t s);
 hipError_t launch_alu(int op, const int32_t *y, const int16_t *b, int64_t n,
                       int p0, const int32_t *tables, void *out, hipStream_t s);
+// ALU ADD (op 4, gen_layer_script.py:1399-1400): out = clip16(a + b)
+hipError_t launch_add16(const int16_t *a, const int16_t *b, int64_t n, int16_t *out,
+                        hipStream_t s);
 hipError_t launch_vec_prologue(const GemvParams &p, hipStream_t s);
 hipError_t launch_matmul(const uint8_t *w, int32_t nrows, const Layout &L,
                          int32_t sh, const int8_t *x8, int32_t B,

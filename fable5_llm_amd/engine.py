@@ -242,6 +242,16 @@ class Context:
         N.check(N.lib().w4a8_matmul_y32_async(self.h, w.h, _dptr(x8), x8.shape[0],
                                               _dptr(y32)), "matmul")
 
+    def mlp_async(self, gate, up, down, p0s, x16, norm_w=None, in_f=0, one_plus=False,
+                  mlp_out=None, res_out=None):
+        """The SwiGLU block on device tensors (w4a8_mlp_async): optional
+        RMSNorm, gate / up, EMUL32, down; mlp_out = int16[H] block output,
+        res_out = clip16(x16 + mlp_out) (may be x16 itself)."""
+        pg, pu, pd = (int(p) for p in p0s)
+        N.check(N.lib().w4a8_mlp_async(
+            self.h, gate.h, up.h, down.h, pg, pu, pd, _dptr(x16), _dptr(norm_w),
+            int(in_f), 1 if one_plus else 0, _dptr(mlp_out), _dptr(res_out)), "mlp")
+
 
 _DEFAULT = None
 

@@ -96,28 +96,25 @@ def alu_emul32(y32, b16, p0):
 
 
 def mlp_fx(xn16, qm, rs_f=RS_F_9B):
-    """SwiGLU block: gate -> SILU32 (out_f 12), up -> SHIFT32W (out_f rs_f),
-    EMUL32 product, DYNQ8 -> down -> int16.  gate/up share one DYNQ8 site
-    and run fused in one launch; the product and down run on the device."""
+    """SwiGLU block (layer_fixed.py:1597-1604): gate -> SILU32 (out_f 12),
+    up -> SHIFT32W (out_f rs_f), EMUL32 product at p0 12, DYNQ8 -> down ->
+    int16, as one device-resident chain (w4a8_mlp_async: gate and up in one
+    launch, then EMUL32, then down).  layer_fixed.py:1602 multiplies the
+    unclipped int64 up value; the engine keeps it as SHIFT32W does
+    (gen_layer_script.py:2176-2186), and the two agree whenever the shifted
+    up value fits int32, i.e. for every right shift of a y32."""
+    import torch
     ctx = default_context()
     wg, wu, wd = _weights(qm["gate"]), _weights(qm["up"]), _weights(qm["down"])
-    x = np.asarray(xn16, dtype=np.int16)
-    # gate: clip(silu(clip(rs(y, p), +-2^20))) in Q12 (layer_fixed.py:1598-1601)
-    p_g = (15 - qm["gate"]["e"] - qm["gate"]["sh"]) + rs_f - 12
-    sg, _x8, e_x, _ = ctx.matvec_fused(wg, x, prologue=N.PRO_DYNQ8,
-                                       epilogue=N.EPI_SILU32, p0=p_g)
-    # up stays 32-bit (SHIFT32W), then EMUL32 by the gate (mlp_block,
-    # gen_layer_script.py:2176-2186).  layer_fixed.py:1602 multiplies the
-    # unclipped int64 value instead; the two agree whenever the shifted up
-    # value fits int32, i.e. for every right shift of a y32.
-    p_u = (15 - qm["up"]["e"] - qm["up"]["sh"]) + rs_f - rs_f
-    u, _, _, _ = ctx.matvec_fused(wu, x, prologue=N.PRO_DYNQ8,
-                                  epilogue=N.EPI_MOVY_P32, p0=p_u)
-    prod = ctx.alu(N.ALU_EMUL32, u, 12, b=sg)
-    p_d = (15 - qm["down"]["e"] - qm["down"]["sh"]) + rs_f - rs_f
-    y, _, _, _ = ctx.matvec_fused(wd, prod, prologue=N.PRO_DYNQ8,
-                                  epilogue=N.EPI_MOVY_I16, p0=p_d)
-    return y.astype(np.int64)
+    p0s = [(15 - qm[k]["e"] - qm[k]["sh"]) + rs_f - out_f
+           for k, out_f in (("gate", 12), ("up", rs_f), ("down", rs_f))]
+    dev = torch.device("cuda", ctx.device)
+    x = torch.from_numpy(np.ascontiguousarray(xn16, dtype=np.int16)).to(dev)
+    y = torch.empty(wd.nrows, dtype=torch.int16, device=dev)
+    torch.cuda.synchronize(dev)          # the input copy ran on torch's stream
+    ctx.mlp_async(wg, wu, wd, p0s, x, mlp_out=y)
+    ctx.sync()
+    return y.cpu().numpy().astype(np.int64)
 
 
 class Amax32:

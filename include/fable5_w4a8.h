@@ -168,6 +168,28 @@ int w4a8_head_argmax_async(w4a8_ctx *ctx, const w4a8_weights *w,
 int w4a8_matmul_y32_async(w4a8_ctx *ctx, const w4a8_weights *w,
                           const int8_t *d_x8, int32_t B, int32_t *d_y32);
 
+/* ---- the SwiGLU FFN block on device buffers ---------------------------
+ * One decoder layer's MLP (gen_layer_script.py:2166-2190 mlp_block;
+ * layer_fixed.py:1597-1604 mlp_fx), enqueued on the context stream:
+ *   x8   = DYNQ8(RMSNorm(x16; norm_w, in_f, one_plus))  (d_norm_w null: DYNQ8(x16))
+ *   sg   = SILU32(gate . x8; p0_gate)              int16 Q12, FFN wide
+ *   u    = SHIFT32W(up . x8; p0_up)                int32, FFN wide
+ *   prod = EMUL32(u, sg; 12)                       int16
+ *   y    = SHIFT32(down . DYNQ8(prod); p0_down)    int16, H wide -> d_mlp_out
+ *   d_res_out = clip16(x16 + y)                    ALU ADD, the residual add
+ * Either output may be null, d_res_out may be x16 itself.  p0_* are MOVY
+ * immediates (shift = p0 - e_x, as in plan sites).  gate, up: FFN x H;
+ * down: H x FFN.  Temporaries live in the context (grown on first use).
+ * Gate and up share one launch; 4 launches in all.  No counterpart in the
+ * reference's C interface: it chains the reference's per-record operations
+ * (MVGO, the SILU32 / SHIFT32W / EMUL32 / DYNQ8 / ADD ALU ops) on the
+ * device. */
+int w4a8_mlp_async(w4a8_ctx *ctx, const w4a8_weights *gate,
+                   const w4a8_weights *up, const w4a8_weights *down,
+                   int32_t p0_gate, int32_t p0_up, int32_t p0_down,
+                   const int16_t *d_x16, const int16_t *d_norm_w, int32_t in_f,
+                   int32_t one_plus, int16_t *d_mlp_out, int16_t *d_res_out);
+
 /* ---- plans: a fixed sequence of sites (and the LM head) replayed as one
  *      unit -- the record stream of one decode step (MOVX/MVGO/FENCE/MOVY
  *      per site, seq_format.py:2077-2231).  Every result is that of running

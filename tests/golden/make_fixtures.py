@@ -11,7 +11,11 @@ and writes compressed .npz fixtures next to this script:
   ref_scripts.npz   every V / R / E / A record of tb/scripts/{layer,token}_s*.txt
                     with a row subset of each weight image (<prefix>_w<wid>.bin)
                     and the matching y32 rows; the full head y32 before each
-                    A record (for the argmax check)
+                    A record (for the argmax check); for the first MLP block
+                    of each script (gate and up V records sharing their input,
+                    then the down V record reading their width), the full gate
+                    and up y32 and the down record's x8 and e_x (the SwiGLU
+                    chain between them, gen_layer_script.py:2166-2190)
 
 File formats are those written by ref/gen_matvec_vectors.py:38-50,
 ref/gen_layer_vectors.py:29-33, ref/gen_rsqrt_cases.py:10-15,
@@ -178,6 +182,8 @@ def scripts(out):
             na = 0
             last_head_y = None
             pending_v = None
+            recent = []          # (v index, wid, nin, nr, full y32) of the last V records
+            mlp_done = False
             for k, hdr, data in parse_script(f"{prefix}.txt"):
                 if k == "R":
                     last_r = (int(hdr[0], 16), s16(data))
@@ -197,6 +203,16 @@ def scripts(out):
                     out[f"{tag}_v{nv}_y32"] = y[rows].astype(np.int32)
                     if nr == int(man[str(wid)]["nrows"]) and wid == max(rowsel):
                         last_head_y = y.astype(np.int32)
+                    if (not mlp_done and len(recent) >= 2 and recent[-1][3] == nin
+                            and recent[-2][3] == nin and recent[-1][2] == recent[-2][2]):
+                        g, u = recent[-2], recent[-1]
+                        out[f"{tag}_mlp_v"] = np.array([g[0], u[0], nv], dtype=np.int64)
+                        out[f"{tag}_mlp_gate_y32"] = g[4].astype(np.int32)
+                        out[f"{tag}_mlp_up_y32"] = u[4].astype(np.int32)
+                        out[f"{tag}_mlp_down_x8"] = x8.astype(np.int8)
+                        out[f"{tag}_mlp_down_e"] = np.array([last_e], dtype=np.int64)
+                        mlp_done = True
+                    recent = (recent + [(nv, wid, nin, nr, y)])[-2:]
                     pending_v = nv
                     nv += 1
                 elif k == "C" and pending_v is not None:
