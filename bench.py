@@ -19,7 +19,8 @@ Prints one JSON line.  `value` = stream bytes / wall time per step.
 `roofline` = the dominant kernel alone: stream bytes / sum of its per-launch
 durations, each launch bracketed by dispatch-recorded HIP events.
 `ffn` = one layer's SwiGLU block per call (w4a8_mlp_async) over the 32
-layers, with the residual add.
+layers, with the residual add.  `head` = the LM head alone, with its
+argmax and with TOPK-32.
 `batched` = the int8-MFMA kernel over the stream's 96 FFN matrices at B
 tokens per pass (--batch), with its GB/s and MFMA utilisation.
 `cpu_baseline` = the C oracle (oracle/law_c.c, OpenMP) over the same stream
@@ -175,6 +176,58 @@ def ffn_leg(st, ctx, steps, warmup):
                      "DYNQ8->down SHIFT32, residual ADD"}, keep
 
 
+def head_leg(st, ctx, steps, warmup):
+    """The 248,320-row LM head on its own (final RMSNorm -> DYNQ8 -> matvec),
+    once with the AMAX32 argmax and once with TOPK-32 (y32 to a scratch
+    vector, then the TOPK kernels), `steps` calls each."""
+    import torch
+    dev = torch.device("cuda", ctx.device)
+    stream = torch.cuda.current_stream(dev)
+    s = st.sites[-1]
+    assert s.head
+    w = st.weights[-1][0]
+    x, nw = st.inputs[-1]
+    res = torch.zeros(2, dtype=torch.int32, device=dev)
+    tk = torch.zeros(66, dtype=torch.int32, device=dev)
+    calls = {
+        "argmax": lambda: ctx.head_argmax_async(w, x, res, prologue=s.prologue, norm_w=nw,
+                                                in_f=s.in_f, one_plus=s.one_plus),
+        "topk32": lambda: ctx.head_topk32_async(w, x, tk, prologue=s.prologue, norm_w=nw,
+                                                in_f=s.in_f, one_plus=s.one_plus),
+    }
+    out = {"rows": s.mats[0].nrows, "bytes": s.mats[0].bytes}
+    for name, fn in calls.items():
+        for _ in range(warmup):
+            fn()
+        ctx.sync()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            fn()
+        e1.record(stream)
+        ctx.sync()
+        torch.cuda.synchronize(dev)
+        us = e0.elapsed_time(e1) * 1e3 / steps
+        out[name] = {"us_per_call": round(us, 2),
+                     "value": round(s.mats[0].bytes / (us * 1e-6) / 1e9, 1), "unit": "GB/s"}
+    keep = (res.cpu().numpy(), tk.cpu().numpy())
+    return out, keep
+
+
+def head_check(ys, keep):
+    """The head leg's argmax and TOPK-32 against the oracle's head y32."""
+    import numpy as np
+    from oracle import law
+    res, tk = keep
+    y = ys[-1][0]
+    vals, rows, count, ovf = law.topk32(y)
+    ok = tuple(int(v) for v in res) == tuple(int(v) for v in law.amax32(y))
+    ok = ok and int(tk[64]) == count and bool(tk[65]) == ovf
+    ok = ok and np.array_equal(tk[:count], vals) and np.array_equal(tk[32:32 + count], rows)
+    return "bit-exact" if ok else "MISMATCH"
+
+
 def ffn_check(st, keep):
     """Layer 0's FFN block against the oracle: law.py for RMSNorm, DYNQ8,
     SILU32, EMUL32 and the shifts, oracle/law_c.c for the matvecs."""
@@ -218,7 +271,7 @@ def batched_check(st, keep):
     return "bit-exact" if bad == 0 else f"MISMATCH in {bad} token rows"
 
 
-def cpu_baseline(st, min_seconds, keep=(), keep_ffn=None):
+def cpu_baseline(st, min_seconds, keep=(), keep_ffn=None, keep_head=None):
     """Oracle leg: the C restatement over the full stream, repeated until
     `min_seconds` of matvec work; returns its rate and the parity check (of
     the stream and of the batched leg's kept outputs)."""
@@ -256,6 +309,7 @@ def cpu_baseline(st, min_seconds, keep=(), keep_ffn=None):
         "parity": "bit-exact" if not bad else f"MISMATCH {len(bad)}: {bad[:5]}",
         "batched_parity": batched_check(st, keep) if keep else None,
         "ffn_parity": ffn_check(st, keep_ffn) if keep_ffn else None,
+        "head_parity": head_check(ys, keep_head) if keep_head else None,
     }
 
 
@@ -282,7 +336,8 @@ def main():
     ap.add_argument("--no-ordered", action="store_true",
                     help="skip timing the same plan strictly in order (graph mode)")
     ap.add_argument("--no-ffn", action="store_true",
-                    help="skip the FFN-block leg (w4a8_mlp_async per layer)")
+                    help="skip the FFN-block leg (w4a8_mlp_async per layer) and the "
+                         "LM-head leg (argmax and TOPK-32 alone)")
     ap.add_argument("--batch", default="8,32",
                     help="token counts B for the batched int8-MFMA leg over the FFN "
                          "matrices (comma-separated, each <= 64; empty: skip)")
@@ -429,12 +484,16 @@ def main():
     if batches:
         line["batched"], keep = batched_leg(st, ctx, batches, min(args.steps, 50),
                                             max(3, args.warmup // 10), args.seed)
+    keep_head = None
+    if not args.no_ffn:
+        line["head"], keep_head = head_leg(st, ctx, min(args.steps, 50),
+                                           max(3, args.warmup // 10))
     keep_ffn = None
     if not args.no_ffn:
         line["ffn"], keep_ffn = ffn_leg(st, ctx, min(args.steps, 50),
                                         max(3, args.warmup // 10))
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(st, args.cpu_seconds, keep, keep_ffn)
+        line["cpu_baseline"] = cpu_baseline(st, args.cpu_seconds, keep, keep_ffn, keep_head)
     st.close()
     ctx.close()
     print(json.dumps(line), flush=True)

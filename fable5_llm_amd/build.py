@@ -13,7 +13,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libfable5_w4a8.so")
-SOURCES = ["w4a8_kernels.hip", "w4a8_stream.hip", "w4a8_mfma.hip", "w4a8_abi.hip"]
+SOURCES = ["w4a8_kernels.hip", "w4a8_stream.hip", "w4a8_mfma.hip", "w4a8_topk.hip",
+           "w4a8_abi.hip"]
 ARCH = os.environ.get("FABLE5_OFFLOAD_ARCH", "gfx950")
 
 

@@ -31,6 +31,8 @@ struct w4a8_ctx {
   size_t stage_cap = 0;
   uint8_t *d_chain = nullptr;   // temporaries of device-side chains (w4a8_mlp_async)
   size_t chain_cap = 0;
+  int32_t *d_topk_flags = nullptr;   // TOPK-32 look-back flags (kTopkFlagWords)
+  int32_t topk_epoch = 0;            // epoch of the last TOPK-32 launch
   int32_t h_tables[kTableLen];
 };
 
@@ -120,6 +122,18 @@ int ensure_stage(w4a8_ctx *c, size_t bytes) {
   return W4A8_OK;
 }
 
+// the context's buffer for the temporaries of device-side chains
+int ensure_chain(w4a8_ctx *c, size_t bytes) {
+  if (bytes <= c->chain_cap) return W4A8_OK;
+  HIP_TRY(hipStreamSynchronize(c->stream));   // earlier chains may still use it
+  if (c->d_chain) HIP_TRY(hipFree(c->d_chain));
+  c->d_chain = nullptr;
+  c->chain_cap = 0;
+  HIP_TRY(hipMalloc(&c->d_chain, bytes));
+  c->chain_cap = bytes;
+  return W4A8_OK;
+}
+
 int ensure_partials(w4a8_ctx *c, int n) {
   if (n <= c->partials_cap) return W4A8_OK;
   if (c->d_partials) HIP_TRY(hipFree(c->d_partials));
@@ -144,6 +158,8 @@ int take_err(w4a8_ctx *c) {
                             "guarantees residency)");
     if (h & 4)
       return fail(W4A8_E_HIP, "a wait between wavefronts of one workgroup timed out");
+    if (h & 8)
+      return fail(W4A8_E_HIP, "TOPK-32's wait for the lists of earlier chunks timed out");
   }
   return W4A8_OK;
 }
@@ -326,7 +342,9 @@ int w4a8_ctx_create(int32_t device, w4a8_ctx **out) {
                        hipMemcpyHostToDevice)) != hipSuccess ||
         (e = hipMalloc(&c->d_err, 64)) != hipSuccess ||
         (e = hipMemset(c->d_err, 0, 64)) != hipSuccess ||
-        (e = hipMalloc(&c->d_result, 64)) != hipSuccess) {
+        (e = hipMalloc(&c->d_result, 64)) != hipSuccess ||
+        (e = hipMalloc(&c->d_topk_flags, sizeof(int32_t) * kTopkFlagWords)) != hipSuccess ||
+        (e = hipMemset(c->d_topk_flags, 0, sizeof(int32_t) * kTopkFlagWords)) != hipSuccess) {
       rc = fail(W4A8_E_HIP, hipGetErrorString(e));
       break;
     }
@@ -350,6 +368,7 @@ int w4a8_ctx_destroy(w4a8_ctx *c) {
   (void)hipFree(c->d_result);
   (void)hipFree(c->d_stage);
   (void)hipFree(c->d_chain);
+  (void)hipFree(c->d_topk_flags);
   if (c->own) (void)hipStreamDestroy(c->own);
   delete c;
   return W4A8_OK;
@@ -736,6 +755,100 @@ int w4a8_matmul_y32_async(w4a8_ctx *c, const w4a8_weights *w, const int8_t *d_x8
   return W4A8_OK;
 }
 
+// ------------------------------------------------------------ TOPK-32
+// One TOPK-32 launch on the context's stream.  Flags hold the epochs of
+// earlier launches; they are cleared (by a kernel, so that a captured graph
+// clears them on every replay) when the stream is being captured -- a graph
+// replays one fixed epoch -- and before the epoch grows too large.
+static int topk_launch(w4a8_ctx *c, const int32_t *d_y, int64_t n, void *scratch,
+                       int32_t *d_out) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing(c->stream, &cs));
+  if (cs != hipStreamCaptureStatusNone || c->topk_epoch + 1 >= kTopkEpochMax) {
+    HIP_TRY(launch_fill_i32(c->d_topk_flags, 0, kTopkFlagWords, c->stream));
+    c->topk_epoch = 0;
+  }
+  const int32_t epoch = ++c->topk_epoch;
+  HIP_TRY(launch_topk32(d_y, n, scratch, c->d_topk_flags, epoch, d_out, c->d_err, c->stream));
+  return W4A8_OK;
+}
+
+int w4a8_head_topk32_async(w4a8_ctx *c, const w4a8_weights *w, int32_t prologue,
+                           const void *d_x, const int16_t *d_norm_w, int32_t in_f,
+                           int32_t one_plus, int32_t e_x, int32_t *d_out) {
+  if (!c || !w || !d_out) return fail(W4A8_E_ARG, "null argument");
+  GemvParams P;
+  int rc = head_params(c, P, w, prologue, d_x, d_norm_w, in_f, one_plus, e_x);
+  if (rc) return rc;
+  const size_t yb = ((size_t)w->nrows * 4 + 255) & ~(size_t)255;
+  DeviceGuard g(c->device);
+  if ((rc = ensure_chain(c, yb + topk_scratch_bytes(w->nrows)))) return rc;
+  int32_t *y = (int32_t *)c->d_chain;
+  P.job[0].epi = EPI_Y32;   // the head's raw y32 (shift 0, seq_format.py:2225-2226)
+  P.job[0].out = y;
+  HIP_TRY(launch_gemv(P, grid_for(c, P.total_tiles), c->stream));
+  return topk_launch(c, y, w->nrows, c->d_chain + yb, d_out);
+}
+
+int w4a8_topk32(w4a8_ctx *c, const int32_t *y32, int64_t n, int32_t *vals, int32_t *rows,
+                int32_t *count, int32_t *overflow) {
+  if (!c || !y32 || n < 1) return fail(W4A8_E_ARG, "bad argument");
+  if (n > (1 << 18))
+    return fail(W4A8_E_RANGE, "topk32: " + std::to_string(n) +
+                                  " elements exceed the 18-bit AMAX32 index (2^18)");
+  DeviceGuard g(c->device);
+  const size_t yb = ((size_t)n * 4 + 255) & ~(size_t)255;
+  int rc = ensure_stage(c, yb + 66 * 4);
+  if (rc) return rc;
+  if ((rc = ensure_chain(c, topk_scratch_bytes(n)))) return rc;
+  int32_t *d_y = (int32_t *)c->d_stage, *d_o = (int32_t *)(c->d_stage + yb);
+  HIP_TRY(hipMemcpyAsync(d_y, y32, (size_t)n * 4, hipMemcpyHostToDevice, c->stream));
+  if ((rc = topk_launch(c, d_y, n, c->d_chain, d_o))) return rc;
+  int32_t h[66];
+  HIP_TRY(hipMemcpyAsync(h, d_o, sizeof(h), hipMemcpyDeviceToHost, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  if ((rc = take_err(c))) return rc;
+  for (int i = 0; i < 32; ++i) {
+    if (vals) vals[i] = h[i];
+    if (rows) rows[i] = h[32 + i];
+  }
+  if (count) *count = h[64];
+  if (overflow) *overflow = h[65];
+  return W4A8_OK;
+}
+
+int w4a8_head_topk32(w4a8_ctx *c, const w4a8_weights *w, int32_t prologue, const void *x,
+                     const int16_t *norm_w, int32_t in_f, int32_t one_plus, int32_t *vals,
+                     int32_t *rows, int32_t *count, int32_t *overflow) {
+  if (!c || !w || !x) return fail(W4A8_E_ARG, "null argument");
+  DeviceGuard g(c->device);
+  const int32_t K = w->L.K;
+  const size_t xb = prologue == PRO_X8 ? (size_t)K : (size_t)K * 2;
+  const size_t o_w = (xb + 255) & ~(size_t)255;
+  const size_t o_o = o_w + (((size_t)K * 2 + 255) & ~(size_t)255);
+  int rc = ensure_stage(c, o_o + 66 * 4);
+  if (rc) return rc;
+  uint8_t *s = c->d_stage;
+  HIP_TRY(hipMemcpyAsync(s, x, xb, hipMemcpyHostToDevice, c->stream));
+  if (prologue == PRO_RMSNORM_DYNQ8 && norm_w)
+    HIP_TRY(hipMemcpyAsync(s + o_w, norm_w, (size_t)K * 2, hipMemcpyHostToDevice,
+                           c->stream));
+  rc = w4a8_head_topk32_async(c, w, prologue, s, (const int16_t *)(s + o_w), in_f, one_plus,
+                              0, (int32_t *)(s + o_o));
+  if (rc) return rc;
+  int32_t h[66];
+  HIP_TRY(hipMemcpyAsync(h, s + o_o, sizeof(h), hipMemcpyDeviceToHost, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  if ((rc = take_err(c))) return rc;
+  for (int i = 0; i < 32; ++i) {
+    if (vals) vals[i] = h[i];
+    if (rows) rows[i] = h[32 + i];
+  }
+  if (count) *count = h[64];
+  if (overflow) *overflow = h[65];
+  return W4A8_OK;
+}
+
 // ------------------------------------------------------------ FFN block
 int w4a8_mlp_async(w4a8_ctx *c, const w4a8_weights *gate, const w4a8_weights *up,
                    const w4a8_weights *down, int32_t p0_gate, int32_t p0_up,
@@ -757,16 +870,9 @@ int w4a8_mlp_async(w4a8_ctx *c, const w4a8_weights *gate, const w4a8_weights *up
   // temporaries: sg int16[FFN], u int32[FFN], prod int16[FFN], y int16[H]
   auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
   const size_t o_u = al(2 * FFN), o_p = o_u + al(4 * FFN), o_y = o_p + al(2 * FFN);
-  const size_t need = o_y + al(2 * H);
   DeviceGuard g(c->device);
-  if (need > c->chain_cap) {
-    HIP_TRY(hipStreamSynchronize(c->stream));   // earlier chains may still read it
-    if (c->d_chain) HIP_TRY(hipFree(c->d_chain));
-    c->d_chain = nullptr;
-    c->chain_cap = 0;
-    HIP_TRY(hipMalloc(&c->d_chain, need));
-    c->chain_cap = need;
-  }
+  int rc0 = ensure_chain(c, o_y + al(2 * H));
+  if (rc0) return rc0;
   int16_t *sg = (int16_t *)c->d_chain;
   int32_t *u = (int32_t *)(c->d_chain + o_u);
   int16_t *prod = (int16_t *)(c->d_chain + o_p);

@@ -181,6 +181,17 @@ hipError_t launch_movy(const int32_t *y, int64_t n, int shift, int mode,
                        void *out, hipStream_t s);
 hipError_t launch_alu(int op, const int32_t *y, const int16_t *b, int64_t n,
                       int p0, const int32_t *tables, void *out, hipStream_t s);
+// TOPK-32 of n head values y, 1 <= n <= 2^18 (w4a8_topk.hip): out =
+// vals[32], rows[32], count, overflow.  scratch: topk_scratch_bytes(n)
+// bytes, no initial contents.  flags: kTopkFlagWords words, zero or left
+// by earlier launches whose epochs were all below epoch (0 < epoch < 2^29).
+constexpr int kTopkMaxChunks = 256;   // chunks of 1024 rows in 2^18 rows
+constexpr int kTopkSuper = 16;        // chunks per super-chunk
+constexpr int kTopkFlagWords = 2 * kTopkMaxChunks + kTopkMaxChunks / kTopkSuper;
+constexpr int32_t kTopkEpochMax = 1 << 29;
+size_t topk_scratch_bytes(int64_t n);
+hipError_t launch_topk32(const int32_t *y, int64_t n, void *scratch, int32_t *flags,
+                         int32_t epoch, int32_t *out, int32_t *err, hipStream_t s);
 // ALU ADD (op 4, gen_layer_script.py:1399-1400): out = clip16(a + b)
 hipError_t launch_add16(const int16_t *a, const int16_t *b, int64_t n, int16_t *out,
                         hipStream_t s);

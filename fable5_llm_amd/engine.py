@@ -210,6 +210,36 @@ class Context:
             "head_argmax")
         return int(idx.value), int(val.value)
 
+    def topk32(self, y32):
+        """TOPK-32 of an int32 vector (one fresh scan): (vals, rows, count,
+        overflow), vals / rows int64[count]."""
+        y = np.ascontiguousarray(np.asarray(y32, dtype=np.int32).reshape(-1))
+        vals, rows = np.zeros(32, np.int32), np.zeros(32, np.int32)
+        cnt, ovf = ctypes.c_int32(), ctypes.c_int32()
+        N.check(N.lib().w4a8_topk32(self.h, _ptr(y), y.size, _ptr(vals), _ptr(rows),
+                                    ctypes.byref(cnt), ctypes.byref(ovf)), "topk32")
+        n = int(cnt.value)
+        return vals[:n].astype(np.int64), rows[:n].astype(np.int64), n, bool(ovf.value)
+
+    def head_topk32(self, w, x, prologue=N.PRO_X8, norm_w=None, in_f=0, one_plus=False):
+        """The head's matvec, then TOPK-32 of its raw y32."""
+        xa = np.ascontiguousarray(x, dtype=np.int8 if prologue == N.PRO_X8 else np.int16)
+        nw = None if norm_w is None else np.ascontiguousarray(np.asarray(norm_w, np.int16))
+        vals, rows = np.zeros(32, np.int32), np.zeros(32, np.int32)
+        cnt, ovf = ctypes.c_int32(), ctypes.c_int32()
+        N.check(N.lib().w4a8_head_topk32(
+            self.h, w.h, int(prologue), _ptr(xa), None if nw is None else _ptr(nw),
+            int(in_f), 1 if one_plus else 0, _ptr(vals), _ptr(rows), ctypes.byref(cnt),
+            ctypes.byref(ovf)), "head_topk32")
+        n = int(cnt.value)
+        return vals[:n].astype(np.int64), rows[:n].astype(np.int64), n, bool(ovf.value)
+
+    def head_topk32_async(self, w, x, out, prologue=N.PRO_DYNQ8, e_x=0, norm_w=None,
+                          in_f=0, one_plus=False):
+        N.check(N.lib().w4a8_head_topk32_async(
+            self.h, w.h, int(prologue), _dptr(x), _dptr(norm_w), int(in_f),
+            1 if one_plus else 0, int(e_x), _dptr(out)), "head_topk32")
+
     def matmul_y32(self, w, x8):
         x = np.ascontiguousarray(np.asarray(x8, dtype=np.int8))
         assert x.ndim == 2 and x.shape[1] == w.K

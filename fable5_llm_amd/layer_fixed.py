@@ -9,6 +9,7 @@ MOVY / ALU / AMAX32 movers, computed on the MI355X engine.
   alu_shift32/shift32w/silu32/emul32   gen_layer_script.py:1397-1423
   Amax32 / head_argmax                 gen_layer_script.py:1424-1433,
                                        gen_model_script.py:627-643
+  head_topk32 / topk32                 the layer_topk32 block, docs/SEQ_ISA.md B8
 
 A quantised matrix `qw` is the reference's dict {"w4", "m", "e", "sh"} (or
 an already-uploaded engine.Weights via qw["dev"]).
@@ -142,3 +143,16 @@ def head_argmax(qw, x, prologue=N.PRO_X8, norm_w=None, in_f=0, one_plus=False):
     """LM head in one pass: (argmax row, its int32 y32), lowest index on ties."""
     return default_context().head_argmax(_weights(qw), x, prologue=prologue,
                                          norm_w=norm_w, in_f=in_f, one_plus=one_plus)
+
+
+def topk32(y32):
+    """TOPK-32 of an int32 vector scanned after one fresh (docs/SEQ_ISA.md
+    B8): (vals, rows, count, overflow), the block's TK_VAL / TK_IDX entries
+    below count and TK_STATUS's count and overflow bit."""
+    return default_context().topk32(y32)
+
+
+def head_topk32(qw, x, prologue=N.PRO_X8, norm_w=None, in_f=0, one_plus=False):
+    """The LM head's matvec then TOPK-32 of its raw y32 (the AMAX32 head
+    loop feeding the block, gen_model_script.py:627-643)."""
+    return default_context().head_topk32(_weights(qw), x, prologue, norm_w, in_f, one_plus)

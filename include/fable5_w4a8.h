@@ -168,6 +168,29 @@ int w4a8_head_argmax_async(w4a8_ctx *ctx, const w4a8_weights *w,
 int w4a8_matmul_y32_async(w4a8_ctx *ctx, const w4a8_weights *w,
                           const int8_t *d_x8, int32_t B, int32_t *d_y32);
 
+/* ---- TOPK-32 over the LM head -----------------------------------------
+ * The layer_topk32 block's contract (docs/SEQ_ISA.md B8): the head's raw
+ * y32 (shift 0) scanned in row order after one fresh; the 32 largest
+ * values sorted descending, ties in row order (entry 0 == the AMAX32
+ * winner); count = min(32, rows); overflow = sticky, set when a row was
+ * rejected (list full, not greater than entry 31) while exactly equal to
+ * entry 31 (TK_STATUS bit 7).  Entries past count are zero.  Replaces the
+ * host's TK_VAL / TK_IDX readback loop; no counterpart in the reference's
+ * C interface. */
+int w4a8_head_topk32(w4a8_ctx *ctx, const w4a8_weights *w, int32_t prologue,
+                     const void *x, const int16_t *norm_w, int32_t in_f,
+                     int32_t one_plus, int32_t *vals, int32_t *rows,
+                     int32_t *count, int32_t *overflow);
+/* the same scan over n <= 2^18 int32 values (an AMAX32 command sequence
+   over any region feeds the block, SEQ_ISA.md B8) */
+int w4a8_topk32(w4a8_ctx *ctx, const int32_t *y32, int64_t n, int32_t *vals,
+                int32_t *rows, int32_t *count, int32_t *overflow);
+/* d_out: int32[66] = vals[32], rows[32], count, overflow */
+int w4a8_head_topk32_async(w4a8_ctx *ctx, const w4a8_weights *w,
+                           int32_t prologue, const void *d_x,
+                           const int16_t *d_norm_w, int32_t in_f,
+                           int32_t one_plus, int32_t e_x, int32_t *d_out);
+
 /* ---- the SwiGLU FFN block on device buffers ---------------------------
  * One decoder layer's MLP (gen_layer_script.py:2166-2190 mlp_block;
  * layer_fixed.py:1597-1604 mlp_fx), enqueued on the context stream:

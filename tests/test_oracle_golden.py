@@ -339,6 +339,94 @@ def test_amax32_ties_lowest_index():
     assert (st.idx, st.val) == (4, 10)
 
 
+# ----------------------------------------------------------- TOPK-32
+def _topk_lexsort(y):
+    """the first 32 elements by (value desc, arrival asc)"""
+    y = np.asarray(y, dtype=np.int64)
+    order = np.lexsort((np.arange(y.size), -y))[:32]
+    return y[order], order
+
+
+def _ovf_prefix_counts(y):
+    """overflow, independently: some arrival i >= 32 had fewer than 32
+    earlier elements above it and at least 32 at or above it (it tied the
+    32nd largest value so far and was rejected)"""
+    y = np.asarray(y, dtype=np.int64)
+    for i in range(32, y.size):
+        g = int(np.count_nonzero(y[:i] > y[i]))
+        ge = int(np.count_nonzero(y[:i] >= y[i]))
+        if g < 32 <= ge:
+            return True
+    return False
+
+
+def test_topk32_is_lexsort_and_prefix_count_overflow():
+    rng = np.random.default_rng(21)
+    for trial in range(200):
+        n = int(rng.integers(1, 400))
+        alpha = int(rng.choice([3, 8, 40, 1 << 30]))
+        y = rng.integers(-alpha, alpha + 1, n)
+        vals, idx, count, ovf = law.topk32(y, chunk=int(rng.integers(1, 300)))
+        ev, ei = _topk_lexsort(y)
+        assert count == min(32, n)
+        assert np.array_equal(vals, ev) and np.array_equal(idx, ei), trial
+        assert ovf == _ovf_prefix_counts(y), trial
+
+
+def test_topk32_entry0_is_amax32_on_script_heads(scripts):
+    n = 0
+    for tag in script_tags():
+        for idx, val, y in script_argmax(scripts, tag):
+            vals, ids, count, _ = law.topk32(y)
+            assert (int(ids[0]), int(vals[0])) == (idx, val)
+            assert count == 32
+            n += 1
+    assert n == 12
+
+
+def test_topk32_named_cases():
+    I32MAX, I32MIN = (1 << 31) - 1, -(1 << 31)
+    rng = np.random.default_rng(7)
+    # fewer than 32 elements: count stops at n, no overflow possible
+    for n in (1, 2, 8, 17, 31):
+        y = rng.integers(I32MIN, I32MAX, n)
+        _, _, count, ovf = law.topk32(y)
+        assert count == n and not ovf
+    # 40 x MAX then 40 x MIN: 32 copies of MAX, first 32 indices, overflow
+    vals, idx, count, ovf = law.topk32([I32MAX] * 40 + [I32MIN] * 40)
+    assert count == 32 and ovf and (vals == I32MAX).all()
+    assert np.array_equal(idx, np.arange(32))
+    # the 33rd element ties entry[31] exactly: literal overflow
+    v = sorted(rng.choice(np.arange(1000, 9000), 32, replace=False).tolist(), reverse=True)
+    y = v + [v[31]]
+    assert law.topk32(y)[3]
+    # entries 30 and 31 equal, then a bigger element displaces entry 31:
+    # the literal bit stays clear, the displaced-tie reading sets
+    v = sorted(rng.choice(np.arange(1000, 9000), 31, replace=False).tolist(), reverse=True)
+    y = v + [v[30], I32MAX]
+    st = law.Topk32().feed(y, fresh=True)
+    assert not st.ovf_lit and st.ovf_disp
+    assert st.lst[0] == (I32MAX, 32)
+    # rails among random values: signed compare at both ends
+    y = rng.integers(I32MIN, I32MAX, 200)
+    y[[0, 5, 77, 199, 3, 100]] = I32MAX
+    y[[1, 6, 78, 198]] = I32MIN
+    vals, idx, _, _ = law.topk32(y)
+    assert list(idx[:6]) == [0, 3, 5, 77, 100, 199] and (vals[:6] == I32MAX).all()
+    # chained chunks without fresh accumulate into one list; fresh clears
+    st = law.Topk32().feed([5, 1], fresh=True).feed([9])
+    assert st.lst[:3] == [(9, 2), (5, 0), (1, 1)]
+    st.feed([3], fresh=True)
+    assert st.lst == [(3, 0)]
+    # the index is the 18-bit element counter: it wraps, ties still go by
+    # arrival
+    y = np.zeros((1 << 18) + 10, dtype=np.int64)
+    y[(1 << 18) + 4] = 7
+    vals, idx, _, _ = law.topk32(y)
+    assert (int(vals[0]), int(idx[0])) == (7, 4)
+    assert list(idx[1:4]) == [0, 1, 2]
+
+
 # ---------------------------------------------- matvec_to / dequant bound
 def test_matvec_to_float_bound():
     # the integer pipeline equals dequantised float math to the final
