@@ -179,7 +179,7 @@ def ffn_leg(st, ctx, steps, warmup):
 def head_leg(st, ctx, steps, warmup):
     """The 248,320-row LM head on its own (final RMSNorm -> DYNQ8 -> matvec),
     once with the AMAX32 argmax and once with TOPK-32 (y32 to a scratch
-    vector, then the TOPK kernels), `steps` calls each."""
+    vector, then the TOPK kernel), `steps` calls each."""
     import torch
     dev = torch.device("cuda", ctx.device)
     stream = torch.cuda.current_stream(dev)

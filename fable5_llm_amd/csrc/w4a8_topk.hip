@@ -30,6 +30,8 @@ namespace {
 
 constexpr int kTkRows = 1024;   // rows per chunk
 constexpr int kTk = 32;
+constexpr int kTkPerLane = kTkRows / 64;
+constexpr int kTkSerialMax = 4;   // candidates a group replays one by one
 
 __device__ __forceinline__ uint64_t tk_key(int32_t v, uint32_t row) {
   return ((uint64_t)((uint32_t)v ^ 0x80000000u) << 32) | (uint64_t)(0xFFFFFFFFu - row);
@@ -40,9 +42,13 @@ __device__ __forceinline__ int32_t tk_val(uint64_t k) {
 __device__ __forceinline__ uint32_t tk_row(uint64_t k) {
   return 0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFu);
 }
-__device__ __forceinline__ uint64_t shfl_up1_u64(uint64_t v) {
-  const uint32_t lo = (uint32_t)__shfl_up((int)(uint32_t)v, 1);
-  const uint32_t hi = (uint32_t)__shfl_up((int)(uint32_t)(v >> 32), 1);
+// lane - 1's value (DPP wave_shr:1; lane 0 keeps its own)
+__device__ __forceinline__ uint64_t shift_up1_u64(uint64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)v, (int)(uint32_t)v,
+                                                            0x138, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)(v >> 32),
+                                                            (int)(uint32_t)(v >> 32), 0x138, 0xF,
+                                                            0xF, false);
   return ((uint64_t)hi << 32) | lo;
 }
 // lane j's 64-bit value (j uniform)
@@ -52,11 +58,12 @@ __device__ __forceinline__ uint64_t lane_u64(uint64_t v, int j) {
   return ((uint64_t)hi << 32) | lo;
 }
 
-// Lane exchange x[lane ^ m].  Distances 1 and 2 are DPP quad permutes, 8 is
-// a DPP rotation by 8 within a row of 16 lanes (its own inverse), 4 takes
-// the rotations by 4 and by 12 (one brings lane + 4, the other lane - 4;
-// `ror4_up` says which, found once per wavefront by tk_ror4_up), and 16 /
-// 32 go through ds_bpermute.
+// Lane exchange x[lane ^ m], without LDS.  Distances 1 and 2 are DPP quad
+// permutes, 8 is a DPP rotation by 8 within a row of 16 lanes (its own
+// inverse), 4 takes the rotations by 4 and by 12 (one brings lane + 4, the
+// other lane - 4; `ror4_up` says which, found once per wavefront by
+// tk_ror4_up), 16 and 32 are the gfx950 row swaps v_permlane16_swap (odd
+// rows of 16 with even rows) and v_permlane32_swap (halves).
 __device__ __forceinline__ bool tk_ror4_up() {
   const int t = __builtin_amdgcn_update_dpp(0, (int)(threadIdx.x & 63), 0x124, 0xF, 0xF, false);
   return __builtin_amdgcn_readfirstlane(t) == 4;   // lane 0 read lane 4
@@ -72,7 +79,15 @@ __device__ __forceinline__ uint32_t xchg32(uint32_t x, int m, bool ror4_up, int 
       return want_up == ror4_up ? a : b;
     }
     case 8: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x128, 0xF, 0xF, false);
-    default: return (uint32_t)__shfl_xor((int)x, m);
+    case 16: {
+      // {x with odd rows <- even rows, x with even rows <- odd rows}
+      const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+      return (lane & 16) ? r[0] : r[1];
+    }
+    default: {
+      const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+      return (lane & 32) ? r[0] : r[1];
+    }
   }
 }
 __device__ __forceinline__ uint64_t xchg64(uint64_t v, int m, bool ror4_up, int lane) {
@@ -108,11 +123,22 @@ __device__ __forceinline__ uint64_t bmerge64(uint64_t v, bool ror4_up, int lane)
 }
 
 // Lanes 0..31 of L and of V each hold 32 keys sorted descending; afterwards
-// lanes 0..31 hold the top 32 of both (V's keys enter lanes 32..63 reversed).
+// lanes 0..31 hold the top 32 of both, descending (lanes 32..63: unspecified).
+// max(L[i], V[31 - i]) holds the top 32 as a bitonic sequence; five
+// half-cleaner stages sort it.  V[31 - i] = row_mirror, then the row swap.
 __device__ __forceinline__ uint64_t merge32v(uint64_t L, uint64_t V, bool ror4_up, int lane) {
-  const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)V, 63 - lane);
-  const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(V >> 32), 63 - lane);
-  return bmerge64(lane < kTk ? L : (((uint64_t)hi << 32) | lo), ror4_up, lane);
+  const uint32_t mlo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)V, 0x140, 0xF, 0xF,
+                                                             false);
+  const uint32_t mhi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(V >> 32), 0x140,
+                                                             0xF, 0xF, false);
+  const uint64_t r = xchg64(((uint64_t)mhi << 32) | mlo, 16, ror4_up, lane);
+  uint64_t v = L > r ? L : r;
+#pragma unroll
+  for (int s = 16; s > 0; s >>= 1) {
+    const uint64_t o = xchg64(v, s, ror4_up, lane);
+    v = (lane & s) == 0 ? (v > o ? v : o) : (v < o ? v : o);
+  }
+  return v;
 }
 
 __device__ __forceinline__ uint64_t ld_coh64(const uint64_t *p) {
@@ -127,47 +153,60 @@ __device__ __forceinline__ void st_coh64(uint64_t *p, uint64_t v) {
 __device__ __forceinline__ void st_coh32(int32_t *p, int32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void tk_wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// Top 32 of the 1024 keys in LDS (0 = no key), descending in lanes 0..31.
-// The 32nd largest of the 64 lane maxima over the strided subsets (lane l:
-// keys l, l + 64, ...), tau, bounds the 32nd largest key from below (32
-// distinct keys are >= tau); the keys >= tau are packed into buf (LDS, 128
-// keys) and merged in 64 at a time.  One wavefront per workgroup, so LDS
-// accesses of the wavefront are ordered by waiting for them.
-__device__ uint64_t top32_chunk(const uint64_t *keys, uint64_t *buf, bool up, int lane) {
-  uint64_t mx = 0;
-  for (int i = lane; i < kTkRows; i += 64) mx = keys[i] > mx ? keys[i] : mx;
-  const uint64_t tau = lane_u64(sort64(mx, up, lane), kTk - 1);
+// Keys stream through buf (LDS, 128 keys) 64 lanes at a time: lanes with q
+// set append their key, and every full 64 are sorted and merged into L.
+// The wavefront is alone in its workgroup and its LDS accesses execute in
+// order, so only the compiler's ordering is fenced.
+struct TopFeed {
+  uint64_t *buf;
   uint64_t L = 0;
   int cnt = 0;   // keys waiting in buf (uniform)
-  for (int i0 = 0; i0 < kTkRows; i0 += 64) {
-    const uint64_t k = keys[i0 + lane];
-    const bool q = k != 0 && k >= tau;
+  __device__ __forceinline__ void add(uint64_t k, bool q, bool up, int lane) {
     const uint64_t m = __ballot(q);
     if (q) buf[cnt + __popcll(m & ((1ull << lane) - 1))] = k;
     cnt += __popcll(m);
-    tk_wait_lds();
     if (cnt >= 64) {
+      asm volatile("" ::: "memory");
       L = merge32v(L, sort64(buf[lane], up, lane), up, lane);
       const uint64_t rest = lane + 64 < cnt ? buf[lane + 64] : 0;
-      tk_wait_lds();
+      asm volatile("" ::: "memory");
       buf[lane] = rest;
       cnt -= 64;
-      tk_wait_lds();
     }
   }
-  if (cnt > 0) L = merge32v(L, sort64(lane < cnt ? buf[lane] : 0, up, lane), up, lane);
-  tk_wait_lds();
-  return L;
+  __device__ __forceinline__ uint64_t finish(bool up, int lane) {
+    asm volatile("" ::: "memory");
+    if (cnt > 0) L = merge32v(L, sort64(lane < cnt ? buf[lane] : 0, up, lane), up, lane);
+    asm volatile("" ::: "memory");
+    return L;
+  }
+};
+
+// Top 32 of the wavefront's 1024 keys, 16 per lane (0 = no key), descending
+// in lanes 0..31.  The 32nd largest of the 64 lane maxima, tau, bounds the
+// 32nd largest key from below (32 distinct keys are >= tau): only keys
+// >= tau are merged.
+__device__ uint64_t top32_chunk(const uint64_t (&k)[kTkPerLane], uint64_t *buf, bool up,
+                                int lane) {
+  uint64_t mx = 0;
+#pragma unroll
+  for (int t = 0; t < kTkPerLane; ++t) mx = k[t] > mx ? k[t] : mx;
+  const uint64_t tau = lane_u64(sort64(mx, up, lane), kTk - 1);
+  TopFeed f{buf};
+#pragma unroll
+  for (int t = 0; t < kTkPerLane; ++t) f.add(k[t], k[t] != 0 && k[t] >= tau, up, lane);
+  return f.finish(up, lane);
 }
 
 // Top 32 of nl <= 16 published lists (32 keys each, descending) at lists:
 // pairs of lists load as bitonic sequences (the second reversed), each pair
 // is merged, then a tree of merges.  All loads are issued before the first
-// is used.
+// is used, and the eight pair merges are independent chains that the
+// wavefront interleaves.
 __device__ uint64_t top32_lists(const uint64_t *lists, int nl, bool up, int lane) {
+  if (nl == 0) return 0;
   uint64_t v[8];
   const int e = lane < kTk ? lane : 63 - lane;
 #pragma unroll
@@ -176,11 +215,13 @@ __device__ uint64_t top32_lists(const uint64_t *lists, int nl, bool up, int lane
     v[p] = j < nl ? ld_coh64(lists + j * kTk + e) : 0;
   }
 #pragma unroll
-  for (int p = 0; p < 8; ++p) v[p] = bmerge64(v[p], up, lane);
+  for (int p = 0; p < 8; ++p)
+    if (2 * p < nl) v[p] = bmerge64(v[p], up, lane);
 #pragma unroll
   for (int w = 1; w < 8; w <<= 1)
 #pragma unroll
-    for (int p = 0; p < 8; p += 2 * w) v[p] = merge32v(v[p], v[p + w], up, lane);
+    for (int p = 0; p < 8; p += 2 * w)
+      if (2 * (p + w) < nl) v[p] = merge32v(v[p], v[p + w], up, lane);
   return v[0];
 }
 
@@ -206,7 +247,6 @@ __device__ bool wait_words(const int32_t *w, int cnt, Pred pred, int lane) {
 __global__ __launch_bounds__(64) void topk_kernel(const int32_t *y, int64_t n, int nchunks,
                                                   int32_t epoch, uint64_t *part, uint64_t *sup,
                                                   int32_t *flags, int32_t *out, int32_t *err) {
-  __shared__ uint64_t keys[kTkRows];
   __shared__ uint64_t buf[128];
   __shared__ int32_t rows[kTkRows];
   int32_t *pub = flags, *done = flags + kTopkMaxChunks, *spub = flags + 2 * kTopkMaxChunks;
@@ -215,13 +255,19 @@ __global__ __launch_bounds__(64) void topk_kernel(const int32_t *y, int64_t n, i
   const bool up = tk_ror4_up();
   const int64_t s0 = (int64_t)c * kTkRows;
   const int64_t end = n < s0 + kTkRows ? n : s0 + kTkRows;
-  for (int i = lane; i < kTkRows; i += 64) {
-    const int64_t r = s0 + i;
-    const int32_t v = r < end ? y[r] : 0;
-    rows[i] = v;
-    keys[i] = r < end ? tk_key(v, (uint32_t)r) : 0;
+  int32_t yv[kTkPerLane];   // rows s0 + lane + 64 t, loads all in flight
+#pragma unroll
+  for (int t = 0; t < kTkPerLane; ++t) {
+    const int64_t r = s0 + lane + 64 * t;
+    yv[t] = r < end ? y[r] : 0;
   }
-  __syncthreads();
+  uint64_t keys[kTkPerLane];
+#pragma unroll
+  for (int t = 0; t < kTkPerLane; ++t) {
+    const int64_t r = s0 + lane + 64 * t;
+    rows[lane + 64 * t] = yv[t];
+    keys[t] = r < end ? tk_key(yv[t], (uint32_t)r) : 0;
+  }
   const uint64_t own = top32_chunk(keys, buf, up, lane);
   if (lane < kTk) st_coh64(part + (int64_t)c * kTk + lane, own);
   wait_vm();
@@ -242,31 +288,54 @@ __global__ __launch_bounds__(64) void topk_kernel(const int32_t *y, int64_t n, i
   const uint64_t pre = merge32v(top32_lists(sup, s, up, lane), W, up, lane);
   // replay this chunk's arrivals
   uint64_t L = pre;
+  int32_t cv = tk_val(lane_u64(L, kTk - 1));   // entry 31's value (INT32_MIN while empty)
   int ovf = 0;
   for (int64_t g = s0; g < end && !ovf; g += 64) {
     const int64_t r = g + lane;
     const bool in = r < end;
     const int32_t v = in ? rows[r - s0] : 0;
-    const int32_t cv0 = tk_val(lane_u64(L, kTk - 1));
     // rows 0..31 always enter; later rows only at or above entry[31]
-    uint64_t cand = __ballot(in && (r < kTk || v >= cv0));
+    const bool isc = in && (r < kTk || v >= cv);
+    uint64_t cand = __ballot(isc);
+    if (__popcll(cand) > kTkSerialMax) {
+      // Only a row equal to an earlier row still in the list can set the
+      // overflow bit.  If no candidate's value equals a list entry's or
+      // another candidate's, the group cannot set it, and the list becomes
+      // the top 32 of the list and the group in one merge.
+      const uint64_t kv = isc ? tk_key(v, (uint32_t)r) : 0;
+      const uint64_t srt = sort64(kv, up, lane);
+      const uint64_t prv = shift_up1_u64(srt);
+      bool tie = lane > 0 && srt != 0 && (uint32_t)(srt >> 32) == (uint32_t)(prv >> 32);
+      // (an empty entry matching a value INT32_MIN only sends the group to
+      // the exact path below)
+      const uint32_t kh = (uint32_t)(kv >> 32), Lh = (uint32_t)(L >> 32);
+#pragma unroll 8
+      for (int e = 0; e < kTk; ++e)
+        tie = tie || (isc && (uint32_t)__builtin_amdgcn_readlane((int)Lh, e) == kh);
+      if (!__any(tie)) {
+        L = merge32v(L, srt, up, lane);
+        cv = tk_val(lane_u64(L, kTk - 1));
+        continue;
+      }
+    }
     while (cand) {
       const int j = __builtin_ctzll(cand);
       cand &= cand - 1;
       const int64_t rj = g + j;
       const int32_t vj = __builtin_amdgcn_readlane(v, j);
-      if (rj >= kTk) {
-        const int32_t cv = tk_val(lane_u64(L, kTk - 1));
-        if (vj < cv) continue;
-        if (vj == cv) {
-          ovf = 1;   // rejected while equal to entry[31]
-          break;
-        }
+      const bool first = rj < kTk;
+      if (!first && vj == cv) {
+        ovf = 1;   // rejected while equal to entry[31]
+        break;
       }
+      // insert at pos (64: rejected, nothing moves); branch-free
       const uint64_t kj = tk_key(vj, (uint32_t)rj);
-      const int pos = __popcll(__ballot(lane < kTk && L > kj));
-      const uint64_t upv = shfl_up1_u64(L);
-      if (lane < kTk && lane >= pos) L = lane == pos ? kj : upv;
+      const uint32_t gt = (uint32_t)__ballot(L > kj);   // entries above kj (lanes 0..31)
+      const int pos = first || vj > cv ? __popc(gt) : 64;
+      const int32_t e30 = tk_val(lane_u64(L, kTk - 2));
+      const uint64_t upv = shift_up1_u64(L);
+      L = lane == pos ? kj : (lane > pos ? upv : L);
+      cv = pos < kTk - 1 ? e30 : (pos == kTk - 1 ? vj : cv);
     }
   }
   if (c == nchunks - 1) {
