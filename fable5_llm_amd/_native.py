@@ -43,6 +43,8 @@ SIGNATURES = {
     "w4a8_dynq8": [_P, _P, _I32, _P, _P],
     "w4a8_rmsnorm": [_P, _P, _P, _I32, _I32, _I32, _P],
     "w4a8_movy": [_P, _P, _I64, _I32, _I32, _P],
+    "w4a8_movy_async": [_P, _P, _I64, _I32, _I32, _P],
+    "w4a8_movx_async": [_P, _P, _I64, _P],
     "w4a8_alu": [_P, _I32, _P, _P, _I64, _I32, _P],
     "w4a8_matvec_y32": [_P, _P, _P, _P],
     "w4a8_matvec_fused": [_P, _P, _I32, _P, _P, _I32, _I32, _I32, _I32, _P, _P,

@@ -160,6 +160,7 @@ int take_err(w4a8_ctx *c) {
       return fail(W4A8_E_HIP, "a wait between wavefronts of one workgroup timed out");
     if (h & 8)
       return fail(W4A8_E_HIP, "TOPK-32's wait for the lists of earlier chunks timed out");
+    if (h & 16) return fail(W4A8_E_RANGE, "MOVX source is not int8-packed");
   }
   return W4A8_OK;
 }
@@ -590,6 +591,30 @@ int w4a8_movy(w4a8_ctx *c, const int32_t *y32, int64_t n, int32_t shift, int32_t
   HIP_TRY(launch_movy(d_y, n, shift, mode, d_o, c->stream));
   HIP_TRY(hipMemcpyAsync(out, d_o, n * ob, hipMemcpyDeviceToHost, c->stream));
   HIP_TRY(hipStreamSynchronize(c->stream));
+  return W4A8_OK;
+}
+
+int w4a8_movy_async(w4a8_ctx *c, const int32_t *d_y32, int64_t n, int32_t shift,
+                    int32_t mode, void *d_out) {
+  if (!c || n < 0 || (n > 0 && (!d_y32 || !d_out))) return fail(W4A8_E_ARG, "bad argument");
+  if (mode != W4A8_MOVY_INT16 && mode != W4A8_MOVY_PAIRS32)
+    return fail(W4A8_E_ARG, "unknown MOVY mode");
+  if (((uintptr_t)d_y32 & 3) || ((uintptr_t)d_out & (mode == W4A8_MOVY_INT16 ? 1 : 3)))
+    return fail(W4A8_E_ARG, "MOVY: y32 and pairs32 output must be 4-byte aligned, int16 "
+                            "output 2-byte aligned");
+  if (n == 0) return W4A8_OK;
+  DeviceGuard g(c->device);
+  HIP_TRY(launch_movy(d_y32, n, shift, mode, d_out, c->stream));
+  return W4A8_OK;
+}
+
+int w4a8_movx_async(w4a8_ctx *c, const int16_t *d_src, int64_t n, int8_t *d_x8) {
+  if (!c || n < 0 || (n > 0 && (!d_src || !d_x8))) return fail(W4A8_E_ARG, "bad argument");
+  if (((uintptr_t)d_src & 1) || ((uintptr_t)d_x8 & 3))
+    return fail(W4A8_E_ARG, "MOVX: source must be 2-byte and x window 4-byte aligned");
+  if (n == 0) return W4A8_OK;
+  DeviceGuard g(c->device);
+  HIP_TRY(launch_movx(d_src, n, d_x8, c->d_err, c->stream));
   return W4A8_OK;
 }
 

@@ -192,6 +192,10 @@ constexpr int32_t kTopkEpochMax = 1 << 29;
 size_t topk_scratch_bytes(int64_t n);
 hipError_t launch_topk32(const int32_t *y, int64_t n, void *scratch, int32_t *flags,
                          int32_t epoch, int32_t *out, int32_t *err, hipStream_t s);
+// MOVX: int8 values in int16 words -> x window, tail to a 4-byte word
+// zeroed; bit 4 of err for a value outside int8
+hipError_t launch_movx(const int16_t *src, int64_t n, int8_t *dst, int32_t *err,
+                       hipStream_t s);
 // ALU ADD (op 4, gen_layer_script.py:1399-1400): out = clip16(a + b)
 hipError_t launch_add16(const int16_t *a, const int16_t *b, int64_t n, int16_t *out,
                         hipStream_t s);

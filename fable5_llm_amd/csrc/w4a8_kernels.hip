@@ -721,6 +721,27 @@ hipError_t launch_movy(const int32_t *y, int64_t n, int shift, int mode, void *o
   return hipGetLastError();
 }
 
+// MOVX (seq_model.py:929-952): the int8 values held in int16 scratch words
+// src[0, n) into the engine's x window, the ragged tail of the last 4-byte
+// word zeroed (SEQ_ISA B6); a value outside int8 sets bit 4 of err.
+__global__ void movx_kernel(const int16_t *src, int64_t n, int64_t nb, int8_t *dst,
+                            int32_t *err) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nb;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int16_t v = i < n ? src[i] : 0;
+    if (v < -128 || v > 127) atomicOr(err, 16);
+    dst[i] = (int8_t)v;
+  }
+}
+
+hipError_t launch_movx(const int16_t *src, int64_t n, int8_t *dst, int32_t *err,
+                       hipStream_t s) {
+  const int64_t nb = (n + 3) & ~(int64_t)3;
+  hipLaunchKernelGGL(movx_kernel, dim3(blocks_for(nb, 256, 4096)), dim3(256), 0, s, src, n,
+                     nb, dst, err);
+  return hipGetLastError();
+}
+
 __global__ void add16_kernel(const int16_t *a, const int16_t *b, int64_t n, int16_t *out) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x)

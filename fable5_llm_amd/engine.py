@@ -158,6 +158,17 @@ class Context:
                                   _ptr(out)), "movy")
         return out
 
+    def movy_async(self, d_y32, n, shift, mode, d_out):
+        """MOVY on device buffers (tensors or raw device addresses)."""
+        N.check(N.lib().w4a8_movy_async(self.h, _dptr(d_y32), int(n), int(shift), int(mode),
+                                        _dptr(d_out)), "movy_async")
+
+    def movx_async(self, d_src, n, d_x8):
+        """MOVX's data move on device buffers: n int8 values held in int16
+        words -> the x window (tail to a 4-byte word zeroed)."""
+        N.check(N.lib().w4a8_movx_async(self.h, _dptr(d_src), int(n), _dptr(d_x8)),
+                "movx_async")
+
     def alu(self, op, y32, p0, b=None):
         y = np.ascontiguousarray(np.asarray(y32, dtype=np.int32).reshape(-1))
         bb = None if b is None else np.ascontiguousarray(np.asarray(b, dtype=np.int16))

@@ -118,6 +118,18 @@ int w4a8_rmsnorm(w4a8_ctx *ctx, const int16_t *x16, const int16_t *w_q14,
 /* seq_model.py:1027-1050 MOVY: out is int16[n] (INT16) or int32[n] (PAIRS32) */
 int w4a8_movy(w4a8_ctx *ctx, const int32_t *y32, int64_t n, int32_t shift,
               int32_t mode, void *out);
+/* The same MOVY on device buffers, enqueued on the context stream (the
+   .seq MOVY record, seq_model.py:1027-1050; shift already resolved through
+   the XRF, seq_format.py:771-782).  d_y32 4-byte aligned; d_out 2-byte
+   (INT16) or 4-byte (PAIRS32) aligned. */
+int w4a8_movy_async(w4a8_ctx *ctx, const int32_t *d_y32, int64_t n,
+                    int32_t shift, int32_t mode, void *d_out);
+/* The .seq MOVX record's data move (seq_model.py:929-952): n int8 values
+   held in int16 scratch words -> the x window d_x8, the tail up to a 4-byte
+   word zeroed (SEQ_ISA B6).  A value outside int8 makes the next sync
+   return W4A8_E_RANGE ("MOVX source is not int8-packed"). */
+int w4a8_movx_async(w4a8_ctx *ctx, const int16_t *d_src, int64_t n,
+                    int8_t *d_x8);
 /* gen_layer_script.py:1397-1423 ALU ops on int32 pairs: SHIFT32, SILU32,
    EMUL32 (b = int16[n]) -> int16 out; SHIFT32W -> int32 out */
 int w4a8_alu(w4a8_ctx *ctx, int32_t op, const int32_t *y32, const int16_t *b,

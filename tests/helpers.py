@@ -1,5 +1,9 @@
 """Seeded synthetic inputs shared by the tests (no reference code)."""
+import json
+
 import numpy as np
+
+from fable5_llm_amd.w4a8_ref import row_beats
 
 from oracle import law
 
@@ -43,3 +47,38 @@ def activation_x16(rng, K, frac=7):
 def norm_weight_q14(rng, K):
     w = rng.normal(1.0, 0.1, K)
     return np.clip(np.rint(w * (1 << 14)), -32768, 32767).astype(np.int16)
+
+
+def hexlines(vals, bits):
+    """Data lines of a record script: one two's-complement hex word a line."""
+    return "".join(f"{int(v) & ((1 << bits) - 1):0{bits // 4}x}\n" for v in vals)
+
+
+def write_fixture_artifacts(d, scripts, tag):
+    """Write one reference script's fixture rows as a generator artifact in
+    directory d: <tag>_w<wid>.bin holding the fixture rows of each image,
+    <tag>.weights.json with those row counts, and <tag>.txt with each V
+    record's R / E / V records cut to the same rows.  Returns the number
+    of V records."""
+    man = {}
+    for key in scripts.files:
+        if key.startswith(f"{tag}_w") and key.endswith("_meta"):
+            wid = int(key[len(tag) + 2:-5])
+            _nr, k, ng, sh, e, stride = (int(v) for v in scripts[key])
+            rows = scripts[f"{tag}_w{wid}_rows"]
+            img = scripts[f"{tag}_w{wid}_img"]
+            (d / f"{tag}_w{wid}.bin").write_bytes(img.tobytes())
+            man[str(wid)] = {"file": f"{tag}_w{wid}.bin", "nrows": len(rows), "k": k,
+                             "ng": ng, "sh": sh, "e": e,
+                             "nbeats": len(rows) * sum(row_beats(k)), "stride": stride}
+    (d / f"{tag}.weights.json").write_text(json.dumps(man))
+    txt = []
+    nv = int(scripts[f"{tag}_counts"][0])
+    for v in range(nv):
+        wid, nin, _nr, e = (int(x) for x in scripts[f"{tag}_v{v}_hdr"])
+        x8 = scripts[f"{tag}_v{v}_x8"]
+        y = scripts[f"{tag}_v{v}_y32"]
+        txt.append(f"R 0 {nin:x}\n" + hexlines(x8, 16) + f"E {e:x}\n"
+                   + f"V {wid:x} 0 {nin:x} {len(y):x}\n" + hexlines(y, 32))
+    (d / f"{tag}.txt").write_text("".join(txt))
+    return nv

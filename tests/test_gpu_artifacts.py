@@ -12,38 +12,9 @@ from fable5_llm_amd import artifacts as A
 from fable5_llm_amd.w4a8_ref import row_beats
 from oracle import cfast, law
 from oracle.fixtures import script_tags
-from tests.helpers import rand_w4_m
+from tests.helpers import hexlines as _hex, rand_w4_m, write_fixture_artifacts as _write_from_fixtures
 
 pytestmark = pytest.mark.gpu
-
-
-def _hex(vals, bits):
-    return "".join(f"{int(v) & ((1 << bits) - 1):0{bits // 4}x}\n" for v in vals)
-
-
-def _write_from_fixtures(d, scripts, tag):
-    man = {}
-    for key in scripts.files:
-        if key.startswith(f"{tag}_w") and key.endswith("_meta"):
-            wid = int(key[len(tag) + 2:-5])
-            _nr, k, ng, sh, e, stride = (int(v) for v in scripts[key])
-            rows = scripts[f"{tag}_w{wid}_rows"]
-            img = scripts[f"{tag}_w{wid}_img"]
-            (d / f"{tag}_w{wid}.bin").write_bytes(img.tobytes())
-            man[str(wid)] = {"file": f"{tag}_w{wid}.bin", "nrows": len(rows), "k": k,
-                             "ng": ng, "sh": sh, "e": e,
-                             "nbeats": len(rows) * sum(row_beats(k)), "stride": stride}
-    (d / f"{tag}.weights.json").write_text(json.dumps(man))
-    txt = []
-    nv = int(scripts[f"{tag}_counts"][0])
-    for v in range(nv):
-        wid, nin, _nr, e = (int(x) for x in scripts[f"{tag}_v{v}_hdr"])
-        x8 = scripts[f"{tag}_v{v}_x8"]
-        y = scripts[f"{tag}_v{v}_y32"]
-        txt.append(f"R 0 {nin:x}\n" + _hex(x8, 16) + f"E {e:x}\n"
-                   + f"V {wid:x} 0 {nin:x} {len(y):x}\n" + _hex(y, 32))
-    (d / f"{tag}.txt").write_text("".join(txt))
-    return nv
 
 
 def test_replay_script_rows(engine, scripts, tmp_path):

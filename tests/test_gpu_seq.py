@@ -1,0 +1,137 @@
+"""The .seq matvec records on the device (fable5_llm_amd.seq.SeqMachine)
+against the oracle's machine model (oracle/seq_model.py) and the reference
+scripts' V records: MOVX / MVGO / MOVY with XRF indirection, XOP, no-wait
+MVGOs and FENCE, RES-sized row chunks of one image, the XWIN / RES banks."""
+import json
+
+import numpy as np
+import pytest
+
+from fable5_llm_amd import seq as S
+from fable5_llm_amd.artifacts import Artifacts, load_weights_manifest
+from fable5_llm_amd.w4a8_ref import row_beats
+from oracle import law
+from oracle.fixtures import script_tags
+from oracle.seq_model import SeqOracle, load_images
+from tests.helpers import rand_w4_m, write_fixture_artifacts
+from tests.seq_streams import (I16_ADDR, PAIRS_ADDR, X_ADDR, movx, movy, mvgo,
+                               v_record_stream, xrf_write)
+
+pytestmark = pytest.mark.gpu
+
+
+def test_script_records_on_device(engine, scripts, tmp_path):
+    nv = 0
+    for tag in script_tags():
+        write_fixture_artifacts(tmp_path, scripts, tag)
+        prefix = str(tmp_path / tag)
+        ents, _ = load_weights_manifest(prefix)
+        with Artifacts(engine, prefix) as art:
+            m = S.SeqMachine(engine, art)
+            for v in range(int(scripts[f"{tag}_counts"][0])):
+                x8, recs, y, p0 = v_record_stream(scripts, tag, v, ents, m.plan)
+                m.write_scratch(X_ADDR, x8)
+                m.run(recs)
+                assert np.array_equal(m.read_pairs(PAIRS_ADDR, y.size), y), (tag, v)
+                if p0 is not None:
+                    got = m.read_scratch(I16_ADDR, y.size).astype(np.int64)
+                    assert np.array_equal(got, law.movy(y, p0, law.MOVY_INT16)), (tag, v)
+                nv += 1
+    assert nv == 372
+
+
+def _synthetic(tmp_path, nrows=9000, K=1024, seed=8):
+    rng = np.random.default_rng(seed)
+    w4, m = rand_w4_m(rng, nrows, K)
+    img, stride = law.pack_ddr_rows(w4, m)
+    (tmp_path / "q_w0.bin").write_bytes(bytes(img))
+    w4b, mb = rand_w4_m(rng, 512, 2048)
+    imgb, strideb = law.pack_ddr_rows(w4b, mb)
+    (tmp_path / "q_w1.bin").write_bytes(bytes(imgb))
+    man = {"0": {"file": "q_w0.bin", "nrows": nrows, "k": K, "ng": K // 128,
+                 "sh": law.sh_for_k(K), "e": -4, "nbeats": nrows * sum(row_beats(K)),
+                 "stride": stride},
+           "1": {"file": "q_w1.bin", "nrows": 512, "k": 2048, "ng": 16,
+                 "sh": law.sh_for_k(2048), "e": -5, "nbeats": 512 * sum(row_beats(2048)),
+                 "stride": strideb}}
+    (tmp_path / "q.weights.json").write_text(json.dumps(man))
+    return str(tmp_path / "q"), man, rng
+
+
+def _both(engine, prefix, man, stage, recs):
+    """Run recs on the device and in the oracle after staging scratch."""
+    ents, _ = load_weights_manifest(prefix)
+    plan = S.plan_weights(ents)
+    o = SeqOracle(load_images(prefix, ents), plan)
+    with Artifacts(engine, prefix) as art:
+        m = S.SeqMachine(engine, art)
+        for addr, vals in stage:
+            m.write_scratch(addr, vals)
+            o.mem[addr:addr + len(vals)] = vals
+        m.run(recs)
+        o.run(S.pack_stream(recs))
+        got = m.read_scratch(0, o.mem.size).astype(np.int64)
+    return got, o
+
+
+def test_row_chunks_banks_xop_nowait(engine, tmp_path):
+    prefix, man, rng = _synthetic(tmp_path)
+    plan = S.plan_weights({k: v for k, v in man.items()})
+    e0, e1 = man["0"], man["1"]
+    s0, s1 = e0["stride"], e1["stride"]
+    xa = rng.integers(-127, 128, 1024)
+    xb = rng.integers(-127, 128, 2048)
+    stage = [(0, xa), (2048, xb)]
+    recs = [xrf_write(S.XRF_EX, 3), xrf_write(S.XRF_K_ATTN, 2),
+            # o_proj-style shift in XRF[5]: 21 - e_x - k_a
+            S.Rec(S.EXT_XOP, target=S.XRF_OSHIFT,
+                  imm32=S.xop_imm(0, S.XOP_NEG, 2, S.XOP_NEG, 21)),
+            movx(0, 0, 0, 1024),
+            movx(1, S.XBANK_WORD, 2048, 2048)]
+    # the 9000-row image in RES-sized chunks (WBASE = base + r0 * stride),
+    # alternating RES banks on channel 0
+    out = 16384
+    for i, r0 in enumerate(range(0, 9000, 2048)):
+        n = min(2048, 9000 - r0)
+        recs += [mvgo(0, plan[0] + r0 * s0, 8, n, e0["sh"], s0, rbank=i & 1),
+                 movy(0, S.RBANK_ROW * (i & 1), n, out + 2 * r0)]
+    # channel 1: no-wait MVGO from the x bank, FENCE, then MOVY int16 through
+    # XRF[5] (IND_ADD) and through XRF[0] (IND_SUB)
+    recs += [mvgo(1, plan[1], 16, 512, e1["sh"], s1, xbank=1, nowait=True),
+             S.Rec(S.OP_FENCE, target=0b0010),
+             movy(1, 0, 512, 40000, imm=0, int16=True, ind=S.IND_ADD, xrf=S.XRF_OSHIFT),
+             movy(1, 100, 300, 41000, imm=12, int16=True, ind=S.IND_SUB, xrf=S.XRF_EX),
+             S.Rec(S.OP_HALT), movx(0, 0, 0, 1024)]          # after HALT: not run
+    got, o = _both(engine, prefix, man, stage, recs)
+    assert np.array_equal(got, o.mem)
+    assert o.xrf[S.XRF_OSHIFT] == 16
+    # the chunks joined give the whole image's y32
+    y_full = o.pairs(out, 9000)
+    assert np.array_equal(y_full, np.concatenate(
+        [o.pairs(out + 2 * r0, min(2048, 9000 - r0)) for r0 in range(0, 9000, 2048)]))
+    assert np.count_nonzero(y_full) > 8000
+
+
+def test_hazards_refused_on_device(engine, tmp_path):
+    prefix, man, rng = _synthetic(tmp_path, nrows=64)
+    plan = S.plan_weights(man)
+    e0 = man["0"]
+    with Artifacts(engine, prefix) as art:
+        m = S.SeqMachine(engine, art)
+        m.write_scratch(0, rng.integers(-127, 128, 1024))
+        m.run([movx(2, 0, 0, 1024), mvgo(2, plan[0], 8, 64, e0["sh"], e0["stride"],
+                                         nowait=True)])
+        for bad in (movy(2, 0, 64, 9000), movx(2, 0, 0, 1024),
+                    mvgo(2, plan[0], 8, 64, e0["sh"], e0["stride"])):
+            with pytest.raises(S.RunningChannelError):
+                m.step(bad)
+        m.run([S.Rec(S.OP_FENCE), movy(2, 0, 64, 9000)])
+        with pytest.raises(RuntimeError, match="not inside one MVGO"):
+            m.step(movy(2, 32, 64, 9000))
+        with pytest.raises(S.SeqUnsupported):
+            m.step(S.Rec(S.OP_CMD))
+        # a MOVX of a value outside int8 is reported at the next sync
+        m.write_scratch(0, [200] + [0] * 1023)
+        m.step(movx(0, 0, 0, 1024))
+        with pytest.raises(AssertionError, match="int8"):
+            engine.sync()
