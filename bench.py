@@ -171,9 +171,9 @@ def ffn_leg(st, ctx, steps, warmup):
             "us_per_layer": round(ms * 1e3 / len(layers), 2),
             "value": round(nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s",
             "pct_of_peak_hbm": round(100.0 * nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 1),
-            "bytes_per_pass": nbytes, "launches_per_layer": 4,
-            "chain": "RMSNorm->DYNQ8->gate SILU32 + up SHIFT32W (one launch), EMUL32, "
-                     "DYNQ8->down SHIFT32, residual ADD"}, keep
+            "bytes_per_pass": nbytes, "launches_per_layer": 2,
+            "chain": "RMSNorm->DYNQ8->gate SILU32 + up SHIFT32W (one launch); "
+                     "EMUL32->DYNQ8->down SHIFT32->residual ADD (one launch)"}, keep
 
 
 def head_leg(st, ctx, steps, warmup):

@@ -892,16 +892,15 @@ int w4a8_mlp_async(w4a8_ctx *c, const w4a8_weights *gate, const w4a8_weights *up
   if (FFN > 16383)
     return fail(W4A8_E_RANGE, "FFN width " + std::to_string(FFN) +
                                   " does not fit an ALU count (max 16383)");
-  // temporaries: sg int16[FFN], u int32[FFN], prod int16[FFN], y int16[H]
+  if (!d_mlp_out && !d_res_out) return fail(W4A8_E_ARG, "mlp: no output requested");
+  // temporaries: sg int16[FFN], u int32[FFN]
   auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
-  const size_t o_u = al(2 * FFN), o_p = o_u + al(4 * FFN), o_y = o_p + al(2 * FFN);
+  const size_t o_u = al(2 * FFN);
   DeviceGuard g(c->device);
-  int rc0 = ensure_chain(c, o_y + al(2 * H));
+  int rc0 = ensure_chain(c, o_u + al(4 * FFN));
   if (rc0) return rc0;
   int16_t *sg = (int16_t *)c->d_chain;
   int32_t *u = (int32_t *)(c->d_chain + o_u);
-  int16_t *prod = (int16_t *)(c->d_chain + o_p);
-  int16_t *y = d_mlp_out ? d_mlp_out : (int16_t *)(c->d_chain + o_y);
   // gate and up share the input: one launch, RMSNorm (or not) -> DYNQ8
   const w4a8_weights *gu[2] = {gate, up};
   const int32_t epi_gu[2] = {EPI_SILU32, EPI_MOVY_P32};
@@ -911,14 +910,24 @@ int w4a8_mlp_async(w4a8_ctx *c, const w4a8_weights *gate, const w4a8_weights *up
                        d_norm_w ? PRO_RMSNORM_DYNQ8 : PRO_DYNQ8, d_x16, d_norm_w, in_f,
                        one_plus, 0, nullptr, nullptr, nullptr);
   if (rc) return rc;
-  // EMUL32 at p0 = 12 (gen_layer_script.py:2182-2184)
-  HIP_TRY(launch_alu(W4A8_ALU_EMUL32, u, sg, FFN, 12, c->d_tables, prod, c->stream));
+  // down: EMUL32 at p0 = 12 (gen_layer_script.py:2182-2184) formed in its
+  // prologue, then DYNQ8; MOVY int16, and the residual ADD
+  // (gen_layer_script.py:1399-1400) in its epilogue
   const int32_t epi_d = EPI_MOVY_I16;
-  void *out_d = y;
-  rc = site_launch(c, 1, &down, &epi_d, &p0_down, &out_d, PRO_DYNQ8, prod, nullptr, 0, 0,
+  void *out_d = d_mlp_out ? (void *)d_mlp_out : (void *)d_res_out;
+  GemvParams P;
+  rc = site_params(c, P, 1, &down, &epi_d, &p0_down, &out_d, PRO_DYNQ8, sg, nullptr, 0, 0,
                    0, nullptr, nullptr, nullptr);
   if (rc) return rc;
-  if (d_res_out) HIP_TRY(launch_add16(d_x16, y, H, d_res_out, c->stream));
+  P.job[0].out = d_mlp_out;
+  P.pro = PRO_EMUL_DYNQ8;
+  P.x2 = u;
+  if (d_res_out) {
+    P.job[0].epi = EPI_MOVY_I16_ADD;
+    P.job[0].res = d_x16;
+    P.job[0].res_out = d_res_out;
+  }
+  HIP_TRY(launch_gemv(P, grid_for(c, P.total_tiles), c->stream));
   return W4A8_OK;
 }
 

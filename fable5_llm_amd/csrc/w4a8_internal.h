@@ -44,11 +44,17 @@ constexpr int kMaxJobs = 6;
 constexpr int kWG = 256;         // threads per workgroup (4 wavefronts)
 constexpr int kWaves = kWG / 64;
 
-enum Prologue { PRO_X8 = 0, PRO_DYNQ8 = 1, PRO_RMSNORM_DYNQ8 = 2 };
+// PRO_EMUL_DYNQ8 (gemv_kernel only, the FFN block's down projection):
+// x16 = clip16(rs(x2 * x, 12)) with x int16 (SILU32 of the gate) and x2
+// int32 (the up projection), i.e. ALU EMUL32 at p0 = 12, then DYNQ8.
+enum Prologue { PRO_X8 = 0, PRO_DYNQ8 = 1, PRO_RMSNORM_DYNQ8 = 2, PRO_EMUL_DYNQ8 = 3 };
+// EPI_MOVY_I16_ADD (gemv_kernel only): EPI_MOVY_I16 into out (when set),
+// and clip16(res[row] + that) into res_out (ALU ADD, the block's residual).
 enum Epilogue {
   EPI_Y32 = 0, EPI_MOVY_I16 = 1, EPI_MOVY_P32 = 2, EPI_SILU32 = 3,
-  EPI_SHIFT_I64 = 4, EPI_ARGMAX = 5
+  EPI_SHIFT_I64 = 4, EPI_ARGMAX = 5, EPI_MOVY_I16_ADD = 6
 };
+constexpr int kEmulP0 = 12;   // EMUL32's shift in the SwiGLU block
 
 struct Layout {
   int32_t K, NG, nblk;
@@ -95,6 +101,8 @@ struct GemvJob {
   int32_t epi;
   int32_t p0;         // epilogue shift = p0 - e_x
   int32_t pad_;
+  const int16_t *res;   // EPI_MOVY_I16_ADD: residual input
+  int16_t *res_out;     // EPI_MOVY_I16_ADD: residual output
 };
 
 struct GemvParams {
@@ -117,6 +125,7 @@ struct GemvParams {
   const int32_t *tables;    // kTableLen entries
   int32_t *err;             // bit 0: y32 overflow; bit 2: an LDS wait gave up
   uint64_t *partials;       // EPI_ARGMAX: one key per workgroup
+  const int32_t *x2;        // PRO_EMUL_DYNQ8: int32[K]
 };
 
 // launchers (all asynchronous on `s`)

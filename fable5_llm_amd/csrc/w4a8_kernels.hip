@@ -58,6 +58,28 @@ __device__ __forceinline__ void pro_load(const GemvParams &P, ProRegs<NT> &X, in
     const int base = c * NT * 8 + tid * 8;
     X.pc[c] = *(const int4 *)(x16 + (base < K ? base : K - 8));
   }
+  if (P.pro == PRO_EMUL_DYNQ8) {
+    // the product is formed here, so the prologue group waits for its
+    // loads now; the weight wavefronts already have their blocks in flight
+    int4 a[ProRegs<NT>::kPc][2];
+#pragma unroll
+    for (int c = 0; c < ProRegs<NT>::kPc; ++c) {
+      const int base = c * NT * 8 + tid * 8;
+      const int32_t *p = P.x2 + (base < K ? base : K - 8);
+      a[c][0] = *(const int4 *)p;
+      a[c][1] = *(const int4 *)(p + 4);
+    }
+#pragma unroll
+    for (int c = 0; c < ProRegs<NT>::kPc; ++c) {
+      const int32_t av[8] = {a[c][0].x, a[c][0].y, a[c][0].z, a[c][0].w,
+                             a[c][1].x, a[c][1].y, a[c][1].z, a[c][1].w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int64_t v = movy_shift((int64_t)av[j] * piece_get(X.pc[c], j), kEmulP0);
+        piece_set(X.pc[c], j, (int16_t)clamp64(v, -32768, 32767));
+      }
+    }
+  }
   if (P.pro == PRO_RMSNORM_DYNQ8) {
 #pragma unroll
     for (int c = 0; c < ProRegs<NT>::kNw; ++c) {
@@ -311,6 +333,12 @@ __device__ __forceinline__ void team_tile_finish(const GemvJob &J, int t, bool v
         case EPI_MOVY_I16:
           ((int16_t *)J.out)[row] = (int16_t)clamp64(movy_shift(y, shift), -32768, 32767);
           break;
+        case EPI_MOVY_I16_ADD: {
+          const int64_t v = clamp64(movy_shift(y, shift), -32768, 32767);
+          if (J.out) ((int16_t *)J.out)[row] = (int16_t)v;
+          J.res_out[row] = (int16_t)clamp64(v + J.res[row], -32768, 32767);
+          break;
+        }
         case EPI_MOVY_P32:
           ((int32_t *)J.out)[row] =
               (int32_t)clamp64(movy_shift(y, shift), -2147483648LL, 2147483647LL);

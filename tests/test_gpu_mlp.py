@@ -135,3 +135,34 @@ def test_mlp_async_rejects_mismatched_shapes(engine):
     finally:
         for w in ws.values():
             w.free()
+
+
+def test_mlp_async_residual_only_and_no_output(engine):
+    # d_mlp_out null: only the residual sum is written; both null is refused
+    rng = np.random.default_rng(12)
+    H, FFN = 512, 1536
+    q = _mats(rng, H, FFN)
+    ws, imgs = {}, {}
+    for k, v in q.items():
+        ws[k], imgs[k] = _upload(engine, v)
+    rs_f = 7
+    x16 = activation_x16(rng, H, rs_f)
+    p0s = [(15 - E_SCALE - q[k][3]) + rs_f - out_f
+           for k, out_f in (("gate", 12), ("up", rs_f), ("down", rs_f))]
+    dev = torch.device("cuda", 0)
+    xd = torch.from_numpy(x16.copy()).to(dev)
+    rd = torch.full((H,), 0x1234, dtype=torch.int16, device=dev)
+    torch.cuda.synchronize()
+    try:
+        engine.mlp_async(ws["gate"], ws["up"], ws["down"], p0s, xd, in_f=rs_f,
+                         mlp_out=None, res_out=rd)
+        engine.sync()
+        ref_y = _oracle_mlp(q, imgs, x16, rs_f)
+        ref_r = law.clip16(x16.astype(np.int64) + ref_y)
+        assert np.array_equal(rd.cpu().numpy().astype(np.int64), ref_r)
+        with pytest.raises(ValueError, match="no output"):
+            engine.mlp_async(ws["gate"], ws["up"], ws["down"], p0s, xd, in_f=rs_f,
+                             mlp_out=None, res_out=None)
+    finally:
+        for w in ws.values():
+            w.free()
