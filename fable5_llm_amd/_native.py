@@ -57,6 +57,7 @@ SIGNATURES = {
                         _I32, _P, _P, _P],
     "w4a8_head_argmax_async": [_P, _P, _I32, _P, _P, _I32, _I32, _I32, _P],
     "w4a8_matmul_y32_async": [_P, _P, _P, _I32, _P],
+    "w4a8_matmul_y32_multi_async": [_P, _I32, _P, _P, _I32, _P],
     "w4a8_topk32": [_P, _P, _I64, _P, _P, _P, _P],
     "w4a8_head_topk32": [_P, _P, _I32, _P, _P, _I32, _I32, _P, _P, _P, _P],
     "w4a8_head_topk32_async": [_P, _P, _I32, _P, _P, _I32, _I32, _I32, _P],

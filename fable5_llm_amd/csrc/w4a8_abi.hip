@@ -780,6 +780,23 @@ int w4a8_matmul_y32_async(w4a8_ctx *c, const w4a8_weights *w, const int8_t *d_x8
   return W4A8_OK;
 }
 
+int w4a8_matmul_y32_multi_async(w4a8_ctx *c, int32_t n, const w4a8_weights *const *w,
+                                const int8_t *const *d_x8, int32_t B, int32_t *const *d_y32) {
+  if (!c || !w || !d_x8 || !d_y32) return fail(W4A8_E_ARG, "null argument");
+  if (n < 1 || n > kMmJobs)
+    return fail(W4A8_E_RANGE, "matmul_multi: 1.." + std::to_string(kMmJobs) + " matrices");
+  if (B < 1 || B > 64) return fail(W4A8_E_RANGE, "batch must be 1..64");
+  MmJobSpec jobs[kMmJobs];
+  for (int i = 0; i < n; ++i) {
+    if (!w[i] || !d_x8[i] || !d_y32[i]) return fail(W4A8_E_ARG, "null weights / x8 / y32");
+    if (!aligned16(d_x8[i])) return fail(W4A8_E_ARG, "x8 must be 16-byte aligned");
+    jobs[i] = MmJobSpec{w[i]->d, (int32_t)w[i]->nrows, w[i]->L, w[i]->sh, d_x8[i], d_y32[i]};
+  }
+  DeviceGuard g(c->device);
+  HIP_TRY(launch_matmul_multi(jobs, n, B, c->d_err, c->stream));
+  return W4A8_OK;
+}
+
 // ------------------------------------------------------------ TOPK-32
 // One TOPK-32 launch on the context's stream.  Flags hold the epochs of
 // earlier launches; they are cleared (by a kernel, so that a captured graph

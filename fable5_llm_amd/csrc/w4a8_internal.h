@@ -209,6 +209,20 @@ hipError_t launch_movx(const int16_t *src, int64_t n, int8_t *dst, int32_t *err,
 hipError_t launch_add16(const int16_t *a, const int16_t *b, int64_t n, int16_t *out,
                         hipStream_t s);
 hipError_t launch_vec_prologue(const GemvParams &p, hipStream_t s);
+// Several matrices for the same B tokens in one batched launch (jobs run
+// one after another on each workgroup, the weight stream running on across
+// them); at most kMmJobs.
+constexpr int kMmJobs = 16;
+struct MmJobSpec {
+  const uint8_t *w;   // tile layout
+  int32_t nrows;
+  Layout L;
+  int32_t sh;
+  const int8_t *x8;   // [B][K]
+  int32_t *y32;       // [B][nrows]
+};
+hipError_t launch_matmul_multi(const MmJobSpec *jobs, int n, int32_t B, int32_t *err,
+                               hipStream_t s);
 hipError_t launch_matmul(const uint8_t *w, int32_t nrows, const Layout &L,
                          int32_t sh, const int8_t *x8, int32_t B,
                          int32_t *y32, int32_t *err, hipStream_t s);

@@ -29,7 +29,11 @@
 //
 // A workgroup works through its tiles in rounds of up to TM tiles (TM * CT
 // <= 4, CT = column tiles of 16 tokens), block-major within a round, so that
-// each block's activations serve every tile of the round.  Every wait between wavefronts is bounded: a wait that gives
+// each block's activations serve every tile of the round.  One launch may
+// carry several matrices (jobs, same tokens, each its own activations): a
+// workgroup's rounds run through its tiles of job 0, then job 1, ..., and
+// the ring, the loaders and the weight pieces in flight run on across the
+// job boundaries, so the weight stream does not drain between matrices.  Every wait between wavefronts is bounded: a wait that gives
 // up sets bit 2 of the error word and an abort word, after which no wait of
 // the workgroup polls again, so a launch always drains.
 #include "w4a8_device.h"
@@ -44,7 +48,6 @@ constexpr int kMW = 8;                     // group wavefronts 0..7
 constexpr int kML = 3;                     // loader wavefronts 8..10 (at most)
 constexpr int kMStore = kMW + kML;         // the store wavefront, 11
 constexpr int kMThreads = (kMW + kML + 1) * 64;
-constexpr int kMD = 16;                    // weight pieces in flight per group wavefront
 constexpr int kXRow = 1024 + 16;           // LDS bytes per token of a block's activations
 constexpr int kMBufDword3 = 0x00020000;    // raw buffer, 32-bit data format
 constexpr int kMAuxNt = 2;                 // buffer-load cache policy: non-temporal
@@ -53,17 +56,24 @@ constexpr int kLdsBytes = 160 * 1024;
 
 static_assert(kXRow % 16 == 0, "token rows stay 16-byte aligned");
 
-struct MmParams {
+struct MmJob {
   const uint8_t *W;     // tile layout
   const int8_t *x8;     // [B][K]
   int32_t *y32;         // [B][nrows]
-  int32_t *err;
   int64_t tile_bytes;
-  int32_t nrows, ntiles, NG, nblk, sh, K, B, CT;
+  int32_t nrows, ntiles, NG, nblk, sh, K;
   int32_t tm;           // tiles per round
+  int32_t pad;
+};
+
+struct MmParams {
+  MmJob job[kMmJobs];
+  int32_t njobs;
+  int32_t B, CT;
   int32_t R;            // LDS slots
   int32_t nl;           // loader wavefronts in use
   int32_t slot_bytes;   // 16 * CT token rows of kXRow, then tm scale rows of 256 B
+  int32_t *err;
 };
 
 // LDS: flags, then the reduction tables, then the ring of slots
@@ -75,6 +85,11 @@ struct MmFlags {
   int32_t abort;
   int32_t err;
   int32_t pad[2];
+  // this workgroup's schedule: job j has nmine[j] of its tiles, global
+  // rounds rbase[j] .. rbase[j + 1] - 1 and steps sbase[j] .. sbase[j + 1] - 1
+  int32_t nmine[kMmJobs];
+  int32_t rbase[kMmJobs + 1];
+  int32_t sbase[kMmJobs + 1];
 };
 constexpr int kFlagBytes = (int)((sizeof(MmFlags) + 255) / 256 * 256);
 
@@ -156,23 +171,57 @@ __device__ __forceinline__ void mm_wait_word(MmFlags &F, const int32_t *p, int v
   }
 }
 
-// A workgroup's tiles are r, r + G, ...; round rho takes tiles rho*tm ..
-// rho*tm + nt - 1 of them, and step s = rho * nblk + kb covers block kb of
-// every tile of round rho.
-__device__ __forceinline__ int round_tiles(const MmParams &P, int nmine, int rho) {
-  return min(P.tm, nmine - rho * P.tm);
+// A workgroup's tiles of a job are r, r + G, ...; the job's round rho takes
+// tiles rho*tm .. rho*tm + nt - 1 of them, and the job's step
+// rho * nblk + kb covers block kb of every tile of round rho.
+__device__ __forceinline__ int round_tiles(const MmJob &J, int nmine, int rho) {
+  return min(J.tm, nmine - rho * J.tm);
+}
+
+// Position in this workgroup's schedule: job j, its round rho and block kb;
+// RHO and S count rounds and steps over all jobs.  Jobs with no tile on this
+// workgroup are skipped.
+struct MmCur {
+  int j, rho, kb, RHO;
+  __device__ void start(const MmFlags &F, int njobs) {
+    j = 0;
+    rho = kb = RHO = 0;
+    while (j < njobs && F.rbase[j + 1] == 0) ++j;
+  }
+  __device__ void next(const MmFlags &F, const MmParams &P) {
+    if (++kb < P.job[j].nblk) return;
+    kb = 0;
+    ++rho;
+    ++RHO;
+    while (j < P.njobs && RHO == F.rbase[j + 1]) {
+      ++j;
+      rho = 0;
+    }
+  }
+};
+
+// job and position of global step s (s < sbase[njobs])
+__device__ __forceinline__ int mm_job_of_step(const MmFlags &F, int njobs, int s) {
+  int j = 0;
+  while (j + 1 < njobs && s >= F.sbase[j + 1]) ++j;
+  return j;
+}
+__device__ __forceinline__ int mm_job_of_round(const MmFlags &F, int njobs, int RHO) {
+  int j = 0;
+  while (j + 1 < njobs && RHO >= F.rbase[j + 1]) ++j;
+  return j;
 }
 
 // Put group 8 kb + w of tile j of round rho in flight: a buffer load whose
 // range is empty (no memory access, zeros) when there is no such tile or
 // group, so every step issues the same loads.
-__device__ __forceinline__ uint4 mm_issue(const MmParams &P, int r, int G, int w, int lane,
+__device__ __forceinline__ uint4 mm_issue(const MmJob &J, int r, int G, int w, int lane,
                                           int rho, int kb, int j, bool real) {
-  const uint8_t *base = P.W;
+  const uint8_t *base = J.W;
   int len = 0;
-  if (real && 8 * kb + w < P.NG) {
-    const int64_t t = (int64_t)r + (int64_t)G * (rho * P.tm + j);
-    base = P.W + t * P.tile_bytes + (int64_t)kb * kBlockBytes + kScaleChunk +
+  if (real && 8 * kb + w < J.NG) {
+    const int64_t t = (int64_t)r + (int64_t)G * (rho * J.tm + j);
+    base = J.W + t * J.tile_bytes + (int64_t)kb * kBlockBytes + kScaleChunk +
            (int64_t)w * kGroupChunk;
     len = kGroupChunk;
   }
@@ -198,9 +247,6 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = gridDim.x, r = blockIdx.x;
-  const int nmine = r < P.ntiles ? (P.ntiles - 1 - r) / G + 1 : 0;
-  const int nrounds = (nmine + P.tm - 1) / P.tm;
-  const int nsteps = nrounds * P.nblk;
 
   if (tid < kRingMax) F.ready[tid] = -1;
   if (tid < kMW) F.done[tid] = -1;
@@ -211,15 +257,28 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
   if (tid == 0) {
     F.abort = 0;
     F.err = 0;
+    F.rbase[0] = F.sbase[0] = 0;
+    for (int j = 0; j < P.njobs; ++j) {
+      const MmJob &J = P.job[j];
+      const int nm = r < J.ntiles ? (J.ntiles - 1 - r) / G + 1 : 0;
+      const int nr = (nm + J.tm - 1) / J.tm;
+      F.nmine[j] = nm;
+      F.rbase[j + 1] = F.rbase[j] + nr;
+      F.sbase[j + 1] = F.sbase[j] + nr * J.nblk;
+    }
   }
   for (int i = tid; i < 2 * TMX * CTX * 4 * 64; i += kMThreads) tables[i] = 0;
   __syncthreads();
+  const int nrounds = F.rbase[P.njobs], nsteps = F.sbase[P.njobs];
 
   if (wave == kMStore) {
     // round rho's sums are complete once all 8 group wavefronts have added
     bool ok = true;
-    for (int rho = 0; rho < nrounds; ++rho) {
-      const int tb = rho & 1, nt = round_tiles(P, nmine, rho);
+    for (int RHO = 0; RHO < nrounds; ++RHO) {
+      const int jb = mm_job_of_round(F, P.njobs, RHO);
+      const MmJob &J = P.job[jb];
+      const int rho = RHO - F.rbase[jb];
+      const int tb = RHO & 1, nt = round_tiles(J, F.nmine[jb], rho);
       int64_t *tbl = tables + tb * (TMX * CTX * 4 * 64);
       if (!mm_wait(F, [&] { return lds_read_i32(&F.tcnt[tb]) == kMW; })) {
         ok = false;
@@ -227,7 +286,7 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
       }
       const int q = lane >> 4, c = lane & 15;
       for (int jj = 0; jj < nt; ++jj) {
-        const int64_t t = (int64_t)r + (int64_t)G * (rho * P.tm + jj);
+        const int64_t t = (int64_t)r + (int64_t)G * (rho * J.tm + jj);
         for (int ct = 0; ct < P.CT; ++ct) {
           for (int e = 0; e < 4; ++e) {
             int64_t &v = tbl[((jj * CTX + ct) * 4 + e) * 64 + lane];
@@ -235,10 +294,10 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
             v = 0;
             const int64_t row = t * kTileRows + 4 * q + e;
             const int tok = ct * 16 + c;
-            if (tok < P.B && row < P.nrows) {
-              const int64_t y = rshr64_mm(tot >> 4, P.sh);   // tot = 16 p
+            if (tok < P.B && row < J.nrows) {
+              const int64_t y = rshr64_mm(tot >> 4, J.sh);   // tot = 16 p
               if (y > 2147483647LL || y < -2147483647LL) mm_lds_or(&F.err, 1);
-              P.y32[(int64_t)tok * P.nrows + row] = (int32_t)y;
+              J.y32[(int64_t)tok * J.nrows + row] = (int32_t)y;
             }
           }
         }
@@ -246,7 +305,7 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
       wait_lds();
       if (lane == 0) {
         lds_write_i32(&F.tcnt[tb], 0);
-        lds_write_i32(&F.tgen[tb], rho + 2);
+        lds_write_i32(&F.tgen[tb], RHO + 2);
       }
     }
     if (!ok && lane == 0) mm_lds_or(&F.err, 4);
@@ -255,24 +314,27 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
     const int l = wave - kMW;
     if (l < P.nl) {
       for (int s = l; s < nsteps; s += P.nl) {
-        const int rho = s / P.nblk, kb = s - rho * P.nblk;
+        const int jb = mm_job_of_step(F, P.njobs, s);
+        const MmJob &J = P.job[jb];
+        const int ls = s - F.sbase[jb];
+        const int rho = ls / J.nblk, kb = ls - rho * J.nblk;
         const int slot = s % P.R;
         // the slot's previous step has been consumed by every group wavefront
         if (s >= P.R &&
             !mm_wait(F, [&] { return lds_read_i32(&F.done[lane & (kMW - 1)]) >= s - P.R; }))
           break;
         uint8_t *sb = ring + (size_t)slot * P.slot_bytes;
-        const int kbytes = min(1024, P.K - kb * 1024);   // multiple of 128
+        const int kbytes = min(1024, J.K - kb * 1024);   // multiple of 128
         for (int tok = 0; tok < P.B; ++tok) {
           const int8_t *src = 16 * lane < kbytes
-                                  ? P.x8 + (int64_t)tok * P.K + kb * 1024 + 16 * lane
-                                  : P.x8;   // nothing to copy: any mapped address
+                                  ? J.x8 + (int64_t)tok * J.K + kb * 1024 + 16 * lane
+                                  : J.x8;   // nothing to copy: any mapped address
           dma16(src, lds_off(sb + tok * kXRow));
         }
-        const int nt = round_tiles(P, nmine, rho);
+        const int nt = round_tiles(J, F.nmine[jb], rho);
         for (int j = 0; j < nt; ++j) {
-          const int64_t t = (int64_t)r + (int64_t)G * (rho * P.tm + j);
-          dma4(P.W + t * P.tile_bytes + (int64_t)kb * kBlockBytes + 4 * lane,
+          const int64_t t = (int64_t)r + (int64_t)G * (rho * J.tm + j);
+          dma4(J.W + t * J.tile_bytes + (int64_t)kb * kBlockBytes + 4 * lane,
                lds_off(sb + 16 * P.CT * kXRow + 256 * j));
         }
         mm_wait_vm_all();
@@ -292,25 +354,26 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
         for (int e = 0; e < 4; ++e) p[a][b][e] = 0;
     // wr[j][d]: tile j's piece of the step s with s % D == d
     uint4 wr[TMX][D];
-    int f_rho = 0, f_kb = 0;   // next step to put in flight
+    MmCur f, cur;   // next step to put in flight; the step being computed
+    f.start(F, P.njobs);
+    cur.start(F, P.njobs);
     auto fill = [&](uint4 (&slot)[TMX][D], const int d) {
-      const int nt = f_rho < nrounds ? round_tiles(P, nmine, f_rho) : 0;
+      const bool any = f.RHO < nrounds;
+      const MmJob &J = P.job[any ? f.j : 0];
+      const int nt = any ? round_tiles(J, F.nmine[f.j], f.rho) : 0;
 #pragma unroll
       for (int j = 0; j < TMX; ++j)
-        slot[j][d] = mm_issue(P, r, G, w, lane, f_rho, f_kb, j, j < nt);
-      if (++f_kb == P.nblk) {
-        f_kb = 0;
-        ++f_rho;
-      }
+        slot[j][d] = mm_issue(J, r, G, w, lane, f.rho, f.kb, j, j < nt);
+      if (any) f.next(F, P);
     };
 #pragma unroll
     for (int d = 0; d < D; ++d) fill(wr, d);
-    int s = 0, rho = 0, kb = 0;
+    int s = 0;
     for (;;) {
 #pragma unroll
       for (int d = 0; d < D; ++d) {
         if (s >= nsteps) goto finished;
-        const int nt = round_tiles(P, nmine, rho);
+        const int nt = round_tiles(P.job[cur.j], F.nmine[cur.j], cur.rho);
         const int slot = s % P.R;
         mm_wait_word<false>(F, &F.ready[slot], s, lane);
         const uint8_t *sb = ring + (size_t)slot * P.slot_bytes;
@@ -353,11 +416,11 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
         fill(wr, d);
         wait_lds();   // this wavefront's reads of the slot are done
         if (lane == 0) lds_write_i32(&F.done[w], s);
-        if (kb == P.nblk - 1) {
-          // end of round rho: add this wavefront's sums into its table
-          const int tb = rho & 1;
+        if (cur.kb == P.job[cur.j].nblk - 1) {
+          // end of round RHO: add this wavefront's sums into its table
+          const int tb = cur.RHO & 1;
           int64_t *tbl = tables + tb * (TMX * CTX * 4 * 64);
-          mm_wait_word<true>(F, &F.tgen[tb], rho, lane);
+          mm_wait_word<true>(F, &F.tgen[tb], cur.RHO, lane);
 #pragma unroll
           for (int jj = 0; jj < TMX; ++jj)
 #pragma unroll
@@ -370,11 +433,8 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
               }
           wait_lds();   // the adds are done before the count
           if (lane == 0) mm_lds_add_rtn(&F.tcnt[tb], 1);
-          kb = 0;
-          ++rho;
-        } else {
-          ++kb;
         }
+        cur.next(F, P);
         ++s;
       }
     }
@@ -389,23 +449,14 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
 
 }  // namespace
 
-hipError_t launch_matmul(const uint8_t *w, int32_t nrows, const Layout &L, int32_t sh,
-                         const int8_t *x8, int32_t B, int32_t *y32, int32_t *err,
-                         hipStream_t s) {
+hipError_t launch_matmul_multi(const MmJobSpec *jobs, int n, int32_t B, int32_t *err,
+                               hipStream_t s) {
+  if (n < 1 || n > kMmJobs || B < 1 || B > 64) return hipErrorInvalidValue;
   MmParams P{};
-  P.W = w;
-  P.x8 = x8;
-  P.y32 = y32;
-  P.err = err;
-  P.tile_bytes = L.tile_bytes;
-  P.nrows = nrows;
-  P.ntiles = (nrows + kTileRows - 1) / kTileRows;
-  P.NG = L.NG;
-  P.nblk = L.nblk;
-  P.sh = sh;
-  P.K = L.K;
+  P.njobs = n;
   P.B = B;
   P.CT = (B + 15) / 16;
+  P.err = err;
   const int tmx = P.CT == 1 ? 4 : (P.CT == 2 ? 2 : 1);
   const int table_bytes = 2 * tmx * (tmx == 4 ? 1 : (tmx == 2 ? 2 : 4)) * 4 * 64 * 8;
   P.slot_bytes = 16 * P.CT * kXRow + tmx * 256;
@@ -417,11 +468,29 @@ hipError_t launch_matmul(const uint8_t *w, int32_t nrows, const Layout &L, int32
   int dev = 0, ncu = 256;
   if (hipGetDevice(&dev) == hipSuccess)
     (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+  int maxt = 1;
+  for (int j = 0; j < n; ++j) {
+    MmJob &J = P.job[j];
+    const MmJobSpec &q = jobs[j];
+    J.W = q.w;
+    J.x8 = q.x8;
+    J.y32 = q.y32;
+    J.tile_bytes = q.L.tile_bytes;
+    J.nrows = q.nrows;
+    J.ntiles = (q.nrows + kTileRows - 1) / kTileRows;
+    J.NG = q.L.NG;
+    J.nblk = q.L.nblk;
+    J.sh = q.sh;
+    J.K = q.L.K;
+    maxt = J.ntiles > maxt ? J.ntiles : maxt;
+  }
+  const int G = maxt < ncu ? maxt : ncu;
   // rounds of tm tiles: as many tiles per round as the workgroups' shares
-  // allow, at most tmx
-  const int G = P.ntiles < ncu ? P.ntiles : ncu;
-  const int per = (P.ntiles + G - 1) / G;
-  P.tm = per < tmx ? per : tmx;
+  // of the job allow, at most tmx
+  for (int j = 0; j < n; ++j) {
+    const int per = (P.job[j].ntiles + G - 1) / G;
+    P.job[j].tm = per < tmx ? per : tmx;
+  }
   const size_t lds = (size_t)kFlagBytes + table_bytes + (size_t)P.R * P.slot_bytes;
   // dynamic LDS beyond the default limit: allowed once per process
   static const hipError_t attr = [] {
@@ -444,6 +513,13 @@ hipError_t launch_matmul(const uint8_t *w, int32_t nrows, const Layout &L, int32
     hipLaunchKernelGGL((matmul_kernel<1, 4>), dim3(G), dim3(kMThreads), lds, s, P);
   }
   return hipGetLastError();
+}
+
+hipError_t launch_matmul(const uint8_t *w, int32_t nrows, const Layout &L, int32_t sh,
+                         const int8_t *x8, int32_t B, int32_t *y32, int32_t *err,
+                         hipStream_t s) {
+  const MmJobSpec j{w, nrows, L, sh, x8, y32};
+  return launch_matmul_multi(&j, 1, B, err, s);
 }
 
 }  // namespace w4a8

@@ -283,6 +283,18 @@ class Context:
         N.check(N.lib().w4a8_matmul_y32_async(self.h, w.h, _dptr(x8), x8.shape[0],
                                               _dptr(y32)), "matmul")
 
+    def matmul_multi_async(self, weights, x8s, y32s):
+        """Several matrices for the same B tokens in one launch (device
+        tensors x8s[i] [B][K_i], y32s[i] [B][nrows_i])."""
+        n = len(weights)
+        assert n == len(x8s) == len(y32s)
+        B = x8s[0].shape[0]
+        assert all(x.shape[0] == B for x in x8s) and all(y.shape[0] == B for y in y32s)
+        wa = (ctypes.c_void_p * n)(*[w.h.value for w in weights])
+        xa = (ctypes.c_void_p * n)(*[x.data_ptr() for x in x8s])
+        ya = (ctypes.c_void_p * n)(*[y.data_ptr() for y in y32s])
+        N.check(N.lib().w4a8_matmul_y32_multi_async(self.h, n, wa, xa, B, ya), "matmul_multi")
+
     def mlp_async(self, gate, up, down, p0s, x16, norm_w=None, in_f=0, one_plus=False,
                   mlp_out=None, res_out=None):
         """The SwiGLU block on device tensors (w4a8_mlp_async): optional

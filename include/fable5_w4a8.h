@@ -179,6 +179,16 @@ int w4a8_head_argmax_async(w4a8_ctx *ctx, const w4a8_weights *w,
                            int32_t one_plus, int32_t e_x, int32_t *d_result);
 int w4a8_matmul_y32_async(w4a8_ctx *ctx, const w4a8_weights *w,
                           const int8_t *d_x8, int32_t B, int32_t *d_y32);
+/* n <= 16 matrices for the same B tokens in one launch (e.g. a layer's
+   gate and up, which share x8): matrix i reads d_x8[i] [B][K_i] and writes
+   d_y32[i] [B][nrows_i], each row bit-identical to w4a8_matmul_y32_async of
+   that matrix alone.  The weight stream runs on across the matrices instead
+   of draining at each launch's end.  No counterpart in the reference's C
+   interface (its engine runs one matrix per MVGO). */
+int w4a8_matmul_y32_multi_async(w4a8_ctx *ctx, int32_t n,
+                                const w4a8_weights *const *w,
+                                const int8_t *const *d_x8, int32_t B,
+                                int32_t *const *d_y32);
 
 /* ---- TOPK-32 over the LM head -----------------------------------------
  * The layer_topk32 block's contract (docs/SEQ_ISA.md B8): the head's raw

@@ -356,3 +356,37 @@ def test_matmul_matches_per_token(engine, B, N_, K):
     for b in range(B):
         assert np.array_equal(got[b], cfast.matvec_y32_img(img, N_, K, sh, x8[b])), b
     w.free()
+
+
+@pytest.mark.parametrize("B", [1, 5, 16, 33, 64])
+def test_matmul_multi_matches_per_token(engine, B):
+    # matrices of different shapes in one launch, two sharing x8, some with
+    # fewer tiles than the grid (workgroups with no tile of a job skip it)
+    import torch
+    rng = np.random.default_rng(900 + B)
+    shapes = [(12288, 4096), (12288, 4096), (40, 256), (4096, 12288), (100, 1024), (33, 3584)]
+    dev = torch.device("cuda", 0)
+    ws, imgs, xs, ys = [], [], [], []
+    xk = {}
+    for i, (N_, K) in enumerate(shapes):
+        img, _ = rand_image(rng, N_, K)
+        ws.append(engine.upload(img, N_, K, law.sh_for_k(K)))
+        imgs.append(img)
+        if K not in xk or i == 3:
+            xk[K] = rng.integers(-128, 128, (B, K)).astype(np.int8)
+        xs.append(xk[K])
+        ys.append(torch.full((B, N_), 0x5A5A5A5A, dtype=torch.int32, device=dev))
+    xd = {id(x): torch.from_numpy(x).to(dev) for x in xs}
+    try:
+        engine.matmul_multi_async(ws, [xd[id(x)] for x in xs], ys)
+        engine.sync()
+        for i, (N_, K) in enumerate(shapes):
+            got = ys[i].cpu().numpy()
+            for b in range(B):
+                ref = cfast.matvec_y32_img(imgs[i], N_, K, law.sh_for_k(K), xs[i][b])
+                assert np.array_equal(got[b], ref), (i, b)
+        with pytest.raises(AssertionError, match="1..16"):
+            engine.matmul_multi_async(ws * 3, [xd[id(x)] for x in xs] * 3, ys * 3)
+    finally:
+        for w in ws:
+            w.free()
