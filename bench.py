@@ -58,6 +58,41 @@ def pmc_traffic(kernel):
 METRIC = "achieved HBM GB/s (% of peak) on W4A8 GEMV; ms per 9B-shape weight stream"
 
 
+def time_passes(ctx, one_pass, stream, steps, warmup):
+    """ms per pass of `one_pass` submitted from Python (eager) and replayed
+    as one HIP graph captured from it (the launches alone, without the host
+    issuing each call); both timed with events on `stream`."""
+    import torch
+
+    def timed(fn):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            fn()
+        e1.record(stream)
+        ctx.sync()
+        torch.cuda.synchronize(stream.device)
+        return e0.elapsed_time(e1) / steps
+
+    for _ in range(warmup):
+        one_pass()
+    ctx.sync()
+    eager = timed(one_pass)
+    side = torch.cuda.Stream(stream.device)
+    g = torch.cuda.CUDAGraph()
+    try:
+        with torch.cuda.graph(g, stream=side):
+            ctx.set_stream(side)
+            one_pass()
+    finally:
+        ctx.set_stream(stream)
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize(stream.device)
+    return timed(g.replay), eager
+
+
 def batched_leg(st, ctx, batches, steps, warmup, seed):
     """The FFN matrices of the stream (32 x gate, up: 12288 x 4096; down:
     4096 x 12288; 2.49 GB, far beyond the 256 MB Infinity Cache) through the
@@ -101,21 +136,11 @@ def batched_leg(st, ctx, batches, steps, warmup, seed):
                                        [x8[m.K] for m in ms],
                                        [y[(mi, m.nrows)] for mi, m in zip(mis, ms)])
 
-        for _ in range(warmup):
-            one_pass()
-        ctx.sync()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(steps):
-            one_pass()
-        e1.record(stream)
-        ctx.sync()
-        torch.cuda.synchronize(dev)
-        ms = e0.elapsed_time(e1) / steps
+        ms, ms_eager = time_passes(ctx, one_pass, stream, steps, warmup)
         gbs = nbytes / (ms * 1e-3) / 1e9
         tops = ops / (ms * 1e-3) / 1e12
         out.append({"B": B, "matrices": len(ffn), "ms_per_pass": round(ms, 4),
+                    "ms_per_pass_eager": round(ms_eager, 4), "timing": "HIP graph of one pass",
                     "value": round(gbs, 1), "unit": "GB/s",
                     "pct_of_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 1),
                     "tops": round(tops, 2),
@@ -164,22 +189,12 @@ def ffn_leg(st, ctx, steps, warmup):
             ctx.mlp_async(wg, wu, wd, p0s, x, norm_w=nw, in_f=s.in_f,
                           one_plus=s.one_plus, mlp_out=y, res_out=res)
 
-    for _ in range(warmup):
-        one_pass()
-    ctx.sync()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(steps):
-        one_pass()
-    e1.record(stream)
-    ctx.sync()
-    torch.cuda.synchronize(dev)
-    ms = e0.elapsed_time(e1) / steps
+    ms, ms_eager = time_passes(ctx, one_pass, stream, steps, warmup)
     nbytes = sum(l[-1] for l in layers)
     si, wg, wu, wd, p0s, x, nw, s, y, res, _ = layers[0]
     keep = (si, p0s, x.cpu().numpy(), nw.cpu().numpy(), y.cpu().numpy(), res.cpu().numpy())
     return {"layers": len(layers), "ms_per_pass": round(ms, 4),
+            "ms_per_pass_eager": round(ms_eager, 4), "timing": "HIP graph of one pass",
             "us_per_layer": round(ms * 1e3 / len(layers), 2),
             "value": round(nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s",
             "pct_of_peak_hbm": round(100.0 * nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 1),

@@ -285,23 +285,48 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
         break;
       }
       const int q = lane >> 4, c = lane & 15;
-      for (int jj = 0; jj < nt; ++jj) {
-        const int64_t t = (int64_t)r + (int64_t)G * (rho * J.tm + jj);
-        for (int ct = 0; ct < P.CT; ++ct) {
+      // the job's fields, read once (kept in registers across the stores)
+      int32_t *const yj = J.y32;
+      const int32_t nrj = J.nrows, shj = J.sh, tmj = J.tm;
+      const int64_t half = shj > 0 ? (int64_t)1 << (shj - 1) : 0;
+      // every table entry read at once, then rounded, checked and stored
+      int64_t tot[TMX][CTX][4];
+#pragma unroll
+      for (int jj = 0; jj < TMX; ++jj)
+#pragma unroll
+        for (int ct = 0; ct < CTX; ++ct)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            tot[jj][ct][e] = tbl[((jj * CTX + ct) * 4 + e) * 64 + lane];
+#pragma unroll
+      for (int jj = 0; jj < TMX; ++jj)
+#pragma unroll
+        for (int ct = 0; ct < CTX; ++ct)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            tbl[((jj * CTX + ct) * 4 + e) * 64 + lane] = 0;
+      bool ovf = false;
+#pragma unroll
+      for (int ct = 0; ct < CTX; ++ct) {
+        const int tok = ct * 16 + c;
+        int32_t *const yt = yj + (int64_t)tok * nrj;
+#pragma unroll
+        for (int jj = 0; jj < TMX; ++jj) {
+          const int64_t row0 = ((int64_t)r + (int64_t)G * (rho * tmj + jj)) * kTileRows + 4 * q;
+#pragma unroll
           for (int e = 0; e < 4; ++e) {
-            int64_t &v = tbl[((jj * CTX + ct) * 4 + e) * 64 + lane];
-            const int64_t tot = v;
-            v = 0;
-            const int64_t row = t * kTileRows + 4 * q + e;
-            const int tok = ct * 16 + c;
-            if (tok < P.B && row < J.nrows) {
-              const int64_t y = rshr64_mm(tot >> 4, J.sh);   // tot = 16 p
-              if (y > 2147483647LL || y < -2147483647LL) mm_lds_or(&F.err, 1);
-              J.y32[(int64_t)tok * J.nrows + row] = (int32_t)y;
+            // y = rshift_round(tot / 16, sh): the magnitude rounded half up
+            const int64_t v = tot[jj][ct][e] >> 4;   // tot = 16 p
+            const int64_t m = ((v < 0 ? -v : v) + half) >> shj;
+            const int64_t y = v < 0 ? -m : m;
+            if (jj < nt && ct < P.CT && tok < P.B && row0 + e < nrj) {
+              ovf = ovf || y > 2147483647LL || y < -2147483647LL;
+              yt[row0 + e] = (int32_t)y;
             }
           }
         }
       }
+      if (ovf) mm_lds_or(&F.err, 1);
       wait_lds();
       if (lane == 0) {
         lds_write_i32(&F.tcnt[tb], 0);
