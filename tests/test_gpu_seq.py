@@ -130,6 +130,20 @@ def test_hazards_refused_on_device(engine, tmp_path):
             m.step(movy(2, 32, 64, 9000))
         with pytest.raises(S.SeqUnsupported):
             m.step(S.Rec(S.OP_CMD))
+        # ranges outside scratch, the x window, RES or the channels are
+        # refused on the host, before any kernel is launched
+        words = m.scratch.numel()
+        for bad in (movx(0, 0, words - 100, 1024),                  # scratch source
+                    movx(0, S.XBANK_WORD + 1500, 0, 1024),           # x window
+                    movx(5, 0, 0, 1024),                             # channel
+                    movy(2, 0, 64, words - 10, int16=True),          # scratch target
+                    movy(2, 0, 64, words - 100),                     # pairs32 target
+                    mvgo(2, plan[0], 8, 4096, e0["sh"], e0["stride"], rbank=1)):   # RES
+            with pytest.raises(ValueError):
+                m.step(bad)
+        m.run([movx(3, 0, 0, 512)])
+        with pytest.raises(ValueError, match="x bytes"):             # x shorter than K
+            m.step(mvgo(3, plan[0], 8, 64, e0["sh"], e0["stride"]))
         # a MOVX of a value outside int8 is reported at the next sync
         m.write_scratch(0, [200] + [0] * 1023)
         m.step(movx(0, 0, 0, 1024))
