@@ -23,6 +23,33 @@ def _dptr(t):
     return ctypes.c_void_p(0 if t is None else t.data_ptr())
 
 
+def _dev(t, need_bytes, name, required=True):
+    """Check a device tensor handed to a kernel as a raw pointer: on the
+    device, contiguous and at least need_bytes long (the C ABI cannot see a
+    pointer's extent, so a short buffer would be written past).  None passes
+    when the argument is optional."""
+    if t is None:
+        if required:
+            raise ValueError(f"{name}: a device tensor is required")
+        return
+    if not getattr(t, "is_cuda", False):
+        raise ValueError(f"{name}: must be a device tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: must be contiguous")
+    have = t.numel() * t.element_size()
+    if have < need_bytes:
+        raise ValueError(f"{name}: {have} bytes, the call touches {need_bytes}")
+
+
+# bytes per output row of each epilogue
+_EPI_BYTES = {N.EPI_Y32: 4, N.EPI_MOVY_I16: 2, N.EPI_MOVY_P32: 4, N.EPI_SILU32: 2,
+              N.EPI_SHIFT_I64: 8}
+
+
+def _x_bytes(prologue, K):
+    return K if prologue == N.PRO_X8 else 2 * K
+
+
 def wire_stride(K):
     ng = K // 128
     return (ng + (ng + 31) // 32) * 64
@@ -159,13 +186,17 @@ class Context:
         return out
 
     def movy_async(self, d_y32, n, shift, mode, d_out):
-        """MOVY on device buffers (tensors or raw device addresses)."""
+        """MOVY on device tensors: n int32 -> int16 (INT16) or int32 (PAIRS32)."""
+        _dev(d_y32, 4 * n, "movy y32")
+        _dev(d_out, (2 if mode == N.MOVY_INT16 else 4) * n, "movy out")
         N.check(N.lib().w4a8_movy_async(self.h, _dptr(d_y32), int(n), int(shift), int(mode),
                                         _dptr(d_out)), "movy_async")
 
     def movx_async(self, d_src, n, d_x8):
         """MOVX's data move on device buffers: n int8 values held in int16
         words -> the x window (tail to a 4-byte word zeroed)."""
+        _dev(d_src, 2 * n, "movx source")
+        _dev(d_x8, (n + 3) // 4 * 4, "movx x window")
         N.check(N.lib().w4a8_movx_async(self.h, _dptr(d_src), int(n), _dptr(d_x8)),
                 "movx_async")
 
@@ -247,6 +278,9 @@ class Context:
 
     def head_topk32_async(self, w, x, out, prologue=N.PRO_DYNQ8, e_x=0, norm_w=None,
                           in_f=0, one_plus=False):
+        _dev(x, _x_bytes(prologue, w.K), "x")
+        _dev(norm_w, 2 * w.K, "norm_w", required=False)
+        _dev(out, 66 * 4, "out")
         N.check(N.lib().w4a8_head_topk32_async(
             self.h, w.h, int(prologue), _dptr(x), _dptr(norm_w), int(in_f),
             1 if one_plus else 0, int(e_x), _dptr(out)), "head_topk32")
@@ -264,6 +298,16 @@ class Context:
                    e_x=0, norm_w=None, in_f=0, one_plus=False, x8_out=None,
                    e_x_out=None, xn_out=None):
         n = len(weights)
+        if not (n == len(epilogues) == len(p0s) == len(outs)):
+            raise ValueError("site: one epilogue, p0 and output per matrix")
+        K = weights[0].K
+        for w, e, o in zip(weights, epilogues, outs):
+            _dev(o, _EPI_BYTES.get(int(e), 8) * w.nrows, "site output")
+        _dev(x, _x_bytes(prologue, K), "x")
+        _dev(norm_w, 2 * K, "norm_w", required=False)
+        _dev(x8_out, K, "x8_out", required=False)
+        _dev(e_x_out, 4, "e_x_out", required=False)
+        _dev(xn_out, 2 * K, "xn_out", required=False)
         wa = (ctypes.c_void_p * n)(*[w.h.value for w in weights])
         oa = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
         ea = np.ascontiguousarray(epilogues, dtype=np.int32)
@@ -275,11 +319,17 @@ class Context:
 
     def head_argmax_async(self, w, x, result, prologue=N.PRO_DYNQ8, e_x=0,
                           norm_w=None, in_f=0, one_plus=False):
+        _dev(x, _x_bytes(prologue, w.K), "x")
+        _dev(norm_w, 2 * w.K, "norm_w", required=False)
+        _dev(result, 8, "result")
         N.check(N.lib().w4a8_head_argmax_async(
             self.h, w.h, int(prologue), _dptr(x), _dptr(norm_w), int(in_f),
             1 if one_plus else 0, int(e_x), _dptr(result)), "head_argmax")
 
     def matmul_async(self, w, x8, y32):
+        B = x8.shape[0]
+        _dev(x8, B * w.K, "x8")
+        _dev(y32, 4 * B * w.nrows, "y32")
         N.check(N.lib().w4a8_matmul_y32_async(self.h, w.h, _dptr(x8), x8.shape[0],
                                               _dptr(y32)), "matmul")
 
@@ -287,9 +337,14 @@ class Context:
         """Several matrices for the same B tokens in one launch (device
         tensors x8s[i] [B][K_i], y32s[i] [B][nrows_i])."""
         n = len(weights)
-        assert n == len(x8s) == len(y32s)
+        if not n == len(x8s) == len(y32s):
+            raise ValueError("matmul_multi: one x8 and one y32 per matrix")
         B = x8s[0].shape[0]
-        assert all(x.shape[0] == B for x in x8s) and all(y.shape[0] == B for y in y32s)
+        for w, x, y in zip(weights, x8s, y32s):
+            if x.shape[0] != B or y.shape[0] != B:
+                raise ValueError("matmul_multi: every x8 and y32 holds the same B tokens")
+            _dev(x, B * w.K, "x8")
+            _dev(y, 4 * B * w.nrows, "y32")
         wa = (ctypes.c_void_p * n)(*[w.h.value for w in weights])
         xa = (ctypes.c_void_p * n)(*[x.data_ptr() for x in x8s])
         ya = (ctypes.c_void_p * n)(*[y.data_ptr() for y in y32s])
@@ -301,6 +356,11 @@ class Context:
         RMSNorm, gate / up, EMUL32, down; mlp_out = int16[H] block output,
         res_out = clip16(x16 + mlp_out) (may be x16 itself)."""
         pg, pu, pd = (int(p) for p in p0s)
+        H = gate.K
+        _dev(x16, 2 * H, "x16")
+        _dev(norm_w, 2 * H, "norm_w", required=False)
+        _dev(mlp_out, 2 * H, "mlp_out", required=False)
+        _dev(res_out, 2 * H, "res_out", required=False)
         N.check(N.lib().w4a8_mlp_async(
             self.h, gate.h, up.h, down.h, pg, pu, pd, _dptr(x16), _dptr(norm_w),
             int(in_f), 1 if one_plus else 0, _dptr(mlp_out), _dptr(res_out)), "mlp")
@@ -336,6 +396,16 @@ class Plan:
                  e_x=0, norm_w=None, in_f=0, one_plus=False, x8_out=None,
                  e_x_out=None, xn_out=None):
         n = len(weights)
+        if not (n == len(epilogues) == len(p0s) == len(outs)):
+            raise ValueError("site: one epilogue, p0 and output per matrix")
+        K = weights[0].K
+        for w, e, o in zip(weights, epilogues, outs):
+            _dev(o, _EPI_BYTES.get(int(e), 8) * w.nrows, "site output")
+        _dev(x, _x_bytes(prologue, K), "x")
+        _dev(norm_w, 2 * K, "norm_w", required=False)
+        _dev(x8_out, K, "x8_out", required=False)
+        _dev(e_x_out, 4, "e_x_out", required=False)
+        _dev(xn_out, 2 * K, "xn_out", required=False)
         wa = (ctypes.c_void_p * n)(*[w.h.value for w in weights])
         oa = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
         ea = np.ascontiguousarray(epilogues, dtype=np.int32)
@@ -351,6 +421,9 @@ class Plan:
 
     def add_head(self, w, x, result, prologue=N.PRO_DYNQ8, e_x=0, norm_w=None,
                  in_f=0, one_plus=False):
+        _dev(x, _x_bytes(prologue, w.K), "x")
+        _dev(norm_w, 2 * w.K, "norm_w", required=False)
+        _dev(result, 8, "result")
         N.check(N.lib().w4a8_plan_add_head(
             self.h, w.h, int(prologue), _dptr(x), _dptr(norm_w), int(in_f),
             1 if one_plus else 0, int(e_x), _dptr(result)), "plan_add_head")

@@ -4,6 +4,8 @@ import ctypes
 import os
 import re
 
+import pytest
+
 from fable5_llm_amd import _native
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -59,3 +61,15 @@ def test_single_hip_runtime_in_process():
     out = subprocess.run([sys.executable, "-c", code], capture_output=True,
                          text=True, timeout=120).stdout.split()
     assert out == ["1", "1"], out
+
+
+def test_device_wrappers_refuse_short_buffers():
+    # the wrappers check device tensors before a raw pointer reaches C (no
+    # GPU needed: the checks run first, and CPU tensors are refused)
+    import torch
+    from fable5_llm_amd import engine as E
+    with pytest.raises(ValueError, match="required"):
+        E._dev(None, 4, "x")
+    E._dev(None, 4, "x", required=False)
+    with pytest.raises(ValueError, match="device tensor"):
+        E._dev(torch.zeros(4, dtype=torch.int32), 16, "x")
