@@ -205,9 +205,6 @@ hipError_t launch_topk32(const int32_t *y, int64_t n, void *scratch, int32_t *fl
 // zeroed; bit 4 of err for a value outside int8
 hipError_t launch_movx(const int16_t *src, int64_t n, int8_t *dst, int32_t *err,
                        hipStream_t s);
-// ALU ADD (op 4, gen_layer_script.py:1399-1400): out = clip16(a + b)
-hipError_t launch_add16(const int16_t *a, const int16_t *b, int64_t n, int16_t *out,
-                        hipStream_t s);
 hipError_t launch_vec_prologue(const GemvParams &p, hipStream_t s);
 // Several matrices for the same B tokens in one batched launch (jobs run
 // one after another on each workgroup, the weight stream running on across

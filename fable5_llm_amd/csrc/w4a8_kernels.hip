@@ -770,19 +770,6 @@ hipError_t launch_movx(const int16_t *src, int64_t n, int8_t *dst, int32_t *err,
   return hipGetLastError();
 }
 
-__global__ void add16_kernel(const int16_t *a, const int16_t *b, int64_t n, int16_t *out) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x)
-    out[i] = (int16_t)clamp64((int64_t)a[i] + (int64_t)b[i], -32768, 32767);
-}
-
-hipError_t launch_add16(const int16_t *a, const int16_t *b, int64_t n, int16_t *out,
-                        hipStream_t s) {
-  hipLaunchKernelGGL(add16_kernel, dim3(blocks_for(n, 256, 4096)), dim3(256), 0, s, a, b, n,
-                     out);
-  return hipGetLastError();
-}
-
 hipError_t launch_alu(int op, const int32_t *y, const int16_t *b, int64_t n, int p0,
                       const int32_t *tables, void *out, hipStream_t s) {
   hipLaunchKernelGGL(alu_kernel, dim3(blocks_for(n, 256, 4096)), dim3(256), 0, s,

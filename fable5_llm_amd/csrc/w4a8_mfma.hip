@@ -234,8 +234,9 @@ __device__ __forceinline__ uint4 mm_issue(const MmJob &J, int r, int G, int w, i
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// steps in flight per group wavefront: TMX pieces each
-template <int TMX>
+// steps in flight per group wavefront: TMX pieces each (one tile a round,
+// as for a matrix with no more tiles than workgroups, goes 8 steps deep)
+template <int TMX, int CTX>
 constexpr int mm_depth() { return TMX >= 4 ? 4 : 8; }
 
 template <int TMX, int CTX>
@@ -369,7 +370,7 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
   } else {
     const int w = wave;
     const int q = lane >> 4, c = lane & 15;
-    constexpr int D = mm_depth<TMX>();
+    constexpr int D = mm_depth<TMX, CTX>();
     int64_t p[TMX][CTX][4];
 #pragma unroll
     for (int a = 0; a < TMX; ++a)
@@ -482,14 +483,7 @@ hipError_t launch_matmul_multi(const MmJobSpec *jobs, int n, int32_t B, int32_t 
   P.B = B;
   P.CT = (B + 15) / 16;
   P.err = err;
-  const int tmx = P.CT == 1 ? 4 : (P.CT == 2 ? 2 : 1);
-  const int table_bytes = 2 * tmx * (tmx == 4 ? 1 : (tmx == 2 ? 2 : 4)) * 4 * 64 * 8;
-  P.slot_bytes = 16 * P.CT * kXRow + tmx * 256;
-  const int avail = kLdsBytes - kFlagBytes - table_bytes;
-  P.R = avail / P.slot_bytes;
-  if (P.R > kRingMax) P.R = kRingMax;
-  if (P.R < 2) return hipErrorInvalidValue;
-  P.nl = P.R - 1 < kML ? P.R - 1 : kML;   // >= 1: R >= 2
+  int tmx = P.CT == 1 ? 4 : (P.CT == 2 ? 2 : 1);
   int dev = 0, ncu = 256;
   if (hipGetDevice(&dev) == hipSuccess)
     (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
@@ -510,6 +504,22 @@ hipError_t launch_matmul_multi(const MmJobSpec *jobs, int n, int32_t B, int32_t 
     maxt = J.ntiles > maxt ? J.ntiles : maxt;
   }
   const int G = maxt < ncu ? maxt : ncu;
+  // one tile per workgroup in every job: rounds of one tile, with the deeper
+  // weight pipeline of the one-tile kernels
+  int maxper = 1;
+  for (int j = 0; j < n; ++j) {
+    const int per = (P.job[j].ntiles + G - 1) / G;
+    maxper = per > maxper ? per : maxper;
+  }
+  if (maxper == 1) tmx = 1;
+  const int ctxt = tmx == 4 ? 1 : (tmx == 2 ? 2 : (P.CT <= 2 ? P.CT : 4));
+  const int table_bytes = 2 * tmx * ctxt * 4 * 64 * 8;
+  P.slot_bytes = 16 * P.CT * kXRow + tmx * 256;
+  const int avail = kLdsBytes - kFlagBytes - table_bytes;
+  P.R = avail / P.slot_bytes;
+  if (P.R > kRingMax) P.R = kRingMax;
+  if (P.R < 2) return hipErrorInvalidValue;
+  P.nl = P.R - 1 < kML ? P.R - 1 : kML;   // >= 1: R >= 2
   // rounds of tm tiles: as many tiles per round as the workgroups' shares
   // of the job allow, at most tmx
   for (int j = 0; j < n; ++j) {
@@ -527,13 +537,23 @@ hipError_t launch_matmul_multi(const MmJobSpec *jobs, int n, int32_t B, int32_t 
     if (e == hipSuccess)
       e = hipFuncSetAttribute((const void *)matmul_kernel<1, 4>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute((const void *)matmul_kernel<1, 1>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute((const void *)matmul_kernel<1, 2>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
     return e;
   }();
   if (attr != hipSuccess) return attr;
-  if (P.CT == 1) {
+  if (tmx == 4) {
     hipLaunchKernelGGL((matmul_kernel<4, 1>), dim3(G), dim3(kMThreads), lds, s, P);
-  } else if (P.CT == 2) {
+  } else if (tmx == 2) {
     hipLaunchKernelGGL((matmul_kernel<2, 2>), dim3(G), dim3(kMThreads), lds, s, P);
+  } else if (ctxt == 1) {
+    hipLaunchKernelGGL((matmul_kernel<1, 1>), dim3(G), dim3(kMThreads), lds, s, P);
+  } else if (ctxt == 2) {
+    hipLaunchKernelGGL((matmul_kernel<1, 2>), dim3(G), dim3(kMThreads), lds, s, P);
   } else {
     hipLaunchKernelGGL((matmul_kernel<1, 4>), dim3(G), dim3(kMThreads), lds, s, P);
   }
