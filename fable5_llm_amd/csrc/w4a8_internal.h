@@ -194,8 +194,8 @@ hipError_t launch_alu(int op, const int32_t *y, const int16_t *b, int64_t n,
 // vals[32], rows[32], count, overflow.  scratch: topk_scratch_bytes(n)
 // bytes, no initial contents.  flags: kTopkFlagWords words, zero or left
 // by earlier launches whose epochs were all below epoch (0 < epoch < 2^29).
-constexpr int kTopkMaxChunks = 256;   // chunks of 1024 rows in 2^18 rows
 constexpr int kTopkSuper = 16;        // chunks per super-chunk
+constexpr int kTopkMaxChunks = 17 * kTopkSuper;   // 2^18 rows: 256 + 1 chunks
 constexpr int kTopkFlagWords = 2 * kTopkMaxChunks + kTopkMaxChunks / kTopkSuper;
 constexpr int32_t kTopkEpochMax = 1 << 29;
 size_t topk_scratch_bytes(int64_t n);

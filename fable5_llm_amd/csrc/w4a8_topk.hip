@@ -28,10 +28,12 @@ namespace w4a8 {
 
 namespace {
 
-constexpr int kTkRows = 1024;   // rows per chunk
+constexpr int kTkRows = 1024;   // rows per chunk, but the first
+constexpr int kTkFirst = 256;   // rows of chunk 0: its replay starts from an
+                                // empty list, so it is kept short
 constexpr int kTk = 32;
 constexpr int kTkPerLane = kTkRows / 64;
-constexpr int kTkSerialMax = 4;   // candidates a group replays one by one
+constexpr int kTkSerialMax = 12;   // candidates a group replays one by one
 
 __device__ __forceinline__ uint64_t tk_key(int32_t v, uint32_t row) {
   return ((uint64_t)((uint32_t)v ^ 0x80000000u) << 32) | (uint64_t)(0xFFFFFFFFu - row);
@@ -253,8 +255,9 @@ __global__ __launch_bounds__(64) void topk_kernel(const int32_t *y, int64_t n, i
   const int lane = threadIdx.x;
   const int c = blockIdx.x;
   const bool up = tk_ror4_up();
-  const int64_t s0 = (int64_t)c * kTkRows;
-  const int64_t end = n < s0 + kTkRows ? n : s0 + kTkRows;
+  const int64_t s0 = c == 0 ? 0 : kTkFirst + (int64_t)(c - 1) * kTkRows;
+  const int64_t e0 = c == 0 ? kTkFirst : s0 + kTkRows;
+  const int64_t end = n < e0 ? n : e0;
   int32_t yv[kTkPerLane];   // rows s0 + lane + 64 t, loads all in flight
 #pragma unroll
   for (int t = 0; t < kTkPerLane; ++t) {
@@ -362,13 +365,18 @@ __global__ __launch_bounds__(64) void topk_kernel(const int32_t *y, int64_t n, i
 
 }  // namespace
 
+int topk_chunks(int64_t n) {
+  return n <= kTkFirst ? 1 : 1 + (int)((n - kTkFirst + kTkRows - 1) / kTkRows);
+}
+
 size_t topk_scratch_bytes(int64_t n) {
-  return (size_t)((n + kTkRows - 1) / kTkRows + kTopkMaxChunks / kTopkSuper) * kTk * 8;
+  return (size_t)(topk_chunks(n) + kTopkMaxChunks / kTopkSuper) * kTk * 8;
 }
 
 hipError_t launch_topk32(const int32_t *y, int64_t n, void *scratch, int32_t *flags,
                          int32_t epoch, int32_t *out, int32_t *err, hipStream_t s) {
-  const int nchunks = (int)((n + kTkRows - 1) / kTkRows);
+  const int nchunks = topk_chunks(n);
+  if (nchunks > kTopkMaxChunks) return hipErrorInvalidValue;
   uint64_t *part = (uint64_t *)scratch;
   hipLaunchKernelGGL(topk_kernel, dim3(nchunks), dim3(64), 0, s, y, n, nchunks, epoch, part,
                      part + (size_t)nchunks * kTk, flags, out, err);
