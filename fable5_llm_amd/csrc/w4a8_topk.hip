@@ -9,7 +9,7 @@
 // (value desc, row asc), so the list is the 32 largest keys of the whole
 // head -- the same for any split of the rows, so it is found chunk by chunk
 // in parallel.  The overflow bit depends on the arrival order, so each chunk
-// of 1024 rows replays its own arrivals against the list of everything
+// (1024 rows; the first 256) replays its own arrivals against the list of everything
 // before it (built from the earlier chunks' lists); only arrivals at or
 // above the running entry[31] can insert or tie, and since entry[31] only
 // rises, an arrival below it when its 64-row group starts stays below.
