@@ -15,7 +15,7 @@ from oracle.fixtures import script_tags
 from oracle.seq_model import SeqOracle, load_images
 from tests.helpers import rand_w4_m, write_fixture_artifacts
 from tests.seq_streams import (I16_ADDR, PAIRS_ADDR, X_ADDR, movx, movy, mvgo,
-                               v_record_stream, xrf_write)
+                               script_stream, v_record_stream, xrf_write)
 
 pytestmark = pytest.mark.gpu
 
@@ -149,3 +149,31 @@ def test_hazards_refused_on_device(engine, tmp_path):
         m.step(movx(0, 0, 0, 1024))
         with pytest.raises(AssertionError, match="int8"):
             engine.sync()
+
+
+@pytest.mark.parametrize("tag", ["layer2", "token1", "token4"])
+def test_whole_script_stream_on_device(engine, scripts, tmp_path, tag):
+    # all of a script's V records in one stream: four channels, both x banks,
+    # no-wait MVGOs drained by FENCEs, MOVYs through XRF[0]; the device's
+    # scratch against the generator's y32 and the oracle machine's scratch
+    write_fixture_artifacts(tmp_path, scripts, tag)
+    prefix = str(tmp_path / tag)
+    ents, _ = load_weights_manifest(prefix)
+    with Artifacts(engine, prefix) as art:
+        m = S.SeqMachine(engine, art, scratch_words=1 << 18)
+        stage, recs, checks, words = script_stream(scripts, tag, ents, m.plan)
+        assert words <= 1 << 18
+        for a, v in stage:
+            m.write_scratch(a, v)
+        m.run(recs)
+        for kind, a, y, p0 in checks:
+            if kind == "pairs":
+                assert np.array_equal(m.read_pairs(a, y.size), y), (tag, a)
+            else:
+                got = m.read_scratch(a, y.size).astype(np.int64)
+                assert np.array_equal(got, law.movy(y, p0, law.MOVY_INT16)), (tag, a)
+        o = SeqOracle(load_images(prefix, ents), m.plan, scratch_words=1 << 18)
+        for a, v in stage:
+            o.mem[a:a + v.size] = v
+        o.run(S.pack_stream(recs))
+        assert np.array_equal(m.read_scratch(0, words).astype(np.int64), o.mem[:words])
