@@ -365,7 +365,7 @@ __global__ __launch_bounds__(64) void topk_kernel(const int32_t *y, int64_t n, i
 
 }  // namespace
 
-int topk_chunks(int64_t n) {
+static int topk_chunks(int64_t n) {
   return n <= kTkFirst ? 1 : 1 + (int)((n - kTkFirst + kTkRows - 1) / kTkRows);
 }
 
