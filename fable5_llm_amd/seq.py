@@ -398,6 +398,21 @@ class SeqMachine:
             raise SeqUnsupported(f"{OP_NAME.get(o, hex(o))} is outside the matvec replay")
         return True
 
+    def free(self):
+        """Release the machine's device memory (its row-range uploads,
+        scratch, x windows and RES); the Artifacts' images stay."""
+        for w in self._pieces.values():
+            w.free()
+        self._pieces = {}
+        self.scratch = self.xwin = self.res = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.eng.sync()
+        self.free()
+
     def run(self, recs):
         """Execute records until HALT or the end; returns the count run."""
         n = 0

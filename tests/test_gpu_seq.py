@@ -159,8 +159,8 @@ def test_whole_script_stream_on_device(engine, scripts, tmp_path, tag):
     write_fixture_artifacts(tmp_path, scripts, tag)
     prefix = str(tmp_path / tag)
     ents, _ = load_weights_manifest(prefix)
-    with Artifacts(engine, prefix) as art:
-        m = S.SeqMachine(engine, art, scratch_words=1 << 18)
+    with Artifacts(engine, prefix) as art, S.SeqMachine(engine, art,
+                                                        scratch_words=1 << 18) as m:
         stage, recs, checks, words = script_stream(scripts, tag, ents, m.plan)
         assert words <= 1 << 18
         for a, v in stage:
