@@ -85,12 +85,15 @@ def time_passes(ctx, one_pass, stream, steps, warmup):
         with torch.cuda.graph(g, stream=side):
             ctx.set_stream(side)
             one_pass()
-    finally:
+    except Exception as e:   # keep the eager figure rather than lose the leg
         ctx.set_stream(stream)
+        torch.cuda.synchronize(stream.device)
+        return eager, eager, f"eager (graph capture failed: {type(e).__name__})"
+    ctx.set_stream(stream)
     for _ in range(3):
         g.replay()
     torch.cuda.synchronize(stream.device)
-    return timed(g.replay), eager
+    return timed(g.replay), eager, "HIP graph of one pass"
 
 
 def batched_leg(st, ctx, batches, steps, warmup, seed):
@@ -136,11 +139,11 @@ def batched_leg(st, ctx, batches, steps, warmup, seed):
                                        [x8[m.K] for m in ms],
                                        [y[(mi, m.nrows)] for mi, m in zip(mis, ms)])
 
-        ms, ms_eager = time_passes(ctx, one_pass, stream, steps, warmup)
+        ms, ms_eager, how = time_passes(ctx, one_pass, stream, steps, warmup)
         gbs = nbytes / (ms * 1e-3) / 1e9
         tops = ops / (ms * 1e-3) / 1e12
         out.append({"B": B, "matrices": len(ffn), "ms_per_pass": round(ms, 4),
-                    "ms_per_pass_eager": round(ms_eager, 4), "timing": "HIP graph of one pass",
+                    "ms_per_pass_eager": round(ms_eager, 4), "timing": how,
                     "value": round(gbs, 1), "unit": "GB/s",
                     "pct_of_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 1),
                     "tops": round(tops, 2),
@@ -189,12 +192,12 @@ def ffn_leg(st, ctx, steps, warmup):
             ctx.mlp_async(wg, wu, wd, p0s, x, norm_w=nw, in_f=s.in_f,
                           one_plus=s.one_plus, mlp_out=y, res_out=res)
 
-    ms, ms_eager = time_passes(ctx, one_pass, stream, steps, warmup)
+    ms, ms_eager, how = time_passes(ctx, one_pass, stream, steps, warmup)
     nbytes = sum(l[-1] for l in layers)
     si, wg, wu, wd, p0s, x, nw, s, y, res, _ = layers[0]
     keep = (si, p0s, x.cpu().numpy(), nw.cpu().numpy(), y.cpu().numpy(), res.cpu().numpy())
     return {"layers": len(layers), "ms_per_pass": round(ms, 4),
-            "ms_per_pass_eager": round(ms_eager, 4), "timing": "HIP graph of one pass",
+            "ms_per_pass_eager": round(ms_eager, 4), "timing": how,
             "us_per_layer": round(ms * 1e3 / len(layers), 2),
             "value": round(nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s",
             "pct_of_peak_hbm": round(100.0 * nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 1),
