@@ -142,6 +142,37 @@ def pack_stream(recs):
     return b"".join(r.to_bytes() for r in recs)
 
 
+def load_seq(prefix):
+    """The records of `<prefix>.seq` (raw records, no header) and its
+    `<prefix>.seq.json` metadata when present, the stream's sha256 checked
+    against the metadata's (ref/seq_format.py:2399-2420,
+    ref/seq_model.py:1384-1389)."""
+    import hashlib
+    import json
+    with open(prefix + ".seq", "rb") as f:
+        buf = f.read()
+    meta = {}
+    if os.path.exists(prefix + ".seq.json"):
+        with open(prefix + ".seq.json") as f:
+            meta = json.load(f)
+        want = meta.get("stream_sha256")
+        if want and hashlib.sha256(buf).hexdigest() != want:
+            raise ValueError(f"{prefix}.seq does not match the sha256 in its .seq.json")
+    return unpack_stream(buf), meta
+
+
+def plan_from_meta(meta):
+    """{wid: WBASE} from a .seq.json's `weights` plan (wid -> {base, ...});
+    a per-channel repack (a list of bases) is not served."""
+    out = {}
+    for k, v in (meta.get("weights") or {}).items():
+        base = v["base"] if isinstance(v, dict) else v
+        if isinstance(base, (list, tuple)):
+            raise ValueError(f"wid {k}: per-channel weight bases are not served")
+        out[int(k)] = int(base)
+    return out
+
+
 def resolve_imm(r, xrf):
     """imm32 after indirection: as is, + XRF[i] or - XRF[i]
     (ref/seq_format.py:771-782)."""

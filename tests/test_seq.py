@@ -137,3 +137,23 @@ def test_oracle_whole_script_stream(scripts, tmp_path, tag):
         want = y if kind == "pairs" else law.movy(y, p0, law.MOVY_INT16)
         assert np.array_equal(got, want), (kind, a)
     assert len(checks) > 80
+
+
+def test_load_seq_and_plan_from_meta(tmp_path):
+    import hashlib
+    recs = [movx(1, 0, 64, 1024), mvgo(1, S.W_BASE + 4096, 8, 16, 5, 576),
+            S.Rec(S.OP_FENCE), S.Rec(S.OP_HALT)]
+    buf = S.pack_stream(recs)
+    (tmp_path / "a.seq").write_bytes(buf)
+    meta = {"stream_sha256": hashlib.sha256(buf).hexdigest(),
+            "weights": {"0": {"base": S.W_BASE, "nrows": 3}, "1": {"base": S.W_BASE + 4096}}}
+    (tmp_path / "a.seq.json").write_text(json.dumps(meta))
+    got, m = S.load_seq(str(tmp_path / "a"))
+    assert got == recs and S.plan_from_meta(m) == {0: S.W_BASE, 1: S.W_BASE + 4096}
+    (tmp_path / "a.seq").write_bytes(buf[:-16] + bytes(16))
+    with pytest.raises(ValueError, match="sha256"):
+        S.load_seq(str(tmp_path / "a"))
+    with pytest.raises(ValueError, match="per-channel"):
+        S.plan_from_meta({"weights": {"0": {"base": [1, 2]}}})
+    (tmp_path / "b.seq").write_bytes(buf)
+    assert S.load_seq(str(tmp_path / "b")) == (recs, {})
