@@ -66,3 +66,14 @@ def test_artifacts_reject_bad_image(engine, tmp_path):
     (tmp_path / "b.weights.json").write_text(json.dumps(man))
     with pytest.raises(AssertionError, match="holds"):
         A.Artifacts(engine, str(tmp_path / "b"))
+
+
+def test_replay_cli(scripts, tmp_path, capsys):
+    # python -m fable5_llm_amd.artifacts <prefix>: one JSON line per script,
+    # exit status 0 when every record matches
+    tag = script_tags()[0]
+    nv = _write_from_fixtures(tmp_path, scripts, tag)
+    assert A.main([str(tmp_path / tag)]) == 0
+    out = [l for l in capsys.readouterr().out.splitlines() if l.startswith("{")]
+    s = json.loads(out[-1])
+    assert s["V"] == nv and s["bad"] == []
