@@ -15,7 +15,7 @@ from oracle.fixtures import script_tags
 from oracle.seq_model import SeqOracle, load_images
 from tests.helpers import rand_w4_m, write_fixture_artifacts
 from tests.seq_streams import (I16_ADDR, PAIRS_ADDR, X_ADDR, movx, movy, mvgo,
-                               script_stream, v_record_stream, xrf_write)
+                               script_stream, swin_stage, v_record_stream, xrf_write)
 
 pytestmark = pytest.mark.gpu
 
@@ -215,3 +215,17 @@ def test_pre_g3_shape_on_device(engine, scripts, tmp_path):
             m.write_scratch(X_ADDR, x8)
             m.run(recs)
             assert np.array_equal(m.read_pairs(PAIRS_ADDR, y.size), y), v
+
+
+def test_swin_staging_on_device(engine, scripts, tmp_path):
+    from tests.test_seq import _swin_stream
+    tag = "token1"
+    write_fixture_artifacts(tmp_path, scripts, tag)
+    prefix = str(tmp_path / tag)
+    ents, _ = load_weights_manifest(prefix)
+    with Artifacts(engine, prefix) as art, S.SeqMachine(engine, art) as m:
+        recs, y = _swin_stream(scripts, tag, ents, m.plan)
+        m.run(recs)
+        got = m.read_pairs(PAIRS_ADDR, y.size)
+        assert np.array_equal(got[1:], y[1:]) and m.read_scratch(PAIRS_ADDR, 1)[0] == -2
+        assert m.tcnt_seq == 7
