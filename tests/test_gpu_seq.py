@@ -229,3 +229,45 @@ def test_swin_staging_on_device(engine, scripts, tmp_path):
         got = m.read_pairs(PAIRS_ADDR, y.size)
         assert np.array_equal(got[1:], y[1:]) and m.read_scratch(PAIRS_ADDR, 1)[0] == -2
         assert m.tcnt_seq == 7
+
+
+def _emb_artifacts(tmp_path, ntok=40, width=1024):
+    """The synthetic images plus an int16 embedding table of int8-range
+    values (so a MOVX can take an EMB's words), width in the manifest."""
+    prefix, man, rng = _synthetic(tmp_path, nrows=256)
+    emb = rng.integers(-127, 128, (ntok, width)).astype("<i2")
+    (tmp_path / "q.emb.bin").write_bytes(emb.tobytes())
+    man2 = dict(man, emb_row_bytes=2 * width)
+    (tmp_path / "q.weights.json").write_text(json.dumps(man2))
+    return prefix, man, emb
+
+
+def test_emb_feeds_the_matvec_on_device(engine, tmp_path):
+    prefix, man, emb = _emb_artifacts(tmp_path)
+    ents, _ = load_weights_manifest(prefix)
+    plan = S.plan_weights(ents)
+    e0 = man["0"]
+    recs = []
+    for tok, addr in ((17, 0), (39, 2048), (0, 4096)):
+        recs += [xrf_write(S.XRF_TOK, tok), S.Rec(S.OP_EMB, addr_lo=addr, len_or_addr_hi=1024)]
+    recs += [movx(0, 0, 2048, 1024), mvgo(0, plan[0], 8, 256, e0["sh"], e0["stride"]),
+             movy(0, 0, 256, 8192), S.Rec(S.OP_EMB, addr_lo=12000, len_or_addr_hi=100),
+             S.Rec(S.OP_HALT)]
+    o = SeqOracle(load_images(prefix, ents), plan, emb=emb)
+    with Artifacts(engine, prefix) as art, S.SeqMachine(engine, art) as m:
+        m.run(recs)
+        o.run(S.pack_stream(recs))
+        got = m.read_scratch(0, o.mem.size).astype(np.int64)
+        assert np.array_equal(got, o.mem)
+        assert np.array_equal(got[2048:3072], emb[39]) and np.array_equal(got[12000:12100], emb[0, :100])
+        assert np.count_nonzero(o.pairs(8192, 256)) > 200
+        m.set_xrf(S.XRF_TOK, 40)
+        with pytest.raises(ValueError, match="token 40"):
+            m.step(S.Rec(S.OP_EMB, addr_lo=0, len_or_addr_hi=8))
+        m.set_xrf(S.XRF_TOK, 1)
+        with pytest.raises(ValueError, match="1025 words"):
+            m.step(S.Rec(S.OP_EMB, addr_lo=0, len_or_addr_hi=1025))
+        with pytest.raises(ValueError, match="no flags"):
+            m.step(S.Rec(S.OP_EMB, flags=1, addr_lo=0, len_or_addr_hi=8))
+        with pytest.raises(ValueError, match="outside"):
+            m.step(S.Rec(S.OP_EMB, addr_lo=m.scratch.numel() - 4, len_or_addr_hi=8))

@@ -214,3 +214,26 @@ def test_oracle_swin_staging(scripts, tmp_path):
     m.run(S.pack_stream(recs))
     got = m.pairs(PAIRS_ADDR, y.size)
     assert np.array_equal(got[1:], y[1:]) and m.mem[PAIRS_ADDR] == -2 and m.tcnt == 7
+
+
+def test_oracle_emb_against_file_bytes(tmp_path):
+    # EMB = the first len words of the row of token XRF[3]
+    # (ref/seq_model.py:1088-1093), checked against the bytes at offset
+    # tok * row_bytes of the file, read without the oracle's reshape
+    rng = np.random.default_rng(31)
+    width, ntok = 64, 9
+    raw = rng.integers(-32768, 32768, ntok * width).astype("<i2").tobytes()
+    (tmp_path / "e.emb.bin").write_bytes(raw)
+    emb = np.fromfile(tmp_path / "e.emb.bin", dtype="<i2").reshape(ntok, width)
+    o = SeqOracle({}, {}, scratch_words=512, emb=emb)
+    recs = [xrf_write(S.XRF_TOK, 5), S.Rec(S.OP_EMB, addr_lo=100, len_or_addr_hi=40),
+            xrf_write(S.XRF_TOK, 8), S.Rec(S.OP_EMB, addr_lo=300, len_or_addr_hi=64)]
+    o.run(S.pack_stream(recs))
+    row = lambda t, n: struct.unpack_from(f"<{n}h", raw, t * 2 * width)
+    assert list(o.mem[100:140]) == list(row(5, 40)) and list(o.mem[300:364]) == list(row(8, 64))
+    assert not o.mem[:100].any() and not o.mem[140:300].any() and o.xrf[S.XRF_TOK] == 8
+    for bad in ([xrf_write(S.XRF_TOK, 9), S.Rec(S.OP_EMB, len_or_addr_hi=4)],
+                [S.Rec(S.OP_EMB, len_or_addr_hi=65)],
+                [S.Rec(S.OP_EMB, flags=2, len_or_addr_hi=4)]):
+        with pytest.raises(AssertionError):
+            SeqOracle({}, {}, scratch_words=512, emb=emb).run(S.pack_stream(bad))
