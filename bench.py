@@ -58,6 +58,70 @@ def pmc_traffic(kernel):
 METRIC = "achieved HBM GB/s (% of peak) on W4A8 GEMV; ms per 9B-shape weight stream"
 
 
+STEADY_BATCH, STEADY_TOL, STEADY_MAX = 10, 0.01, 400
+
+
+def warm_until_steady(run, sync, stream, min_steps):
+    """Untimed steps until the step time has settled: at least `min_steps`,
+    then batches of STEADY_BATCH steps (event-timed) until two consecutive
+    batch means differ by less than STEADY_TOL, at most STEADY_MAX steps in
+    all.  The GPU's clocks take tens of steps of continuous work to reach
+    their steady state after idling.  Returns (steps run, last batch ms)."""
+    import torch
+    for _ in range(min_steps):
+        run()
+    n, prev, last = min_steps, None, None
+    while n < STEADY_MAX:
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(STEADY_BATCH):
+            run()
+        e1.record(stream)
+        sync()
+        e1.synchronize()
+        n += STEADY_BATCH
+        last = e0.elapsed_time(e1) / STEADY_BATCH
+        if prev is not None and abs(last - prev) < STEADY_TOL * prev:
+            break
+        prev = last
+    return n, last
+
+
+def time_steps(st, ctx, stream, steps, warmup):
+    """Warm up until steady, time `steps` replays (wall clock and events),
+    then -- at the same clock state, with no idle gap -- `steps` more
+    persistent launches each bracketed by dispatch-recorded events (the
+    roofline's kernel time; graph mode: one profiled pass)."""
+    import numpy as np
+    import torch
+    n_warm, _ = warm_until_steady(st.run, ctx.sync, stream, warmup)
+    ctx.sync()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        st.run()
+    e1.record(stream)
+    ctx.sync()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    out = {"ms_per_step": wall * 1e3 / steps,
+           "ms_per_step_hip_events": e0.elapsed_time(e1) / steps,
+           "warmup_steps_run": n_warm}
+    try:
+        launches = st.plan.time_launches(steps)
+        out["launch_ms"] = launches
+        out["kernel_ms"] = float(np.median(launches))
+        out["nlaunch"] = 1
+    except ValueError:   # graph mode: one launch per site
+        prof = st.profile()
+        out["kernel_ms"] = float(prof.sum())
+        out["nlaunch"] = int(prof.size)
+    return out
+
+
 def time_passes(ctx, one_pass, stream, steps, warmup):
     """ms per pass of `one_pass` submitted from Python (eager) and replayed
     as one HIP graph captured from it (the launches alone, without the host
@@ -301,6 +365,52 @@ def batched_check(st, keep):
     return "bit-exact" if bad == 0 else f"MISMATCH in {bad} token rows"
 
 
+def chained_leg(ctx, stream, args):
+    """The decode step with its dependences: every site reads an earlier
+    site's output (stream9b.chain_sources; the swiglu sites form
+    EMUL32(gate, up) in their prologue), so every site after the first
+    waits for the one before it.  Timed as one persistent launch (fences
+    derived from the buffers: 128) and as a HIP graph of one launch per
+    site.  Same shapes and bytes as the headline stream; its own weights
+    (scales 2^U(-13, -7), so that the chain does not saturate)."""
+    from fable5_llm_amd import _native as N
+    from fable5_llm_amd import stream9b
+    st = stream9b.Stream9B(ctx, seed=args.seed + 1, chain=True, mode=N.PLAN_PERSISTENT,
+                           fences=N.FENCE_AUTO)
+    ctx.sync()
+    fenced = st.plan.fenced()
+    out = {"fences": sum(1 for f in fenced if f != N.WAIT_NONE),
+           "grid_wide_waits": fenced.count(N.WAIT_GRID),
+           "stamped_input_waits": fenced.count(N.WAIT_INPUT),
+           "bytes_per_step": st.bytes}
+    for name, mode in (("persistent", N.PLAN_PERSISTENT), ("graph", N.PLAN_GRAPH)):
+        st.plan.set_mode(mode)
+        tm = time_steps(st, ctx, stream, args.steps, args.warmup)
+        gbs = st.bytes / (tm["ms_per_step"] * 1e-3) / 1e9
+        leg = {"ms_per_step": round(tm["ms_per_step"], 4), "value": round(gbs, 1),
+               "unit": "GB/s", "pct_of_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 1),
+               "warmup_steps_run": tm["warmup_steps_run"]}
+        if name == "persistent":
+            ach = st.bytes / (tm["kernel_ms"] * 1e-3) / 1e9
+            leg["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS,
+                               "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBS, 4),
+                               "kernel": "stream_kernel",
+                               "avg_launch_us": round(tm["kernel_ms"] * 1e3, 3)}
+        out[name] = leg
+    st.plan.set_mode(N.PLAN_PERSISTENT)
+    return st, out
+
+
+def chain_check(st):
+    """The chained stream's last run against the oracle run site after site
+    (each site fed from the oracle's own output of its producer)."""
+    from tests import stream_check as sc
+    host = sc.host_inputs(st)
+    ref, _ = sc.run_cpu_stream(st, host)
+    bad = sc.compare(st, host, ref)
+    return "bit-exact" if not bad else f"MISMATCH {len(bad)}: {bad[:5]}"
+
+
 def cpu_baseline(st, min_seconds, keep=(), keep_ffn=None, keep_head=None):
     """Oracle leg: the C restatement over the full stream, repeated until
     `min_seconds` of matvec work; returns its rate and the parity check (of
@@ -309,12 +419,13 @@ def cpu_baseline(st, min_seconds, keep=(), keep_ffn=None, keep_head=None):
     from oracle import cfast
     from tests import stream_check as sc
     host = sc.host_inputs(st)
-    passes, total, ys = 0, 0.0, None
-    while passes < 1 or total < min_seconds:
-        ys, t = sc.run_cpu_stream(st, host)
-        total += t
+    ref, total = sc.run_cpu_stream(st, host)
+    passes = 1
+    while total < min_seconds:
+        total += sc.time_cpu_matvecs(st, host, ref)
         passes += 1
-    bad = sc.compare(st, host, ys)
+    bad = sc.compare(st, host, ref)
+    ys = [r["ys"] for r in ref]
     # single-threaded numpy restatement on one 4096 x 4096 matrix (sample)
     from oracle import law
     s0 = st.sites[1]
@@ -343,6 +454,11 @@ def cpu_baseline(st, min_seconds, keep=(), keep_ffn=None, keep_head=None):
     }
 
 
+def log(msg):
+    """Progress to stderr (the JSON line alone goes to stdout)."""
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -365,6 +481,9 @@ def main():
                          "or only where it shares a buffer with one")
     ap.add_argument("--no-ordered", action="store_true",
                     help="skip timing the same plan strictly in order (graph mode)")
+    ap.add_argument("--no-chain", action="store_true",
+                    help="skip the chained decode step (every site reads an earlier "
+                         "site's output)")
     ap.add_argument("--no-ffn", action="store_true",
                     help="skip the FFN-block leg (w4a8_mlp_async per layer) and the "
                          "LM-head leg (argmax and TOPK-32 alone)")
@@ -404,55 +523,39 @@ def main():
             "graph": N.PLAN_GRAPH}[args.mode]
     persistent = mode != N.PLAN_GRAPH
     fences = N.FENCE_AUTO if args.fences == "auto" else N.FENCE_ALL
+    log("building the stream")
     st = stream9b.Stream9B(ctx, seed=args.seed, mode=mode, fences=fences)
     ctx.sync()
     t_build = time.perf_counter() - t_build
     tot = stream9b.totals(st.sites)
 
-    for _ in range(args.warmup):
-        st.run()
-    ctx.sync()
-    torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record(stream)
-    for _ in range(args.steps):
-        st.run()
-    e1.record(stream)
-    ctx.sync()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_step = wall * 1e3 / args.steps
-    ms_step_ev = e0.elapsed_time(e1) / args.steps
-
     import numpy as np
-    # per-launch kernel time, ms (dispatch-recorded events; median of 5)
-    prof = np.median(np.stack([st.profile() for _ in range(5)]), axis=0)
-    kern_ms = float(prof.sum())
-    nlaunch = 1 if persistent else int(prof.size)
+    log("timing the headline step")
+    tm = time_steps(st, ctx, stream, args.steps, args.warmup)
+    ms_step, ms_step_ev = tm["ms_per_step"], tm["ms_per_step_hip_events"]
+    kern_ms, nlaunch = tm["kernel_ms"], tm["nlaunch"]
     achieved = st.bytes / (kern_ms * 1e-3) / 1e9
     kernel = "stream_kernel" if persistent else "gemv_kernel"
 
     ordered = None
     if not args.no_ordered and persistent:
+        log("timing the ordered (graph mode) step")
         # the same plan with every site after the previous one: graph mode
         st.plan.set_mode(N.PLAN_GRAPH)
-        for _ in range(max(3, args.warmup // 2)):
-            st.run()
-        ctx.sync()
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            st.run()
-        ctx.sync()
-        ms_o = (time.perf_counter() - t0) * 1e3 / args.steps
-        gbs_o = st.bytes / (ms_o * 1e-3) / 1e9
+        to = time_steps(st, ctx, stream, args.steps, 3)
+        gbs_o = st.bytes / (to["ms_per_step"] * 1e-3) / 1e9
         ordered = {
-            "mode": "graph", "ms_per_step": round(ms_o, 4), "value": round(gbs_o, 1),
-            "unit": "GB/s", "pct_of_peak_hbm": round(100.0 * gbs_o / PEAK_HBM_GBS, 1),
-            "note": "every site starts after the previous one completes (a decode "
-                    "step's chain of dependent sites); one gemv_kernel launch per site"}
+            "mode": "graph", "ms_per_step": round(to["ms_per_step"], 4),
+            "value": round(gbs_o, 1), "unit": "GB/s",
+            "pct_of_peak_hbm": round(100.0 * gbs_o / PEAK_HBM_GBS, 1),
+            "note": "the same independent-input plan with every site starting after "
+                    "the previous one completes; one gemv_kernel launch per site"}
         st.plan.set_mode(mode)
+
+    chained = stc = None
+    if not args.no_chain:
+        log("chained step")
+        stc, chained = chained_leg(ctx, stream, args)
 
     line = {
         "metric": METRIC,
@@ -463,6 +566,11 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
         "ms_per_step_hip_events": round(ms_step_ev, 4),
+        "warmup_steps_run": tm["warmup_steps_run"],
+        "warmup_rule": (f"at least --warmup steps, then batches of {STEADY_BATCH} until two "
+                        f"consecutive batch means differ by < {STEADY_TOL:.0%} (at most "
+                        f"{STEADY_MAX} steps); the roofline's launches follow the timed "
+                        "steps with no idle gap"),
         "pct_of_peak_hbm": round(100.0 * st.bytes / (ms_step * 1e-3) / 1e9 / PEAK_HBM_GBS, 1),
         "higher_is_better": True,
         "scaling": "weak",
@@ -501,6 +609,9 @@ def main():
             "launches_per_step": nlaunch,
             "avg_launch_us": round(kern_ms / nlaunch * 1e3, 3),
             "bytes_per_launch": round(st.bytes / nlaunch),
+            "timing": ("median of --steps back-to-back launches, dispatch-recorded HIP "
+                       "events, right after the timed steps" if persistent else
+                       "one profiled pass, dispatch-recorded HIP events per launch"),
         },
         "reference_fpga": {
             "stream_ms": 54.408, "gbs": 75.2,
@@ -509,21 +620,36 @@ def main():
     }
     if ordered:
         line["ordered"] = ordered
+    if chained:
+        # what each fence adds over the independent-input step, same mode
+        if persistent:
+            chained["persistent"]["us_per_fence_over_unfenced"] = round(
+                (chained["persistent"]["ms_per_step"] - ms_step) * 1e3 / max(1, chained["fences"]), 3)
+        line["chained"] = chained
     batches = [int(b) for b in args.batch.split(",") if b.strip()]
     keep = ()
     if batches:
+        log("batched leg")
         line["batched"], keep = batched_leg(st, ctx, batches, min(args.steps, 50),
                                             max(3, args.warmup // 10), args.seed)
     keep_head = None
     if not args.no_ffn:
+        log("head leg")
         line["head"], keep_head = head_leg(st, ctx, min(args.steps, 50),
                                            max(3, args.warmup // 10))
     keep_ffn = None
     if not args.no_ffn:
+        log("ffn leg")
         line["ffn"], keep_ffn = ffn_leg(st, ctx, min(args.steps, 50),
                                         max(3, args.warmup // 10))
     if not args.no_cpu:
+        log("cpu baseline and parity")
         line["cpu_baseline"] = cpu_baseline(st, args.cpu_seconds, keep, keep_ffn, keep_head)
+        if stc is not None:
+            log("chained parity")
+            chained["parity"] = chain_check(stc)
+    if stc is not None:
+        stc.close()
     st.close()
     ctx.close()
     print(json.dumps(line), flush=True)

@@ -13,12 +13,13 @@ OK = 0
 E_SHAPE, E_ENVELOPE, E_ACC_OVF, E_Y32_OVF, E_HIP, E_ARG, E_RANGE = \
     -1, -2, -3, -4, -5, -6, -7
 
-PRO_X8, PRO_DYNQ8, PRO_RMSNORM_DYNQ8 = 0, 1, 2
+PRO_X8, PRO_DYNQ8, PRO_RMSNORM_DYNQ8, PRO_EMUL_DYNQ8 = 0, 1, 2, 3
 EPI_Y32, EPI_MOVY_I16, EPI_MOVY_P32, EPI_SILU32, EPI_SHIFT_I64 = 0, 1, 2, 3, 4
 ALU_SHIFT32, ALU_SILU32, ALU_EMUL32, ALU_SHIFT32W = 1, 6, 8, 9
 MOVY_PAIRS32, MOVY_INT16 = 0, 1
 PLAN_GRAPH, PLAN_PERSISTENT, PLAN_PERSISTENT_COOP = 0, 1, 2
 FENCE_ALL, FENCE_AUTO = 0, 1
+WAIT_NONE, WAIT_GRID, WAIT_INPUT = 0, 1, 2   # w4a8_plan_fences
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
@@ -65,11 +66,14 @@ SIGNATURES = {
     "w4a8_plan_create": [_P, ctypes.POINTER(_P)],
     "w4a8_plan_add_site": [_P, _I32, _PP, _P, _P, _PP, _I32, _P, _P, _I32, _I32,
                            _I32, _P, _P, _P],
+    "w4a8_plan_add_site_emul": [_P, _I32, _PP, _P, _P, _PP, _P, _P, _P, _P],
     "w4a8_plan_add_head": [_P, _P, _I32, _P, _P, _I32, _I32, _I32, _P],
     "w4a8_plan_set_mode": [_P, _I32],
     "w4a8_plan_set_fences": [_P, _I32],
+    "w4a8_plan_fences": [_P, _I32, _P],
     "w4a8_plan_run": [_P],
     "w4a8_plan_profile": [_P, _I32, _P],
+    "w4a8_plan_time_launches": [_P, _I32, _P],
     "w4a8_plan_destroy": [_P],
 }
 STRING_FUNCS = ("w4a8_version", "w4a8_last_error")

@@ -806,12 +806,16 @@ static int topk_launch(w4a8_ctx *c, const int32_t *d_y, int64_t n, void *scratch
                        int32_t *d_out) {
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   HIP_TRY(hipStreamIsCapturing(c->stream, &cs));
-  if (cs != hipStreamCaptureStatusNone || c->topk_epoch + 1 >= kTopkEpochMax) {
+  if (cs != hipStreamCaptureStatusNone || c->topk_epoch == 0 ||
+      c->topk_epoch + 1 >= kTopkEpochMax) {
     HIP_TRY(launch_fill_i32(c->d_topk_flags, 0, kTopkFlagWords, c->stream));
     c->topk_epoch = 0;
   }
   const int32_t epoch = ++c->topk_epoch;
   HIP_TRY(launch_topk32(d_y, n, scratch, c->d_topk_flags, epoch, d_out, c->d_err, c->stream));
+  // a captured launch replays this epoch with its own clear; the next eager
+  // launch clears the flags first
+  if (cs != hipStreamCaptureStatusNone) c->topk_epoch = 0;
   return W4A8_OK;
 }
 
@@ -970,6 +974,9 @@ struct w4a8_plan {
   uint32_t *d_done = nullptr;
   uint32_t epoch = 0;               // launches since d_done was zeroed
   int8_t *d_stage = nullptr;
+  uint64_t *d_stamped = nullptr;    // stamped words of outputs read through them
+  int64_t stamped_words = 0;
+  bool dependent = false;           // some site waits for, or forms, others' results
   int G = 0;
   int head_site = -1;
   int32_t *head_result = nullptr;
@@ -979,9 +986,12 @@ static void plan_drop_persistent(w4a8_plan *p) {
   if (p->d_sites) (void)hipFree(p->d_sites);
   if (p->d_done) (void)hipFree(p->d_done);
   if (p->d_stage) (void)hipFree(p->d_stage);
+  if (p->d_stamped) (void)hipFree(p->d_stamped);
   p->d_sites = nullptr;
   p->d_done = nullptr;
   p->d_stage = nullptr;
+  p->d_stamped = nullptr;
+  p->stamped_words = 0;
   p->epoch = 0;
   p->G = 0;
 }
@@ -999,6 +1009,7 @@ static void step_ranges(const w4a8_plan::Step &st, std::vector<ByteRange> &rd,
   };
   add(rd, P.x, P.pro == PRO_X8 ? (int64_t)P.K : 2 * (int64_t)P.K);
   if (P.pro == PRO_RMSNORM_DYNQ8) add(rd, P.norm_w, 2 * (int64_t)P.K);
+  if (P.pro == PRO_EMUL_DYNQ8) add(rd, P.x2, 4 * (int64_t)P.K);
   for (int j = 0; j < P.njobs; ++j) {
     const GemvJob &J = P.job[j];
     int64_t es = 0;
@@ -1024,22 +1035,76 @@ static bool ranges_meet(const std::vector<ByteRange> &a, const std::vector<ByteR
   return false;
 }
 
-// W4A8_FENCE_AUTO: a site waits for the whole GPU only when it reads what a
-// site since the last fence writes, or writes what one of those reads or
-// writes -- the reference sequencer's FENCE rule (a result is waited for
-// before it is consumed, seq_format.py:2077-2231), applied across sites.
-static void plan_fences(const w4a8_plan *p, std::vector<GemvParams> &sites) {
+// The job of site j (since `from`) whose int16 output holds site i's whole x,
+// when it is the only write site i's x meets among sites from..i-1 and x
+// starts at an even row: (j, job, first word), else j = -1.
+struct StampSrc {
+  int site = -1, job = -1;
+  int64_t word = 0;
+};
+static StampSrc stamp_source(const std::vector<GemvParams> &sites,
+                             const std::vector<std::vector<ByteRange>> &wr, int from, int i) {
+  StampSrc none, got;
+  const GemvParams &C = sites[i];
+  if ((C.pro != PRO_DYNQ8 && C.pro != PRO_RMSNORM_DYNQ8) || C.K % 2) return none;
+  const ByteRange x{(uintptr_t)C.x, (uintptr_t)C.x + 2 * (uintptr_t)C.K};
+  int writers = 0;
+  for (int j = from; j < i; ++j)
+    for (const auto &w : wr[j])
+      if (w.lo < x.hi && x.lo < w.hi) ++writers;
+  if (writers != 1) return none;
+  for (int j = from; j < i; ++j)
+    for (int k = 0; k < sites[j].njobs; ++k) {
+      const GemvJob &J = sites[j].job[k];
+      if ((J.epi != EPI_MOVY_I16 && J.epi != EPI_SILU32) || J.nrows % 2) continue;
+      const uintptr_t lo = (uintptr_t)J.out, hi = lo + 2 * (uintptr_t)J.nrows;
+      if (x.lo >= lo && x.hi <= hi && (x.lo - lo) % 4 == 0) {
+        got.site = j;
+        got.job = k;
+        got.word = (int64_t)((x.lo - lo) / 4);
+        return got;
+      }
+    }
+  return none;
+}
+
+// W4A8_FENCE_AUTO: a site waits only when it reads what a site since the
+// last fence writes, or writes what one of those reads or writes -- the
+// reference sequencer's FENCE rule (a result is waited for before it is
+// consumed, seq_format.py:2077-2231), applied across sites.  When its one
+// dependence is reading its int16 input x from one output of such a site,
+// it waits for that output's stamped words alone (src[i]); otherwise for
+// every workgroup to have finished every earlier site (fence).
+static void plan_fences(const w4a8_plan *p, std::vector<GemvParams> &sites,
+                        std::vector<StampSrc> &src) {
   const int n = (int)p->steps.size();
   std::vector<std::vector<ByteRange>> rd(n), wr(n);
   for (int i = 0; i < n; ++i) step_ranges(p->steps[i], rd[i], wr[i]);
-  int last = 0;   // first site since the last fence
+  src.assign(n, StampSrc{});
+  int last = 0;   // first site since the last grid-wide fence
   for (int i = 0; i < n; ++i) {
     bool f = i > 0 && p->fences == W4A8_FENCE_ALL;
-    for (int j = last; j < i && !f; ++j)
-      f = ranges_meet(rd[i], wr[j]) || ranges_meet(wr[i], rd[j]) || ranges_meet(wr[i], wr[j]);
+    bool meets = false, x_only = true;
+    const uintptr_t x0 = (uintptr_t)sites[i].x;
+    for (int j = last; j < i && !f; ++j) {
+      for (const auto &a : rd[i])
+        if (ranges_meet({a}, wr[j])) {
+          meets = true;
+          x_only = x_only && a.lo == x0;   // the first read range is x
+        }
+      if (ranges_meet(wr[i], rd[j]) || ranges_meet(wr[i], wr[j])) meets = true, x_only = false;
+    }
+    if (meets && !f) {
+      if (x_only) src[i] = stamp_source(sites, wr, last, i);
+      f = src[i].site < 0;
+    }
     sites[i].fence = f ? 1 : 0;
     if (f) last = i;
     sites[i].fence_at = last;
+    sites[i].stamp_src = src[i].site;
+    // behind a fence, or reading stamped words, every workgroup computes the
+    // site's prologue itself
+    sites[i].local_pro = last > 0 || src[i].site >= 0 ? 1 : 0;
   }
 }
 
@@ -1071,10 +1136,38 @@ static int plan_build_persistent(w4a8_plan *p) {
     sites[i].tile_rot = (int32_t)((V - off % V) % V);
     off += sites[i].total_tiles;
   }
-  plan_fences(p, sites);
+  std::vector<StampSrc> src;
+  plan_fences(p, sites, src);
+  // stamped words for every output a later site reads through them (one
+  // block per (site, job), nrows / 2 words), cleared with the flags
+  std::vector<int64_t> word0(n * kMaxJobs, -1);
+  int64_t words = 0;
+  for (int i = 0; i < n; ++i)
+    if (src[i].site >= 0) {
+      int64_t &w0 = word0[src[i].site * kMaxJobs + src[i].job];
+      if (w0 < 0) {
+        w0 = words;
+        words += sites[src[i].site].job[src[i].job].nrows / 2;
+      }
+    }
   HIP_TRY(hipMalloc(&p->d_sites, sizeof(GemvParams) * (size_t)n));
   HIP_TRY(hipMalloc(&p->d_done, sizeof(uint32_t) * stream_counter_words(p->G, n)));
   HIP_TRY(hipMalloc(&p->d_stage, (size_t)kStageBytes * (size_t)n));
+  p->stamped_words = words;
+  p->dependent = false;
+  for (int i = 0; i < n; ++i)
+    p->dependent = p->dependent || sites[i].local_pro || sites[i].stamp_src >= 0 ||
+                   sites[i].pro == PRO_EMUL_DYNQ8;
+  if (words > 0) HIP_TRY(hipMalloc(&p->d_stamped, sizeof(uint64_t) * (size_t)words));
+  for (int i = 0; i < n; ++i) {
+    for (int k = 0; k < sites[i].njobs; ++k) {
+      const int64_t w0 = word0[i * kMaxJobs + k];
+      sites[i].job[k].stamped = w0 >= 0 ? p->d_stamped + w0 : nullptr;
+    }
+    sites[i].x_stamped =
+        src[i].site >= 0 ? p->d_stamped + word0[src[i].site * kMaxJobs + src[i].job] + src[i].word
+                         : nullptr;
+  }
   p->epoch = 0;
   HIP_TRY(hipMemcpy(p->d_sites, sites.data(), sizeof(GemvParams) * (size_t)n,
                     hipMemcpyHostToDevice));
@@ -1094,6 +1187,8 @@ static int plan_launch_persistent(w4a8_plan *p, hipStream_t s, hipEvent_t e0,
   if (p->epoch == 0 || cs != hipStreamCaptureStatusNone ||
       (uint64_t)(p->epoch + 1) * (uint64_t)(n + 1) > 0xFFFFFFFFull) {
     HIP_TRY(launch_fill_i32((int32_t *)p->d_done, 0, (int64_t)stream_counter_words(p->G, n), s));
+    if (p->stamped_words > 0)
+      HIP_TRY(launch_fill_i32((int32_t *)p->d_stamped, 0, 2 * p->stamped_words, s));
     p->epoch = 0;
   }
   StreamParams sp{};
@@ -1106,7 +1201,11 @@ static int plan_launch_persistent(w4a8_plan *p, hipStream_t s, hipEvent_t e0,
   sp.err = p->ctx->d_err;
   sp.result = p->head_result;
   sp.trace = trace;
-  HIP_TRY(launch_stream(sp, p->G, s, p->mode == W4A8_PLAN_PERSISTENT_COOP, e0, e1));
+  HIP_TRY(launch_stream(sp, p->G, s, p->mode == W4A8_PLAN_PERSISTENT_COOP, p->dependent, e0,
+                        e1));
+  // A captured launch replays this epoch with its own fill; the memory holds
+  // whatever ran last, so the next eager launch clears it first.
+  if (cs != hipStreamCaptureStatusNone) p->epoch = 0;
   return W4A8_OK;
 }
 
@@ -1143,6 +1242,26 @@ int w4a8_plan_add_site(w4a8_plan *p, int32_t nmat, const w4a8_weights *const *w,
   int rc = site_params(p->ctx, st.P, nmat, w, epilogue, p0, d_out, prologue, d_x,
                        d_norm_w, in_f, one_plus, e_x, d_x8_out, d_e_x_out, d_xn_out);
   if (rc) return rc;
+  st.grid = grid_for(p->ctx, st.P.total_tiles);
+  st.head = false;
+  st.result = nullptr;
+  p->steps.push_back(st);
+  plan_drop_graph(p);
+  return W4A8_OK;
+}
+
+int w4a8_plan_add_site_emul(w4a8_plan *p, int32_t nmat, const w4a8_weights *const *w,
+                            const int32_t *epilogue, const int32_t *p0, void *const *d_out,
+                            const int16_t *d_x, const int32_t *d_x2, int8_t *d_x8_out,
+                            int32_t *d_e_x_out) {
+  if (!p || !w || !epilogue || !p0 || !d_out) return fail(W4A8_E_ARG, "null argument");
+  if (!d_x2 || !aligned16(d_x2)) return fail(W4A8_E_ARG, "x2 must be a 16-byte aligned pointer");
+  w4a8_plan::Step st{};
+  int rc = site_params(p->ctx, st.P, nmat, w, epilogue, p0, d_out, PRO_DYNQ8, d_x, nullptr, 0,
+                       0, 0, d_x8_out, d_e_x_out, nullptr);
+  if (rc) return rc;
+  st.P.pro = PRO_EMUL_DYNQ8;
+  st.P.x2 = d_x2;
   st.grid = grid_for(p->ctx, st.P.total_tiles);
   st.head = false;
   st.result = nullptr;
@@ -1199,6 +1318,18 @@ int w4a8_plan_set_fences(w4a8_plan *p, int32_t fences) {
     return fail(W4A8_E_ARG, "unknown fence mode");
   if (fences != p->fences) plan_drop_graph(p);
   p->fences = fences;
+  return W4A8_OK;
+}
+
+int w4a8_plan_fences(w4a8_plan *p, int32_t n, int32_t *fenced) {
+  if (!p || (n > 0 && !fenced)) return fail(W4A8_E_ARG, "null argument");
+  if (n != (int32_t)p->steps.size())
+    return fail(W4A8_E_ARG, "plan has " + std::to_string(p->steps.size()) + " steps");
+  std::vector<GemvParams> sites(n);
+  for (int i = 0; i < n; ++i) sites[i] = p->steps[i].P;
+  std::vector<StampSrc> src;
+  plan_fences(p, sites, src);
+  for (int i = 0; i < n; ++i) fenced[i] = sites[i].fence ? 1 : (src[i].site >= 0 ? 2 : 0);
   return W4A8_OK;
 }
 
@@ -1293,6 +1424,35 @@ int w4a8_plan_profile(w4a8_plan *p, int32_t n, float *ms) {
   for (auto &e : ev)
     if (e) (void)hipEventDestroy(e);
   return rc;
+}
+
+int w4a8_plan_time_launches(w4a8_plan *p, int32_t n, float *ms) {
+  if (!p || n < 1 || !ms) return fail(W4A8_E_ARG, "null argument or n < 1");
+  if (p->mode == W4A8_PLAN_GRAPH)
+    return fail(W4A8_E_ARG, "w4a8_plan_time_launches times persistent plans");
+  if (p->steps.empty()) return fail(W4A8_E_ARG, "empty plan");
+  w4a8_ctx *c = p->ctx;
+  DeviceGuard g(c->device);
+  if (!p->d_sites) {
+    int rc = plan_build_persistent(p);
+    if (rc) {
+      plan_drop_persistent(p);
+      return rc;
+    }
+  }
+  std::vector<hipEvent_t> ev(2 * (size_t)n, nullptr);
+  int rc = W4A8_OK;
+  for (auto &e : ev)
+    if (!rc && hipEventCreate(&e) != hipSuccess) rc = fail(W4A8_E_HIP, "hipEventCreate");
+  for (int i = 0; !rc && i < n; ++i)
+    rc = plan_launch_persistent(p, c->stream, ev[2 * i], ev[2 * i + 1]);
+  if (!rc && hipStreamSynchronize(c->stream) != hipSuccess) rc = fail(W4A8_E_HIP, "sync");
+  for (int i = 0; !rc && i < n; ++i)
+    if (hipEventElapsedTime(&ms[i], ev[2 * i], ev[2 * i + 1]) != hipSuccess)
+      rc = fail(W4A8_E_HIP, "hipEventElapsedTime");
+  for (auto &e : ev)
+    if (e) (void)hipEventDestroy(e);
+  return rc ? rc : take_err(c);
 }
 
 int w4a8_plan_destroy(w4a8_plan *p) {

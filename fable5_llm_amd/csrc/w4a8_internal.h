@@ -44,9 +44,9 @@ constexpr int kMaxJobs = 6;
 constexpr int kWG = 256;         // threads per workgroup (4 wavefronts)
 constexpr int kWaves = kWG / 64;
 
-// PRO_EMUL_DYNQ8 (gemv_kernel only, the FFN block's down projection):
-// x16 = clip16(rs(x2 * x, 12)) with x int16 (SILU32 of the gate) and x2
-// int32 (the up projection), i.e. ALU EMUL32 at p0 = 12, then DYNQ8.
+// PRO_EMUL_DYNQ8 (the FFN block's down projection): x16 = clip16(rs(x2 * x,
+// 12)) with x int16 (SILU32 of the gate) and x2 int32 (the up projection),
+// i.e. ALU EMUL32 at p0 = 12, then DYNQ8.
 enum Prologue { PRO_X8 = 0, PRO_DYNQ8 = 1, PRO_RMSNORM_DYNQ8 = 2, PRO_EMUL_DYNQ8 = 3 };
 // EPI_MOVY_I16_ADD (gemv_kernel only): EPI_MOVY_I16 into out (when set),
 // and clip16(res[row] + that) into res_out (ALU ADD, the block's residual).
@@ -103,6 +103,9 @@ struct GemvJob {
   int32_t pad_;
   const int16_t *res;   // EPI_MOVY_I16_ADD: residual input
   int16_t *res_out;     // EPI_MOVY_I16_ADD: residual output
+  uint64_t *stamped;    // persistent stream, int16 outputs read by a later site
+                        // through stamped words: word i = rows 2i, 2i+1 (low 32
+                        // bits) and the producing site's stamp (high 32 bits)
 };
 
 struct GemvParams {
@@ -119,6 +122,14 @@ struct GemvParams {
   int32_t fence;            // persistent stream: every earlier site completes on all
                             // workgroups before this one reads its activations
   int32_t fence_at;         // persistent stream: the last fenced site <= this one (0: none)
+  int32_t local_pro;        // persistent stream: every workgroup computes this site's
+                            // prologue itself, after the wait for site fence_at
+                            // (exports by workgroup site % G), instead of copying it
+                            // from the staging area
+  int32_t stamp_src;        // persistent stream: x is read through stamped words
+                            // written by site stamp_src (x_stamped), instead of after
+                            // a grid-wide wait; -1: not
+  const uint64_t *x_stamped;  // ... the words holding x[0..K) (K / 2 of them)
   int8_t *x8_out;           // optional (written by workgroup 0)
   int32_t *e_x_out;         // optional
   int16_t *xn_out;          // optional RMSNorm output
@@ -154,7 +165,9 @@ struct StreamParams {
                             // per site whose activations are staged (stores epoch), then
                             // the head's key and arrival count (stream_head_word0)
   uint32_t epoch;           // launches since `done` was zeroed, this one included:
-                            // every flag value it stores exceeds all earlier ones
+                            // every flag value it stores exceeds all earlier ones;
+                            // site s of this launch stamps its words
+                            // (epoch - 1) * (nsites + 1) + s + 1
   int8_t *stage;            // nsites * kStageBytes: each site's x8, corrections, e_x
   int32_t *err;             // bit 1: a completion wait gave up; bit 2: an LDS wait did
   int32_t *result;          // head: (index, value) of the maximum, written by the
@@ -163,10 +176,13 @@ struct StreamParams {
                             // workgroup 0 as it starts each site, and at its end
 };
 // one workgroup per CU; `cooperative`: through the cooperative launch API.
+// `dependent`: the kernel built for plans with dependent sites (any site
+// with local_pro, stamp_src >= 0 or PRO_EMUL_DYNQ8); the other one leaves
+// that code out, and is what plans of independent sites run.
 // start / stop (optional) bracket the kernel: recorded by the dispatch itself
 // for the plain launch, around it for the cooperative one
 hipError_t launch_stream(const StreamParams &sp, int grid, hipStream_t s, bool cooperative,
-                         hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
+                         bool dependent, hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 int stream_max_blocks_per_cu();
 // uint32 words of flags a grid of `grid` workgroups running nsites sites needs
 size_t stream_counter_words(int grid, int nsites);

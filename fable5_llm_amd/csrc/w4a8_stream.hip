@@ -83,6 +83,7 @@ struct __align__(16) Lds {
   int32_t ex[kNB];                  // ... and its e_x
   int32_t wsite[kCW];               // site each weight wavefront works on (nsites: done)
   int32_t gridok;                   // last fenced site whose grid-wide wait has passed
+  int32_t served;                   // last site whose outputs the control wavefront stored
   int32_t psync[kPW];               // prologue wavefronts' barrier phases
   int32_t abort;                    // set by the first LDS wait that gives up
   int32_t err;                      // error bits found inside the workgroup
@@ -92,6 +93,17 @@ struct __align__(16) Lds {
   int32_t pmx[kPW];                 // prologue partial maxima
   uint64_t best;                    // argmax key of the head's rows seen here (0: none)
 };
+
+// The workgroup's LDS block.
+__shared__ Lds g_lds;
+
+// a pointer argument of a non-inlined function, made wavefront-uniform
+__device__ __forceinline__ void *uniform_ptr(const void *p) {
+  const uint64_t a = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  return (void *)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
 
 // ---------------------------------------------------------------------------
 // LDS synchronisation
@@ -286,11 +298,15 @@ __device__ __forceinline__ void tile_epilogue(Lds &L, int kt, CJob &J, int tl, i
 }
 
 // ------------------------------------------------------------- control
-// Store the outputs of this CU's tiles of site P (tile numbers kt0, ...).
+// Store the outputs of this CU's tiles of site P (tile numbers kt0, ...), and
+// for a job read through stamped words also the words (lanes 0..7: rows
+// 2l, 2l+1 of the tile with `stamp`; each an 8-byte store, which lands
+// whole, so a reader that sees the stamp sees the rows).
 // Argmax tiles stage nothing: their slot is freed by the wavefront that
 // completes them, which is waited for here too, so that no wavefront still
 // reads this site's activations once this returns.
-__device__ void ctrl_serve(CSite &P, Lds &L, int kt0, int r, int G, int lane) {
+template <bool kDep>
+__device__ void ctrl_serve(CSite &P, Lds &L, int kt0, int r, int G, int lane, uint32_t stamp) {
   const int first = (r + P.tile_rot) % G;
   for (int i = 0, t = first; t < P.total_tiles; ++i, t += G) {
     CJob &J = P.job[job_of(P, t)];
@@ -301,6 +317,14 @@ __device__ void ctrl_serve(CSite &P, Lds &L, int kt0, int r, int G, int lane) {
       continue;
     }
     lds_wait_eq(L, &L.tready[slot], kt + 1, lane);
+    if (kDep && J.stamped && lane < kTileRows / 2) {
+      // rows 2l and 2l + 1 (int16 epilogues); nrows is even
+      const int row = (t - J.tile0) * kTileRows + 2 * lane;
+      const uint32_t lo = (uint32_t)(uint16_t)(int16_t)L.tv[slot][2 * lane];
+      const uint32_t hi = (uint32_t)(uint16_t)(int16_t)L.tv[slot][2 * lane + 1];
+      if (row < J.nrows)
+        store_coherent(J.stamped + row / 2, (uint64_t)(lo | (hi << 16)) | ((uint64_t)stamp << 32));
+    }
     if (lane < kTileRows) {
       const int64_t v = L.tv[slot][lane];
       const int row = (t - J.tile0) * kTileRows + lane;
@@ -339,6 +363,37 @@ __device__ void grid_wait(uint32_t *flags, int G, uint32_t v, int lane, int32_t 
 
 
 // ------------------------------------------------------------- prologue
+// The prologue wavefronts' barrier state: its phase, and whether every wait
+// so far ended.  A value type, passed in and out of the staged prologue's
+// (non-inlined) function, so it stays in registers.
+struct PSync {
+  int32_t phase;
+  int32_t ok;
+};
+
+// barrier of the 3 prologue wavefronts only (bounded), through L.psync
+__device__ __forceinline__ void psync(Lds &L, PSync &ps, int pw, int lane) {
+  ++ps.phase;
+  wait_lds();
+  if (lane == 0) lds_write_i32(&L.psync[pw], ps.phase);
+  bool done = false;
+  for (uint32_t n = 0; n < kLdsSpin && !done; ++n)
+    done = __all(lds_read_i32(&L.psync[lane % kPW]) >= ps.phase);
+  ps.ok = ps.ok && done;
+}
+
+// Bring site P's table entry into the scalar cache (one load per 64-byte
+// line), so that the waits and the epilogue at the site's fence do not each
+// miss on it.
+__device__ __forceinline__ void touch_site(CSite *P) {
+  typedef const __attribute__((address_space(4))) int32_t CInt;
+  CInt *q = (CInt *)P;
+  int32_t acc = 0;
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(GemvParams) / 4); i += 16) acc ^= q[i];
+  asm volatile("" ::"s"(acc));
+}
+
 // One 16-byte piece of a vector through a buffer whose range ends with the
 // vector: lanes past it read zero.  Agent-coherent, since an earlier site on
 // another CU may have written it.
@@ -351,20 +406,38 @@ __device__ __forceinline__ int4 vec_load(__amdgpu_buffer_rsrc_t rs, int off) {
 // in chunks g = pw, pw + 3, ... of 512 elements (lane l holds elements
 // 8l..8l+7 of a chunk, so the 4 lanes of a DPP quad hold 32 consecutive
 // elements -- one (group, k-quarter) of the weight layout), the RMSNorm
-// weights alike; for int8 x (PRO_X8), 1 KiB chunks of 16 bytes per lane.
+// weights and the int32 second factor of PRO_EMUL_DYNQ8 alike; for int8 x
+// (PRO_X8), 1 KiB chunks of 16 bytes per lane.
 struct ProX {
   int4 pc[kPC];
   int4 wv[kPN];
+  int4 x2[kPC];   // PRO_EMUL_DYNQ8: the second factor of half the chunks at a time
 };
+constexpr int kPC2 = kPC / 2;   // chunks per half of the second factor
+static_assert(kPC % 2 == 0, "the second factor is loaded in two halves");
+
+// The second factor of chunks h * kPC2 .. + kPC2 (PRO_EMUL_DYNQ8) into X.x2.
+__device__ __forceinline__ void pro_issue_x2(ProX &X, CSite &P, int half, int pw, int lane) {
+  const int x2len = P.pro == PRO_EMUL_DYNQ8 ? 4 * P.K : 0;
+  const __amdgpu_buffer_rsrc_t r2 =
+      __builtin_amdgcn_make_buffer_rsrc((void *)P.x2, (short)0, x2len, kBufDword3);
+#pragma unroll
+  for (int i = 0; i < kPC2; ++i) {
+    const int off = (((half * kPC2 + i) * kPW + pw) * kChunk + lane * 8) * 4;
+    X.x2[2 * i] = vec_load(r2, off);
+    X.x2[2 * i + 1] = vec_load(r2, off + 16);
+  }
+}
 
 // Put site P's inputs for prologue wavefront pw in flight: always the same
-// kPC + kPN buffer loads (out of range where there is nothing to load, or
-// when !real), so a wait for one register set never waits for the other.
-__device__ __forceinline__ void pro_issue(ProX &X, CSite &P, bool real, int pw, int lane) {
+// buffer loads (out of range where there is nothing to load), all issued
+// before any is waited for.
+template <bool kDep>
+__device__ __forceinline__ void pro_issue(ProX &X, CSite &P, int pw, int lane) {
   const int K = P.K;
   const bool x8 = P.pro == PRO_X8;
-  const int xlen = real ? (x8 ? K : 2 * K) : 0;
-  const int wlen = real && P.pro == PRO_RMSNORM_DYNQ8 ? 2 * K : 0;
+  const int xlen = x8 ? K : 2 * K;
+  const int wlen = P.pro == PRO_RMSNORM_DYNQ8 ? 2 * K : 0;
   const __amdgpu_buffer_rsrc_t rx =
       __builtin_amdgcn_make_buffer_rsrc((void *)P.x, (short)0, xlen, kBufDword3);
   const __amdgpu_buffer_rsrc_t rw =
@@ -377,6 +450,52 @@ __device__ __forceinline__ void pro_issue(ProX &X, CSite &P, bool real, int pw, 
   }
 #pragma unroll
   for (int c = 0; c < kPN; ++c) X.wv[c] = vec_load(rw, ((c * kPW + pw) * kChunk + lane * 8) * 2);
+  if (kDep) pro_issue_x2(X, P, 0, pw, lane);
+}
+
+// Site P's x through the stamped words of site P.stamp_src (stamp): every
+// lane's chunks as in pro_issue (lane l of chunk c: elements 8l..8l+7, four
+// words in two 16-byte loads, into X.pc[c] and X.x2[c]), reloaded until every
+// word of the wavefront carries the stamp; then X.pc[c] holds the chunk's
+// 8 int16.  The RMSNorm weights are loaded first, as in pro_issue.
+// Bounded: false if the words never all arrived (err bit 1).
+__device__ __forceinline__ bool pro_issue_stamped(ProX &X, CSite &P, uint32_t stamp, int pw,
+                                                  int lane, int32_t *err) {
+  const int K = P.K;
+  const int wlen = P.pro == PRO_RMSNORM_DYNQ8 ? 2 * K : 0;
+  const __amdgpu_buffer_rsrc_t rw =
+      __builtin_amdgcn_make_buffer_rsrc((void *)P.norm_w, (short)0, wlen, kBufDword3);
+#pragma unroll
+  for (int c = 0; c < kPN; ++c) X.wv[c] = vec_load(rw, ((c * kPW + pw) * kChunk + lane * 8) * 2);
+  // words past K are out of the buffer's range: they read as zero, so a
+  // chunk past K is taken as arrived
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc((void *)P.x_stamped, (short)0, 4 * K, kBufDword3);
+  bool ok = false;
+  for (uint32_t n = 0; n < kGridSpin && !ok; ++n) {
+    if (n > 0) __builtin_amdgcn_s_sleep(2);
+    bool mine = true;
+#pragma unroll
+    for (int c = 0; c < kPC; ++c) {
+      const int off = ((c * kPW + pw) * kChunk + lane * 8) * 4;
+      X.pc[c] = vec_load(rx, off);
+      X.x2[c] = vec_load(rx, off + 16);
+    }
+#pragma unroll
+    for (int c = 0; c < kPC; ++c) {
+      const bool past = (c * kPW + pw) * kChunk >= K;
+      mine = mine && (past || ((uint32_t)X.pc[c].y == stamp && (uint32_t)X.pc[c].w == stamp &&
+                               (uint32_t)X.x2[c].y == stamp && (uint32_t)X.x2[c].w == stamp));
+    }
+    ok = __all(mine);
+  }
+  if (!ok && lane == 0) atomicOr(err, 2);
+#pragma unroll
+  for (int c = 0; c < kPC; ++c) {
+    X.pc[c] = make_int4(X.pc[c].x, X.pc[c].z, X.x2[c].x, X.x2[c].z);
+    X.x2[c] = make_int4(0, 0, 0, 0);   // dead from here: no registers held
+  }
+  return ok;
 }
 
 // 8 bytes into the staging area, visible to every CU once waited for
@@ -384,15 +503,29 @@ __device__ __forceinline__ void stage_u64(int8_t *p, uint32_t lo, uint32_t hi) {
   store_coherent((uint64_t *)p, (uint64_t)lo | ((uint64_t)hi << 32));
 }
 
-// The prologue of site P by the 3 prologue wavefronts (pw = 0..2; sync is
+// Where a prologue puts x8 and the offset corrections: the site's staging
+// area in global memory (agent-coherent stores, kLds false) or this CU's
+// own LDS buffer (kLds true); the layout is the same.
+template <bool kLds>
+__device__ __forceinline__ void put_x8(int8_t *base, int off, uint32_t lo, uint32_t hi) {
+  if (kLds) *(uint2 *)(base + off) = make_uint2(lo, hi);
+  else stage_u64(base + off, lo, hi);
+}
+template <bool kLds>
+__device__ __forceinline__ void put_corr(int8_t *base, int i, int32_t v) {
+  int32_t *xlo = (int32_t *)(base + kXloOff);
+  if (kLds) xlo[i] = v;
+  else store_coherent(&xlo[i], v);
+}
+
+// The prologue of site P by the 3 prologue wavefronts (pw = 0..2; ps is
 // their barrier) from the inputs in X: x8 and the offset corrections into
-// the site's staging area stg (agent-coherent stores), and the site's
-// exports (x8, e_x, the RMSNorm output); returns e_x.  Chunks past K are
-// skipped.
-__device__ int group_prologue(CSite &P, Lds &L, int8_t *stg, int pw, int lane,
-                              GroupSync<kPW, false> &sync, ProX &X) {
+// `out` (put_x8 / put_corr), and, when `exports`, the site's exports (x8, e_x, the RMSNorm
+// output); returns e_x.  Chunks past K are skipped.
+template <bool kLds, bool kDep>
+__device__ __forceinline__ int group_prologue(CSite &P, Lds &L, int8_t *out, bool exports,
+                                              int pw, int lane, PSync &ps, ProX &X) {
   const int K = P.K;
-  int32_t *xlo = (int32_t *)(stg + kXloOff);
   if (P.pro == PRO_X8) {
 #pragma unroll
     for (int c = 0; c < kPX; ++c) {
@@ -406,15 +539,38 @@ __device__ int group_prologue(CSite &P, Lds &L, int8_t *stg, int pw, int lane,
         t = __builtin_amdgcn_sdot4(v.z, 0x01010101, t, false);
         t += __builtin_amdgcn_update_dpp(0, t, 0xB1, 0xF, 0xF, false);
         if (off < K) {
-          stage_u64(stg + off, (uint32_t)v.x, (uint32_t)v.y);
-          stage_u64(stg + off + 8, (uint32_t)v.z, (uint32_t)v.w);
-          if ((lane & 1) == 0) store_coherent(&xlo[off / 32], -8 * t);
-          if (P.x8_out) *(int4 *)(P.x8_out + off) = v;
+          put_x8<kLds>(out, off, (uint32_t)v.x, (uint32_t)v.y);
+          put_x8<kLds>(out, off + 8, (uint32_t)v.z, (uint32_t)v.w);
+          if ((lane & 1) == 0) put_corr<kLds>(out, off / 32, -8 * t);
+          if (exports && P.x8_out) *(int4 *)(P.x8_out + off) = v;
         }
       }
     }
-    if (P.e_x_out && pw == 0 && lane == 0) *P.e_x_out = P.e_x_given;
+    if (exports && P.e_x_out && pw == 0 && lane == 0) *P.e_x_out = P.e_x_given;
     return P.e_x_given;
+  }
+  if (kDep && P.pro == PRO_EMUL_DYNQ8) {
+    // ALU EMUL32 at p0 = 12 (gen_layer_script.py:1414-1418): clip16 of the
+    // rounded product, then DYNQ8 below.  The second factor of the first
+    // half of the chunks came with the inputs; the second half's is loaded
+    // into the same registers once those are used.
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (h == 1) pro_issue_x2(X, P, 1, pw, lane);
+#pragma unroll
+      for (int i = 0; i < kPC2; ++i) {
+        const int c = h * kPC2 + i;
+        if ((c * kPW + pw) * kChunk < K) {
+          const int4 a = X.x2[2 * i], b = X.x2[2 * i + 1];
+          const int32_t av[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int64_t v = rshr64((int64_t)av[j] * piece_get(X.pc[c], j), kEmulP0);
+            piece_set(X.pc[c], j, (int16_t)clamp64(v, -32768, 32767));
+          }
+        }
+      }
+    }
   }
   if (P.pro == PRO_RMSNORM_DYNQ8) {
     // layer_fixed.py:1262-1278 in sign-magnitude form (rshift_round rounds
@@ -430,7 +586,7 @@ __device__ int group_prologue(CSite &P, Lds &L, int8_t *stg, int pw, int lane,
         }
     ss = wave_sum_u64(ss);
     if (lane == 0) L.pss[pw] = (int64_t)ss;
-    sync();
+    psync(L, ps, pw, lane);
     ss = 0;
 #pragma unroll
     for (int w = 0; w < kPW; ++w) ss += (uint64_t)L.pss[w];
@@ -468,7 +624,7 @@ __device__ int group_prologue(CSite &P, Lds &L, int8_t *stg, int pw, int lane,
           const int32_t qm = min(q32, 32767 + (int32_t)neg);
           piece_set(X.pc[c], j, (int16_t)(neg ? -qm : qm));
         }
-        if (P.xn_out && base < K) *(int4 *)(P.xn_out + base) = X.pc[c];
+        if (exports && P.xn_out && base < K) *(int4 *)(P.xn_out + base) = X.pc[c];
       }
     }
   }
@@ -480,7 +636,7 @@ __device__ int group_prologue(CSite &P, Lds &L, int8_t *stg, int pw, int lane,
       for (int j = 0; j < 8; ++j) mx = max(mx, abs((int32_t)piece_get(X.pc[c], j)));
   mx = wave_max_i32(mx);
   if (lane == 0) L.pmx[pw] = mx;
-  sync();
+  psync(L, ps, pw, lane);
   mx = 0;
 #pragma unroll
   for (int w = 0; w < kPW; ++w) mx = max(mx, L.pmx[w]);
@@ -508,27 +664,29 @@ __device__ int group_prologue(CSite &P, Lds &L, int8_t *stg, int pw, int lane,
       t4 += __builtin_amdgcn_update_dpp(0, t4, 0xB1, 0xF, 0xF, false);
       t4 += __builtin_amdgcn_update_dpp(0, t4, 0x4E, 0xF, 0xF, false);
       if (base < K) {
-        stage_u64(stg + base, lo, hi);
-        if ((lane & 3) == 0) store_coherent(&xlo[base / 32], -8 * t4);
-        if (P.x8_out) *(uint2 *)(P.x8_out + base) = make_uint2(lo, hi);
+        put_x8<kLds>(out, base, lo, hi);
+        if ((lane & 3) == 0) put_corr<kLds>(out, base / 32, -8 * t4);
+        if (exports && P.x8_out) *(uint2 *)(P.x8_out + base) = make_uint2(lo, hi);
       }
     }
   }
-  if (P.e_x_out && pw == 0 && lane == 0) *P.e_x_out = e;
+  if (exports && P.e_x_out && pw == 0 && lane == 0) *P.e_x_out = e;
   return e;
 }
 
 // Site s's prologue, by the CU that owns it: inputs, compute, then -- every
 // store of the three wavefronts complete -- e_x and the site's flag.
-__device__ void compute_publish(CSite &P, Lds &L, int8_t *stg, uint32_t *flag, uint32_t epoch,
-                                int pw, int lane, GroupSync<kPW, false> &sync) {
+template <bool kDep>
+__device__ PSync compute_publish(CSite &P, Lds &L, int8_t *stg, uint32_t *flag, uint32_t epoch,
+                                 int pw, int lane, PSync ps) {
   ProX X;
-  pro_issue(X, P, true, pw, lane);
-  const int e = group_prologue(P, L, stg, pw, lane, sync, X);
+  pro_issue<kDep>(X, P, pw, lane);
+  const int e = group_prologue<false, kDep>(P, L, stg, true, pw, lane, ps, X);
   if (pw == 0 && lane == 0) store_coherent((int32_t *)(stg + kXB), (int32_t)e);
   wait_vm_all();
-  sync();
+  psync(L, ps, pw, lane);
   if (pw == 0 && lane == 0) store_coherent(flag, epoch);
+  return ps;
 }
 
 // the wavefront waits until site s's activations are staged in this launch
@@ -610,10 +768,185 @@ __device__ void head_arrive(const StreamParams &S, int G, uint64_t best) {
   S.result[1] = (int32_t)((uint32_t)(k >> 32) ^ 0x80000000u);
 }
 
+// The prologue wavefronts' program: every site's activations, in order,
+// into the LDS ring.  A function of its own, not inlined: its code (the
+// RMSNorm, EMUL32 and DYNQ8 variants, staged and local) would otherwise share
+// one register allocation and layout with the weight wavefronts' loop, which
+// measured slower on the independent-input stream although none of it runs
+// there.  Arguments are made wavefront-uniform, so table reads stay scalar.
+template <bool kDep>
+__device__ __forceinline__ void prologue_role(const GemvParams *sites_arg, int nsites, int r,
+                                           int G, int wave, uint32_t *done, int8_t *stage,
+                                           uint32_t epoch, int32_t *err) {
+  Lds &L = g_lds;
+  CSite *sites = (CSite *)uniform_ptr(sites_arg);
+  done = (uint32_t *)uniform_ptr(done);
+  stage = (int8_t *)uniform_ptr(stage);
+  err = (int32_t *)uniform_ptr(err);
+  nsites = __builtin_amdgcn_readfirstlane(nsites);
+  r = __builtin_amdgcn_readfirstlane(r);
+  G = __builtin_amdgcn_readfirstlane(G);
+  wave = __builtin_amdgcn_readfirstlane(wave);
+  epoch = __builtin_amdgcn_readfirstlane(epoch);
+  const uint32_t fbase = (epoch - 1u) * (uint32_t)(nsites + 1);
+  const int tid = threadIdx.x, lane = tid & 63;
+  // Every site's prologue is computed once, by CU s % G, into the site's
+  // staging area (a site behind no fence at once, a fenced one after its
+  // grid-wide wait); every CU then copies the staged sites, in order, into
+  // its buffer ring ahead of the weight wavefronts.
+  const int pw = wave - kPW0;
+  // (default wave priority: these wavefronts mostly wait, and raised
+  // priority lets their polls outrank the weight wavefronts' work)
+  PSync ps{0, 1};
+  uint32_t *sflag = done + stream_flag_site0(G);
+  bool ok = true;
+  for (int s = r; s < nsites; s += G)
+    if (sites[s].fence_at == 0)
+      ps = compute_publish<kDep>(sites[s], L, stage + (size_t)s * kStageBytes, sflag + s, epoch,
+                           pw, lane, ps);
+  for (int s = 0; s < nsites; ++s) {
+    // lane-derived addresses are recomputed per site from an opaque copy
+    // of the thread index, so the compiler does not keep them live
+    int tid_s = tid;
+    asm volatile("" : "+v"(tid_s));
+    const int lane = tid_s & 63;
+    CSite &P = sites[s];
+    const int8_t *stg = stage + (size_t)s * kStageBytes;
+    const int b = s % kNB;
+    if (kDep) touch_site(&P);
+    if (kDep && P.local_pro) {
+      // behind a fence, every CU computes the site's prologue itself,
+      // straight into its LDS buffer: one read of the inputs after the
+      // grid-wide wait, instead of a staged copy that would first have to
+      // be computed, published and flagged by one CU
+      if (s >= kNB) ok = wait_weights_past(L, s - kNB, lane) && ok;
+      ok = lds_wait_ge(&L.gridok, P.fence_at) && ok;
+      ProX X;
+      if (P.stamp_src >= 0) {
+        // no grid-wide wait: the input's own words say when it is whole.
+        // Polled once this CU has stored its own share (a CU that polls
+        // while others still stream would only add traffic).
+        ok = lds_wait_ge(&L.served, P.stamp_src) && ok;
+        ok = pro_issue_stamped(X, P, fbase + (uint32_t)P.stamp_src + 1u, pw, lane, err) && ok;
+      } else {
+        pro_issue<kDep>(X, P, pw, lane);
+      }
+      const int e = group_prologue<true, kDep>(P, L, L.x[b], s % G == r, pw, lane, ps, X);
+      if (lane == 0) {
+        if (pw == 0) lds_write_i32(&L.ex[b], e);
+        lds_write_i32(&L.ready[b][pw], s);
+      }
+      continue;
+    }
+    if (s % G == r && P.fence_at > 0) {
+      ok = lds_wait_ge(&L.gridok, P.fence_at) && ok;
+      ps = compute_publish<kDep>(P, L, stage + (size_t)s * kStageBytes, sflag + s, epoch, pw,
+                           lane, ps);
+    }
+    if (s >= kNB) ok = wait_weights_past(L, s - kNB, lane) && ok;
+    ok = wait_staged(sflag + s, epoch, lane, err) && ok;
+    load_staged(stg, L.x[b], P.K, pw, lane);
+    const int e = __hip_atomic_load((const int32_t *)(stg + kXB), __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    wait_vm_all();
+    // this wavefront's copies into buffer b have landed (lds_write_i32
+    // waits for its LDS work first); the site is ready once all three
+    // have posted
+    if (lane == 0) {
+      if (pw == 0) lds_write_i32(&L.ex[b], e);
+      lds_write_i32(&L.ready[b][pw], s);
+    }
+  }
+  if (!(ok && ps.ok) && lane == 0) lds_or_i32(&L.err, 4);
+}
+
+// The weight wavefronts' program.  (As a function of its own, with a
+// register allocation apart from the other roles', it ran 1-2 % slower on
+// the independent-input stream and 2.5 % slower on the chained one than
+// inlined, so it is inlined.)  The arguments are made wavefront-uniform, so
+// table reads stay scalar loads.
+template <bool kDep>
+__device__ __forceinline__ void weight_role(const GemvParams *sites_arg, int nsites, int r,
+                                            int G, int wave) {
+  Lds &L = g_lds;
+  CSite *sites = (CSite *)uniform_ptr(sites_arg);
+  nsites = __builtin_amdgcn_readfirstlane(nsites);
+  r = __builtin_amdgcn_readfirstlane(r);
+  G = __builtin_amdgcn_readfirstlane(G);
+  wave = __builtin_amdgcn_readfirstlane(wave);
+  const int tid = threadIdx.x, lane = tid & 63;
+  // A holds item k of this wavefront's sequence, B item k + 1; cn is the
+  // next item to put in flight
+  Cursor ca, cb, cn;
+  cur_init(sites, nsites, r, G, wave, ca);
+  cb = ca;
+  cur_next(sites, nsites, r, G, cb);
+  cn = cb;
+  cur_next(sites, nsites, r, G, cn);
+  BlockRegs A, B;
+  issue_block(A, sites, nsites, G, ca, lane);
+  issue_block(B, sites, nsites, G, cb, lane);
+  int s_cur = -1, e_x = 0, contributors = 0;
+  int64_t p = 0;
+  // consume the block in R (item c; this wavefront's next item is nx),
+  // refill R with the item two ahead, and add into the tile after this
+  // wavefront's last block of it
+  auto step = [&](BlockRegs &R, Cursor &c, const Cursor &nx) {
+    // the lane-derived addresses are recomputed from an opaque copy of the
+    // thread index, so the compiler does not keep them all live
+    int tid_s = tid;
+    asm volatile("" : "+v"(tid_s));
+    const int lane_s = tid_s & 63;
+    if (c.s != s_cur) {
+      // done with every earlier site; wait for this one's activations
+      s_cur = c.s;
+      lds_write_i32(&L.wsite[wave], s_cur);
+      wait_ready(L, s_cur % kNB, s_cur, lane_s);
+      e_x = __builtin_amdgcn_readfirstlane(lds_read_i32(&L.ex[s_cur % kNB]));
+      contributors = min(sites[s_cur].nblk, kCW);
+    }
+    CSite &P = sites[c.s];
+    const int i = c.j / c.nblk, b = c.j - i * c.nblk;
+    const int8_t *xb = L.x[c.s % kNB];
+    p = dot_block(R, groups_in(P.NG, b), b * kGroupsPerBlock, lane_s & 3, xb,
+                  (const int32_t *)(xb + kXloOff), p);
+    const bool last = !(nx.s == c.s && nx.j / nx.nblk == i);
+    const Cursor done = c;
+    auto finish_tile = [&]() {
+      const int kt = done.kt0 + i;
+      if (tile_add(L, kt, p, contributors, lane_s)) {
+        const int t = done.first + i * G;
+        CJob &J = P.job[job_of(P, t)];
+        tile_epilogue(L, kt, J, t - J.tile0, e_x, lane_s);
+      }
+      p = 0;
+    };
+    // At this wavefront's last block of a site, its tile is finished before
+    // the refill: the refill's cursor reads table entries of sites further
+    // ahead, and a scalar-cache miss there would delay the site's completion
+    // -- which a fenced site after it waits for.  Elsewhere the refill goes
+    // first, to keep the weight stream full.
+    const bool site_end = kDep && nx.s != c.s;
+    if (last && site_end) finish_tile();
+    c = cn;
+    cur_next(sites, nsites, r, G, cn);
+    issue_block(R, sites, nsites, G, c, lane_s);
+    if (last && !site_end) finish_tile();
+  };
+  for (;;) {
+    if (ca.s >= nsites) break;
+    step(A, ca, cb);
+    if (cb.s >= nsites) break;
+    step(B, cb, ca);
+  }
+  lds_write_i32(&L.wsite[wave], nsites);
+}
+
+template <bool kDep>
 __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
                                                           const GemvParams *__restrict__ sites_arg) {
   CSite *sites = (CSite *)sites_arg;
-  __shared__ Lds L;
+  Lds &L = g_lds;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = gridDim.x, r = blockIdx.x;
@@ -635,6 +968,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
   if (tid < kCW) L.wsite[tid] = 0;
   if (tid < kPW) L.psync[tid] = 0;
   if (tid == 0) {
+    L.served = -1;
     L.gridok = 0;
     L.abort = 0;
     L.err = 0;
@@ -649,7 +983,12 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
     for (int s = 0; s < nsites; ++s) {
       CSite &P = sites[s];
       if (S.trace && r == 0 && lane == 0) S.trace[s] = wall_clock64();
-      ctrl_serve(P, L, kt0, r, G, lane);
+      // the next sites' table entries, for the waits, epilogues and weight
+      // cursors around their fences
+      if (kDep)
+        for (int a = s + 1; a < nsites && a <= s + 3; ++a) touch_site(&sites[a]);
+      ctrl_serve<kDep>(P, L, kt0, r, G, lane, fbase + (uint32_t)s + 1u);
+      if (kDep && lane == 0) lds_write_i32(&L.served, s);
       {
         const int first = (r + P.tile_rot) % G;
         kt0 += first < P.total_tiles ? (P.total_tiles - 1 - first) / G + 1 : 0;
@@ -663,107 +1002,9 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
       }
     }
   } else if (wave >= kPW0) {
-    // Every site's prologue is computed once, by CU s % G, into the site's
-    // staging area (a site behind no fence at once, a fenced one after its
-    // grid-wide wait); every CU then copies the staged sites, in order, into
-    // its buffer ring ahead of the weight wavefronts.
-    const int pw = wave - kPW0;
-    // (default wave priority: these wavefronts mostly wait, and raised
-    // priority lets their polls outrank the weight wavefronts' work)
-    GroupSync<kPW, false> sync{L.psync, kPW0, 0, true};
-    uint32_t *sflag = S.done + stream_flag_site0(G);
-    bool ok = true;
-    for (int s = r; s < nsites; s += G)
-      if (sites[s].fence_at == 0)
-        compute_publish(sites[s], L, S.stage + (size_t)s * kStageBytes, sflag + s, S.epoch,
-                        pw, lane, sync);
-    for (int s = 0; s < nsites; ++s) {
-      // lane-derived addresses are recomputed per site from an opaque copy
-      // of the thread index, so the compiler does not keep them live
-      int tid_s = tid;
-      asm volatile("" : "+v"(tid_s));
-      const int lane = tid_s & 63;
-      CSite &P = sites[s];
-      const int8_t *stg = S.stage + (size_t)s * kStageBytes;
-      if (s % G == r && P.fence_at > 0) {
-        ok = lds_wait_ge(&L.gridok, P.fence_at) && ok;
-        compute_publish(P, L, S.stage + (size_t)s * kStageBytes, sflag + s, S.epoch, pw, lane,
-                        sync);
-      }
-      const int b = s % kNB;
-      if (s >= kNB) ok = wait_weights_past(L, s - kNB, lane) && ok;
-      ok = wait_staged(sflag + s, S.epoch, lane, S.err) && ok;
-      load_staged(stg, L.x[b], P.K, pw, lane);
-      const int e = __hip_atomic_load((const int32_t *)(stg + kXB), __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
-      wait_vm_all();
-      // this wavefront's copies into buffer b have landed (lds_write_i32
-      // waits for its LDS work first); the site is ready once all three
-      // have posted
-      if (lane == 0) {
-        if (pw == 0) lds_write_i32(&L.ex[b], e);
-        lds_write_i32(&L.ready[b][pw], s);
-      }
-    }
-    if (!(ok && sync.ok) && lane == 0) lds_or_i32(&L.err, 4);
+    prologue_role<kDep>(sites_arg, S.nsites, r, G, wave, S.done, S.stage, S.epoch, S.err);
   } else {
-    // A holds item k of this wavefront's sequence, B item k + 1; cn is the
-    // next item to put in flight
-    Cursor ca, cb, cn;
-    cur_init(sites, nsites, r, G, wave, ca);
-    cb = ca;
-    cur_next(sites, nsites, r, G, cb);
-    cn = cb;
-    cur_next(sites, nsites, r, G, cn);
-    BlockRegs A, B;
-    issue_block(A, sites, nsites, G, ca, lane);
-    issue_block(B, sites, nsites, G, cb, lane);
-    int s_cur = -1, e_x = 0, contributors = 0;
-    int64_t p = 0;
-    // consume the block in R (item c; this wavefront's next item is nx),
-    // refill R with the item two ahead, and add into the tile after this
-    // wavefront's last block of it
-    auto step = [&](BlockRegs &R, Cursor &c, const Cursor &nx) {
-      // the lane-derived addresses are recomputed from an opaque copy of the
-      // thread index, so the compiler does not keep them all live
-      int tid_s = tid;
-      asm volatile("" : "+v"(tid_s));
-      const int lane_s = tid_s & 63;
-      if (c.s != s_cur) {
-        // done with every earlier site; wait for this one's activations
-        s_cur = c.s;
-        lds_write_i32(&L.wsite[wave], s_cur);
-        wait_ready(L, s_cur % kNB, s_cur, lane_s);
-        e_x = __builtin_amdgcn_readfirstlane(lds_read_i32(&L.ex[s_cur % kNB]));
-        contributors = min(sites[s_cur].nblk, kCW);
-      }
-      CSite &P = sites[c.s];
-      const int i = c.j / c.nblk, b = c.j - i * c.nblk;
-      const int8_t *xb = L.x[c.s % kNB];
-      p = dot_block(R, groups_in(P.NG, b), b * kGroupsPerBlock, lane_s & 3, xb,
-                    (const int32_t *)(xb + kXloOff), p);
-      const bool last = !(nx.s == c.s && nx.j / nx.nblk == i);
-      const Cursor done = c;
-      c = cn;
-      cur_next(sites, nsites, r, G, cn);
-      issue_block(R, sites, nsites, G, c, lane_s);
-      if (last) {
-        const int kt = done.kt0 + i;
-        if (tile_add(L, kt, p, contributors, lane_s)) {
-          const int t = done.first + i * G;
-          CJob &J = P.job[job_of(P, t)];
-          tile_epilogue(L, kt, J, t - J.tile0, e_x, lane_s);
-        }
-        p = 0;
-      }
-    };
-    for (;;) {
-      if (ca.s >= nsites) break;
-      step(A, ca, cb);
-      if (cb.s >= nsites) break;
-      step(B, cb, ca);
-    }
-    lds_write_i32(&L.wsite[wave], nsites);
+    weight_role<kDep>(sites_arg, nsites, r, G, wave);
   }
 
   int tid_e = tid;
@@ -781,29 +1022,32 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
 }  // namespace
 
 hipError_t launch_stream(const StreamParams &sp, int grid, hipStream_t s, bool cooperative,
-                         hipEvent_t start, hipEvent_t stop) {
+                         bool dependent, hipEvent_t start, hipEvent_t stop) {
   const GemvParams *sites = sp.sites;
+  auto kernel = dependent ? stream_kernel<true> : stream_kernel<false>;
   if (cooperative) {
     void *args[] = {(void *)&sp, (void *)&sites};
     hipError_t e = start ? hipEventRecord(start, s) : hipSuccess;
     if (e == hipSuccess)
-      e = hipLaunchCooperativeKernel((const void *)stream_kernel, dim3(grid), dim3(kThreads),
-                                     args, 0, s);
+      e = hipLaunchCooperativeKernel((const void *)kernel, dim3(grid), dim3(kThreads), args, 0,
+                                     s);
     if (e == hipSuccess && stop) e = hipEventRecord(stop, s);
     return e;
   }
   // events, when given, are recorded by the dispatch itself
-  hipExtLaunchKernelGGL(stream_kernel, dim3(grid), dim3(kThreads), 0, s, start, stop, 0, sp,
-                        sites);
+  hipExtLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), 0, s, start, stop, 0, sp, sites);
   return hipGetLastError();
 }
 
 int stream_max_blocks_per_cu() {
-  int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, stream_kernel, kThreads, 0) !=
-          hipSuccess || n < 1)
-    n = 1;
-  return n > 1 ? 1 : n;
+  int n = 0, m = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, stream_kernel<false>, kThreads, 0) !=
+          hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&m, stream_kernel<true>, kThreads, 0) !=
+          hipSuccess)
+    return 1;
+  n = n < m ? n : m;
+  return n < 1 ? 1 : (n > 1 ? 1 : n);
 }
 
 size_t stream_counter_words(int grid, int nsites) {

@@ -419,6 +419,33 @@ class Plan:
         self.nsites += 1
         self.nmats += n
 
+    def add_site_emul(self, weights, epilogues, p0s, outs, x, x2, x8_out=None,
+                      e_x_out=None):
+        """The SwiGLU product site: DYNQ8(EMUL32(x2, x; 12)) with x the
+        gate's SILU32 output (int16) and x2 the up projection's (int32),
+        then the site's matrices (the down projection)."""
+        n = len(weights)
+        if not (n == len(epilogues) == len(p0s) == len(outs)):
+            raise ValueError("site: one epilogue, p0 and output per matrix")
+        K = weights[0].K
+        for w, e, o in zip(weights, epilogues, outs):
+            _dev(o, _EPI_BYTES.get(int(e), 8) * w.nrows, "site output")
+        _dev(x, 2 * K, "x")
+        _dev(x2, 4 * K, "x2")
+        _dev(x8_out, K, "x8_out", required=False)
+        _dev(e_x_out, 4, "e_x_out", required=False)
+        wa = (ctypes.c_void_p * n)(*[w.h.value for w in weights])
+        oa = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
+        ea = np.ascontiguousarray(epilogues, dtype=np.int32)
+        pa = np.ascontiguousarray(p0s, dtype=np.int32)
+        N.check(N.lib().w4a8_plan_add_site_emul(
+            self.h, n, wa, _ptr(ea), _ptr(pa), oa, _dptr(x), _dptr(x2),
+            _dptr(x8_out), _dptr(e_x_out)), "plan_add_site_emul")
+        self._keep += [weights, outs, x, x2, x8_out, e_x_out]
+        self.bytes += sum(w.wire_bytes for w in weights)
+        self.nsites += 1
+        self.nmats += n
+
     def add_head(self, w, x, result, prologue=N.PRO_DYNQ8, e_x=0, norm_w=None,
                  in_f=0, one_plus=False):
         _dev(x, _x_bytes(prologue, w.K), "x")
@@ -441,6 +468,15 @@ class Plan:
         one); results are the same either way."""
         N.check(N.lib().w4a8_plan_set_fences(self.h, int(fences)), "plan_set_fences")
 
+    def fenced(self):
+        """Per site, how a persistent replay orders it (under the current
+        fence mode): N.WAIT_NONE, N.WAIT_GRID (every earlier site on every
+        workgroup) or N.WAIT_INPUT (the one earlier output it reads, through
+        that output's stamped words)."""
+        f = np.zeros(self.nsites, dtype=np.int32)
+        N.check(N.lib().w4a8_plan_fences(self.h, self.nsites, _ptr(f)), "plan_fences")
+        return [int(v) for v in f]
+
     def run(self):
         N.check(N.lib().w4a8_plan_run(self.h), "plan_run")
 
@@ -448,6 +484,13 @@ class Plan:
         """Per-step GEMV kernel times in ms (one eager, instrumented pass)."""
         ms = np.zeros(self.nsites, dtype=np.float32)
         N.check(N.lib().w4a8_plan_profile(self.h, self.nsites, _ptr(ms)), "plan_profile")
+        return ms
+
+    def time_launches(self, n):
+        """Kernel ms of each of n back-to-back replays of a persistent plan
+        (dispatch-recorded events)."""
+        ms = np.zeros(n, dtype=np.float32)
+        N.check(N.lib().w4a8_plan_time_launches(self.h, n, _ptr(ms)), "plan_time_launches")
         return ms
 
     def close(self):

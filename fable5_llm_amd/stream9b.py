@@ -121,10 +121,10 @@ def chunks_head(nrows, chunk=2048):
 # ---------------------------------------------------------------------------
 # device-resident synthetic stream
 # ---------------------------------------------------------------------------
-def synth_image(gen, nrows, K):
+def synth_image(gen, nrows, K, log2_lo=-10.0):
     """Row image of random W4A8 weights on the device: every weight byte is
-    two uniform int4 codes; scales s = 2^U(-10, -4) encoded at e = -3 as
-    m = round(s * 2^18) (w4a8_ref.py:170-176)."""
+    two uniform int4 codes; scales s = 2^U(log2_lo, log2_lo + 6) encoded at
+    e = -3 as m = round(s * 2^18) (w4a8_ref.py:170-176)."""
     import torch
     ng = K // 128
     stride = (ng + (ng + 31) // 32) * 64
@@ -132,7 +132,7 @@ def synth_image(gen, nrows, K):
     img[:, :K // 2] = torch.randint(0, 256, (nrows, K // 2), dtype=torch.uint8,
                                     device=gen.device, generator=gen)
     u = torch.rand((nrows, ng), dtype=torch.float64, device=gen.device, generator=gen)
-    m = torch.clamp(torch.round(torch.exp2(-10.0 + 6.0 * u) * (1 << 18)), 1, 65535)
+    m = torch.clamp(torch.round(torch.exp2(log2_lo + 6.0 * u) * (1 << 18)), 1, 65535)
     m = m.to(torch.int32)
     img[:, K // 2:K // 2 + 2 * ng] = torch.stack(
         [m & 0xFF, m >> 8], dim=-1).reshape(nrows, 2 * ng).to(torch.uint8)
@@ -162,34 +162,121 @@ def synth_norm_w(gen, K, one_plus):
     return torch.clamp(q, -32768, 32767).to(torch.int16)
 
 
+def chain_sources(sites):
+    """For a chained step, where each site's int16 input comes from: None
+    for the step's own input (the first site's residual stream), else
+    (site, matrix, first row) of the earlier output it reads, K rows long.
+
+    The layer math between sites (attention, the DeltaNet recurrence, the
+    SwiGLU product, residual adds) is out of scope; each site reads the
+    output that stands in its place in the decode order
+    (gen_layer_script.py:1928-2190), so every site depends on the one
+    before it, as in the reference's sequencer:
+      ln1        <- the previous layer's down projection (layer 0: the input)
+      dn_heads   <- in_z (4096 rows, the gated-heads path)
+      attn_heads <- q_proj rows 0..4095
+      ln2        <- out / o_proj
+      swiglu     <- EMUL32(gate, up): the SwiGLU product, formed in the
+                    site's prologue (its second factor: emul_sources)
+      final_norm <- the last down projection"""
+    src, prev = [], None
+    for si, s in enumerate(sites):
+        tail = s.name.split(".")[-1]
+        if s.head or tail == "ln1":
+            src.append(prev)
+        elif tail == "dn_heads":
+            src.append((si - 1, 1, 0))
+        elif tail == "attn_heads":
+            src.append((si - 1, 0, 0))
+        elif tail == "ln2":
+            src.append((si - 1, 0, 0))
+        elif tail == "swiglu":
+            src.append((si - 1, 0, 0))
+            prev = (si, 0, 0)
+        else:
+            raise ValueError(f"no chain source for site {s.name}")
+    for si, (s, c) in enumerate(zip(sites, src)):
+        if c is not None:
+            m = sites[c[0]].mats[c[1]]
+            assert c[0] < si and c[2] + s.K <= m.nrows and m.epi in (
+                N.EPI_MOVY_I16, N.EPI_SILU32), (s.name, m.name)
+    return src
+
+
+def emul_sources(sites):
+    """For a chained step: (site, matrix) of the up projection whose int32
+    output is the second factor of each swiglu site's EMUL32, else None."""
+    out = []
+    for si, s in enumerate(sites):
+        if s.name.endswith(".swiglu"):
+            up = sites[si - 1].mats[1]
+            assert up.epi == N.EPI_MOVY_P32 and up.nrows == s.K, up.name
+            out.append((si - 1, 1))
+        else:
+            out.append(None)
+    return out
+
+
+# Scales of the chained step's weights: 2^U(-13, -7), a gain of about one per
+# site.  With the 2^U(-10, -4) scales of the independent-input stream every
+# matvec scales its input up about 8 times, so a chain saturates: SILU32
+# outputs clip and the down projections see constant inputs.  The bytes,
+# shapes and order are the same, so the timing is too.
+CHAIN_LOG2_LO = -13.0
+
+
 class Stream9B:
     """All 249 matrices resident on one device with their inputs and
-    outputs, wired into one Plan (site order kept)."""
+    outputs, wired into one Plan (site order kept).
 
-    def __init__(self, ctx, seed=0, sites=None, mode=N.PLAN_PERSISTENT, fences=N.FENCE_ALL):
+    chain=False: every site reads its own seeded input, so the sites share
+    no buffer.  chain=True: every site reads an earlier site's output
+    (chain_sources; the swiglu sites form EMUL32(gate, up) in their
+    prologue), so each one waits for the site before it, as in a decode
+    step; only the first site's input (`x0`) is seeded, and the weights'
+    scales are CHAIN_LOG2_LO's.
+    weights_from: another Stream9B whose resident matrices this one uses
+    (same schedule) instead of uploading its own."""
+
+    def __init__(self, ctx, seed=0, sites=None, mode=N.PLAN_PERSISTENT, fences=N.FENCE_ALL,
+                 chain=False, weights_from=None):
         import torch
         from .engine import Plan
         self.ctx = ctx
         self.sites = sites or schedule()
+        self.chain = chain
+        self.src = chain_sources(self.sites) if chain else [None] * len(self.sites)
+        self.emul = emul_sources(self.sites) if chain else [None] * len(self.sites)
+        log2_lo = CHAIN_LOG2_LO if chain else -10.0
         dev = torch.device("cuda", ctx.device)
         gen = torch.Generator(device=dev)
         gen.manual_seed(seed)
         self.e_x = torch.zeros(len(self.sites), dtype=torch.int32, device=dev)
         self.inputs, self.weights, self.outs, self.x8 = [], [], [], []
+        self.own_weights = weights_from is None
+        self.x0 = None
         self.plan = Plan(ctx)
         for si, s in enumerate(self.sites):
             x = synth_x16(gen, s.K, s.in_f)
+            if self.src[si] is not None:
+                psi, pmi, off = self.src[si]
+                x = self.outs[psi][pmi][off:off + s.K]
+            elif chain:
+                self.x0 = x
             nw = synth_norm_w(gen, s.K, s.one_plus) if s.prologue == N.PRO_RMSNORM_DYNQ8 else None
             x8 = torch.empty(s.K, dtype=torch.int8, device=dev)
             ws, outs, imgs = [], [], []
-            for m in s.mats:
-                imgs.append(synth_image(gen, m.nrows, m.K))
-            # the images were written on torch's stream; the engine may run
-            # on its own: order the repack after them, and keep them alive
-            # until it has run
-            torch.cuda.current_stream(dev).synchronize()
-            for m, img in zip(s.mats, imgs):
-                ws.append(ctx.upload(img, m.nrows, m.K, sh_for_k(m.K)))
+            if weights_from is None:
+                for m in s.mats:
+                    imgs.append(synth_image(gen, m.nrows, m.K, log2_lo))
+                # the images were written on torch's stream; the engine may
+                # run on its own: order the repack after them, and keep them
+                # alive until it has run
+                torch.cuda.current_stream(dev).synchronize()
+                for m, img in zip(s.mats, imgs):
+                    ws.append(ctx.upload(img, m.nrows, m.K, sh_for_k(m.K)))
+            else:
+                ws = list(weights_from.weights[si])
             for m in s.mats:
                 if s.head:
                     outs.append(torch.zeros(2, dtype=torch.int32, device=dev))
@@ -203,6 +290,11 @@ class Stream9B:
                                    in_f=s.in_f, one_plus=s.one_plus)
                 # the head's DYNQ8 input is not exported by the fused launch
                 x8 = None
+            elif self.emul[si] is not None:
+                up = self.outs[self.emul[si][0]][self.emul[si][1]]
+                self.plan.add_site_emul(ws, [m.epi for m in s.mats],
+                                        [m.p0(s.in_f) for m in s.mats], outs, x, up,
+                                        x8_out=x8, e_x_out=self.e_x[si:si + 1])
             else:
                 self.plan.add_site(ws, [m.epi for m in s.mats],
                                    [m.p0(s.in_f) for m in s.mats], outs, x,
@@ -224,8 +316,38 @@ class Stream9B:
     def profile(self):
         return self.plan.profile()
 
+    def reseed(self, seed):
+        """New seeded inputs in place (the plan keeps its pointers): every
+        site's own input (for a chain, only the first site's) and every
+        RMSNorm weight, drawn in site order, so two streams reseeded alike
+        have equal inputs whatever they were built from."""
+        import torch
+        gen = torch.Generator(device=self.e_x.device)
+        gen.manual_seed(seed)
+        for si, s in enumerate(self.sites):
+            x, nw = self.inputs[si]
+            if self.src[si] is None:
+                x.copy_(synth_x16(gen, s.K, s.in_f))
+            if nw is not None:
+                nw.copy_(synth_norm_w(gen, s.K, s.one_plus))
+        torch.cuda.synchronize(self.e_x.device)
+
+    def clear_outputs(self, value=0):
+        """Overwrite every output, export and the head result (a later run
+        must write them all again)."""
+        import torch
+        for outs in self.outs:
+            for o in outs:
+                o.fill_(value)
+        for x8 in self.x8:
+            if x8 is not None:
+                x8.fill_(value)
+        self.e_x.fill_(value)
+        torch.cuda.synchronize(self.e_x.device)
+
     def close(self):
         self.plan.close()
-        for ws in self.weights:
-            for w in ws:
-                w.free()
+        if self.own_weights:
+            for ws in self.weights:
+                for w in ws:
+                    w.free()

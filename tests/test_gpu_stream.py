@@ -1,9 +1,18 @@
 """The full Qwen3.5-9B-shaped stream (249 matrices, 4.09 GB) on the device,
-replayed as a HIP graph and as one persistent launch (every site fenced, and
-fenced only where buffers are shared), checked bit-exactly against the
-C/numpy oracle:
-every site's DYNQ8 output and exponent, every MOVY / SILU32 output, and the
-LM-head argmax."""
+checked bit-exactly against the C/numpy oracle: every site's DYNQ8 output
+and exponent, every MOVY / SILU32 output and the LM-head argmax.
+
+Two streams over one set of weights each:
+  * independent inputs (every site its own seeded vector; the bench's
+    headline workload), and
+  * chained (every site reads an earlier site's output, the swiglu sites
+    form EMUL32(gate, up) in their prologue: a decode step's dependences),
+in every plan mode: HIP graph, persistent with fences from buffers or on
+every site, and the cooperative launch.  Each runs 4 input seeds, twice
+each, with every output overwritten before each run, so a site that read
+an input before its producer finished, or a replay that skipped work,
+cannot pass (the reference's discipline: at least 4 seeds, each run
+twice, CHARTER.md:21-26)."""
 import numpy as np
 import pytest
 
@@ -13,28 +22,78 @@ from tests import stream_check as sc
 
 pytestmark = pytest.mark.gpu
 
+MODES = [(N.PLAN_GRAPH, N.FENCE_ALL), (N.PLAN_PERSISTENT, N.FENCE_AUTO),
+         (N.PLAN_PERSISTENT, N.FENCE_ALL), (N.PLAN_PERSISTENT_COOP, N.FENCE_AUTO)]
+SEEDS = (101, 202, 303, 404)
 
-@pytest.mark.parametrize("mode,fences", [(N.PLAN_GRAPH, N.FENCE_ALL),
-                                         (N.PLAN_PERSISTENT, N.FENCE_ALL),
-                                         (N.PLAN_PERSISTENT, N.FENCE_AUTO),
-                                         (N.PLAN_PERSISTENT_COOP, N.FENCE_AUTO)])
-def test_full_stream_bit_exact(engine, mode, fences):
-    st = stream9b.Stream9B(engine, seed=7, mode=mode, fences=fences)
+
+def _mode_name(mode, fences):
+    return {N.PLAN_GRAPH: "graph", N.PLAN_PERSISTENT: "persistent",
+            N.PLAN_PERSISTENT_COOP: "coop"}[mode] + \
+        ("/auto" if fences == N.FENCE_AUTO else "/all")
+
+
+def _check_modes(engine, chain, weight_seed):
+    base = stream9b.Stream9B(engine, seed=weight_seed, chain=chain, mode=MODES[0][0],
+                             fences=MODES[0][1])
+    views = [base] + [stream9b.Stream9B(engine, chain=chain, weights_from=base, mode=m,
+                                        fences=f) for m, f in MODES[1:]]
     try:
-        st.run()
-        st.run()                      # second replay of the same graph
-        engine.sync()
-        host = sc.host_inputs(st)
-        ys, _ = sc.run_cpu_stream(st, host)
-        bad = sc.compare(st, host, ys)
-        assert not bad, bad[:10]
-        # replays are deterministic: a third run leaves every output unchanged
-        before = [o.clone() for outs in st.outs for o in outs]
-        st.run()
-        engine.sync()
-        after = [o for outs in st.outs for o in outs]
-        assert all(bool((a == b).all()) for a, b in zip(before, after))
-        prof = st.profile()
-        assert prof.shape == (129,) and np.all(prof > 0)
+        imgs = sc.images(base)
+        for seed in SEEDS:
+            ref = None
+            for st, (m, f) in zip(views, MODES):
+                st.reseed(seed)
+                for rep in range(2):
+                    st.clear_outputs(-1)
+                    st.run()
+                    engine.sync()
+                    host = sc.host_inputs(st, imgs)
+                    if ref is None:
+                        ref, _ = sc.run_cpu_stream(st, host)
+                        if chain:
+                            # a chain worth checking: no output collapsed
+                            distinct, railed = sc.spread(ref)
+                            assert distinct >= 32 and railed < 0.25, (distinct, railed)
+                    bad = sc.compare(st, host, ref)
+                    assert not bad, (_mode_name(m, f), seed, rep, bad[:10])
+        for st in views:
+            prof = st.profile()
+            assert prof.shape == (129,) and np.all(prof > 0)
+    finally:
+        for st in views[1:]:
+            st.close()
+        base.close()
+
+
+def test_full_stream_bit_exact(engine):
+    _check_modes(engine, chain=False, weight_seed=7)
+
+
+def test_chained_stream_bit_exact(engine):
+    _check_modes(engine, chain=True, weight_seed=11)
+
+
+def test_chained_fences_derived(engine):
+    """With fences from buffers, every site of the chain after the first
+    waits for the one before it: through the stamped words of the output it
+    reads where that is its one dependence, else (the swiglu sites, whose
+    EMUL32 reads two outputs) for the whole GPU.  With FENCE_ALL every site
+    waits for the whole GPU; the independent-input stream waits for
+    nothing."""
+    st = stream9b.Stream9B(engine, seed=3, chain=True, mode=N.PLAN_PERSISTENT,
+                           fences=N.FENCE_AUTO)
+    try:
+        fenced = st.plan.fenced()
+        want = [N.WAIT_NONE] + [N.WAIT_GRID if s.name.endswith(".swiglu") else N.WAIT_INPUT
+                                for s in st.sites[1:]]
+        assert fenced == want, fenced
+        st.plan.set_fences(N.FENCE_ALL)
+        assert st.plan.fenced() == [N.WAIT_NONE] + [N.WAIT_GRID] * (len(st.sites) - 1)
+    finally:
+        st.close()
+    st = stream9b.Stream9B(engine, seed=3, mode=N.PLAN_PERSISTENT, fences=N.FENCE_AUTO)
+    try:
+        assert st.plan.fenced() == [N.WAIT_NONE] * len(st.sites)
     finally:
         st.close()
