@@ -1039,9 +1039,34 @@ static bool ranges_meet(const std::vector<ByteRange> &a, const std::vector<ByteR
 // when it is the only write site i's x meets among sites from..i-1 and x
 // starts at an even row: (j, job, first word), else j = -1.
 struct StampSrc {
-  int site = -1, job = -1;
+  int site = -1, job = -1;   // job kProduct: the site's EMUL32 product words
   int64_t word = 0;
 };
+constexpr int kProduct = -2;
+
+// Site i forms EMUL32(x2, x) of the two outputs of one site j (since
+// `from`): x = job 0's int16 output, x2 = job 1's int32 output, both exactly
+// K rows.  When every workgroup holds the same tiles of both jobs (tiles per
+// job a multiple of the grid G, at most kPairTiles each), site j can form
+// the product itself, and site i reads it through stamped words.
+static StampSrc product_source(const std::vector<GemvParams> &sites, int from, int i, int G) {
+  StampSrc none, got;
+  const GemvParams &C = sites[i];
+  if (C.pro != PRO_EMUL_DYNQ8 || C.K % kTileRows || G < 1) return none;
+  for (int j = from; j < i; ++j) {
+    const GemvParams &P = sites[j];
+    if (P.njobs != 2 || P.job[0].out != C.x || (const void *)P.job[1].out != C.x2) continue;
+    const int T = C.K / kTileRows;
+    if ((P.job[0].epi != EPI_SILU32 && P.job[0].epi != EPI_MOVY_I16) ||
+        P.job[1].epi != EPI_MOVY_P32 || P.job[0].nrows != C.K || P.job[1].nrows != C.K ||
+        P.total_tiles != 2 * T || T % G || T / G > kPairTiles)
+      return none;
+    got.site = j;
+    got.job = kProduct;
+    return got;
+  }
+  return none;
+}
 static StampSrc stamp_source(const std::vector<GemvParams> &sites,
                              const std::vector<std::vector<ByteRange>> &wr, int from, int i) {
   StampSrc none, got;
@@ -1068,6 +1093,11 @@ static StampSrc stamp_source(const std::vector<GemvParams> &sites,
   return none;
 }
 
+// the persistent launch's grid: one workgroup per CU
+static int plan_grid(const w4a8_plan *p) {
+  return p->G > 0 ? p->G : p->ctx->num_cu * stream_max_blocks_per_cu();
+}
+
 // W4A8_FENCE_AUTO: a site waits only when it reads what a site since the
 // last fence writes, or writes what one of those reads or writes -- the
 // reference sequencer's FENCE rule (a result is waited for before it is
@@ -1086,16 +1116,22 @@ static void plan_fences(const w4a8_plan *p, std::vector<GemvParams> &sites,
     bool f = i > 0 && p->fences == W4A8_FENCE_ALL;
     bool meets = false, x_only = true;
     const uintptr_t x0 = (uintptr_t)sites[i].x;
+    bool inputs_only = true;   // ... or its x2 (PRO_EMUL_DYNQ8)
+    const uintptr_t x2 = (uintptr_t)sites[i].x2;
     for (int j = last; j < i && !f; ++j) {
       for (const auto &a : rd[i])
         if (ranges_meet({a}, wr[j])) {
           meets = true;
           x_only = x_only && a.lo == x0;   // the first read range is x
+          inputs_only = inputs_only && (a.lo == x0 || (x2 && a.lo == x2));
         }
-      if (ranges_meet(wr[i], rd[j]) || ranges_meet(wr[i], wr[j])) meets = true, x_only = false;
+      if (ranges_meet(wr[i], rd[j]) || ranges_meet(wr[i], wr[j]))
+        meets = true, x_only = inputs_only = false;
     }
     if (meets && !f) {
       if (x_only) src[i] = stamp_source(sites, wr, last, i);
+      if (src[i].site < 0 && inputs_only)
+        src[i] = product_source(sites, last, i, plan_grid(p));
       f = src[i].site < 0;
     }
     sites[i].fence = f ? 1 : 0;
@@ -1119,7 +1155,7 @@ static int plan_build_persistent(w4a8_plan *p) {
       p->head_site = i;
       p->head_result = p->steps[i].result;
     }
-  p->G = c->num_cu * stream_max_blocks_per_cu();
+  p->G = plan_grid(p);
   std::vector<GemvParams> sites(n);
   // tile t of site s goes to workgroup (off_s + t) mod G: the tiles of
   // consecutive sites continue one round-robin, so every workgroup's share
@@ -1140,14 +1176,17 @@ static int plan_build_persistent(w4a8_plan *p) {
   plan_fences(p, sites, src);
   // stamped words for every output a later site reads through them (one
   // block per (site, job), nrows / 2 words), cleared with the flags
-  std::vector<int64_t> word0(n * kMaxJobs, -1);
+  // (slot kMaxJobs of a site: its EMUL32 product's words)
+  std::vector<int64_t> word0(n * (kMaxJobs + 1), -1);
+  auto slot = [&](const StampSrc &a) { return a.site * (kMaxJobs + 1) +
+                                              (a.job == kProduct ? kMaxJobs : a.job); };
   int64_t words = 0;
   for (int i = 0; i < n; ++i)
     if (src[i].site >= 0) {
-      int64_t &w0 = word0[src[i].site * kMaxJobs + src[i].job];
+      int64_t &w0 = word0[slot(src[i])];
       if (w0 < 0) {
         w0 = words;
-        words += sites[src[i].site].job[src[i].job].nrows / 2;
+        words += (src[i].job == kProduct ? sites[i].K : sites[src[i].site].job[src[i].job].nrows) / 2;
       }
     }
   HIP_TRY(hipMalloc(&p->d_sites, sizeof(GemvParams) * (size_t)n));
@@ -1161,12 +1200,15 @@ static int plan_build_persistent(w4a8_plan *p) {
   if (words > 0) HIP_TRY(hipMalloc(&p->d_stamped, sizeof(uint64_t) * (size_t)words));
   for (int i = 0; i < n; ++i) {
     for (int k = 0; k < sites[i].njobs; ++k) {
-      const int64_t w0 = word0[i * kMaxJobs + k];
+      const int64_t w0 = word0[i * (kMaxJobs + 1) + k];
       sites[i].job[k].stamped = w0 >= 0 ? p->d_stamped + w0 : nullptr;
     }
-    sites[i].x_stamped =
-        src[i].site >= 0 ? p->d_stamped + word0[src[i].site * kMaxJobs + src[i].job] + src[i].word
-                         : nullptr;
+    const int64_t pw0 = word0[i * (kMaxJobs + 1) + kMaxJobs];
+    sites[i].prod_stamped = pw0 >= 0 ? p->d_stamped + pw0 : nullptr;
+    sites[i].x_stamped = src[i].site >= 0 ? p->d_stamped + word0[slot(src[i])] + src[i].word
+                                          : nullptr;
+    // a site reading a product formed by its producer is a DYNQ8 site of it
+    if (src[i].job == kProduct) sites[i].pro = PRO_DYNQ8;
   }
   p->epoch = 0;
   HIP_TRY(hipMemcpy(p->d_sites, sites.data(), sizeof(GemvParams) * (size_t)n,

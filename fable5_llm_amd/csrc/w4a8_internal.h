@@ -130,6 +130,12 @@ struct GemvParams {
                             // written by site stamp_src (x_stamped), instead of after
                             // a grid-wide wait; -1: not
   const uint64_t *x_stamped;  // ... the words holding x[0..K) (K / 2 of them)
+  uint64_t *prod_stamped;   // persistent stream, a site of two int16 / int32 jobs of
+                            // equal rows (a gate and an up projection): the stamped
+                            // words of EMUL32(job 1, job 0; 12), formed as the
+                            // control wavefront stores job 1's tiles (a workgroup
+                            // holds the same tiles of both jobs: tiles per job are a
+                            // multiple of the grid, at most kPairTiles per workgroup)
   int8_t *x8_out;           // optional (written by workgroup 0)
   int32_t *e_x_out;         // optional
   int16_t *xn_out;          // optional RMSNorm output
@@ -154,6 +160,7 @@ hipError_t launch_gemv_timed(const GemvParams &p, int grid, hipStream_t s,
 // registers, 1 control wavefront, 3 prologue wavefronts); a site with
 // `fence` set waits for one completion flag per workgroup.
 constexpr int kStreamNormKMax = 4096;   // RMSNorm sites of a persistent plan
+constexpr int kPairTiles = 8;           // tiles per job and workgroup of a paired site
 struct StreamParams {
   const GemvParams *sites;  // device array, nsites entries
   int32_t nsites;

@@ -84,6 +84,8 @@ struct __align__(16) Lds {
   int32_t wsite[kCW];               // site each weight wavefront works on (nsites: done)
   int32_t gridok;                   // last fenced site whose grid-wide wait has passed
   int32_t served;                   // last site whose outputs the control wavefront stored
+  int16_t pairv[kPairTiles][kTileRows];  // paired site: job 0's outputs of this CU's tiles
+  int16_t prod[kTileRows];          // ... and one tile's EMUL32 products
   int32_t psync[kPW];               // prologue wavefronts' barrier phases
   int32_t abort;                    // set by the first LDS wait that gives up
   int32_t err;                      // error bits found inside the workgroup
@@ -337,6 +339,25 @@ __device__ void ctrl_serve(CSite &P, Lds &L, int kt0, int r, int G, int lane, ui
         }
       }
       L.tv[slot][lane] = 0;
+      if (kDep && P.prod_stamped) {
+        // a paired site: this CU's tiles of job 0 come first (npair of
+        // them), then the same tiles of job 1; ALU EMUL32 at p0 = 12
+        // (gen_layer_script.py:1414-1418) of the two, as job 1's are stored
+        const int npair = P.total_tiles / 2 / G;
+        if (i < npair) {
+          L.pairv[i][lane] = (int16_t)v;
+        } else {
+          const int64_t pr = rshr64(v * (int64_t)L.pairv[i - npair][lane], kEmulP0);
+          L.prod[lane] = (int16_t)clamp64(pr, -32768, 32767);
+        }
+      }
+    }
+    if (kDep && P.prod_stamped && i >= P.total_tiles / 2 / G && lane < kTileRows / 2) {
+      wait_lds();
+      const int row = (t - J.tile0) * kTileRows + 2 * lane;
+      const uint32_t lo = (uint32_t)(uint16_t)L.prod[2 * lane];
+      const uint32_t hi = (uint32_t)(uint16_t)L.prod[2 * lane + 1];
+      store_coherent(P.prod_stamped + row / 2, (uint64_t)(lo | (hi << 16)) | ((uint64_t)stamp << 32));
     }
     if (lane == 0) {
       lds_write_i32(&L.tcnt[slot], 0);

@@ -76,17 +76,19 @@ def test_chained_stream_bit_exact(engine):
 
 def test_chained_fences_derived(engine):
     """With fences from buffers, every site of the chain after the first
-    waits for the one before it: through the stamped words of the output it
-    reads where that is its one dependence, else (the swiglu sites, whose
-    EMUL32 reads two outputs) for the whole GPU.  With FENCE_ALL every site
-    waits for the whole GPU; the independent-input stream waits for
-    nothing."""
+    waits for the one before it, through the stamped words of what it
+    reads: the output it reads, or for a swiglu site the EMUL32 product
+    that its ln2 site forms when every workgroup holds the same gate and up
+    tiles (12288 / 16 tiles a multiple of the grid), else the whole GPU.
+    With FENCE_ALL every site waits for the whole GPU; the independent-input
+    stream waits for nothing."""
     st = stream9b.Stream9B(engine, seed=3, chain=True, mode=N.PLAN_PERSISTENT,
                            fences=N.FENCE_AUTO)
     try:
         fenced = st.plan.fenced()
-        want = [N.WAIT_NONE] + [N.WAIT_GRID if s.name.endswith(".swiglu") else N.WAIT_INPUT
-                                for s in st.sites[1:]]
+        paired = (stream9b.FFN // 16) % engine.grid == 0
+        want = [N.WAIT_NONE] + [N.WAIT_GRID if s.name.endswith(".swiglu") and not paired
+                                else N.WAIT_INPUT for s in st.sites[1:]]
         assert fenced == want, fenced
         st.plan.set_fences(N.FENCE_ALL)
         assert st.plan.fenced() == [N.WAIT_NONE] + [N.WAIT_GRID] * (len(st.sites) - 1)
