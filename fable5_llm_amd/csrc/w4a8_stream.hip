@@ -539,6 +539,34 @@ __device__ __forceinline__ void put_corr(int8_t *base, int i, int32_t v) {
   else store_coherent(&xlo[i], v);
 }
 
+// Packed 16-bit helpers for the prologue: two int16 of a 32-bit word per
+// instruction (v_pk_* integer operations; exact integer arithmetic).
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// |v| of both int16 of w, as uint16 (|-32768| = 32768)
+__device__ __forceinline__ u16x2 abs2(int32_t w) {
+  const u16x2 u = __builtin_bit_cast(u16x2, w);
+  const u16x2 n = (u16x2)(0) - u;
+  return __builtin_bit_cast(
+      u16x2, __builtin_elementwise_max(__builtin_bit_cast(s16x2, u), __builtin_bit_cast(s16x2, n)));
+}
+
+// DYNQ8 of both int16 of w at exponent e (half = (1 << e) >> 1, e <= 9):
+// clip(rshift_round(v, e), -127, 127) in each 16-bit half (its low byte is
+// the int8)
+__device__ __forceinline__ uint32_t dynq2(int32_t w, u16x2 half, u16x2 e2) {
+  u16x2 q = (abs2(w) + half) >> e2;   // <= 32768 + 256: no wrap
+  q = __builtin_elementwise_min(q, (u16x2)(127));
+  const u16x2 sgn = __builtin_bit_cast(u16x2, __builtin_bit_cast(s16x2, w) >> (s16x2)(15));
+  return __builtin_bit_cast(uint32_t, (q ^ sgn) - sgn);
+}
+
+// the low bytes of the four int16 in (a, b) as one word: a.lo, a.hi, b.lo, b.hi
+__device__ __forceinline__ uint32_t pack4(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x06040200u);
+}
+
 // The prologue of site P by the 3 prologue wavefronts (pw = 0..2; ps is
 // their barrier) from the inputs in X: x8 and the offset corrections into
 // `out` (put_x8 / put_corr), and, when `exports`, the site's exports (x8, e_x, the RMSNorm
@@ -596,15 +624,18 @@ __device__ __forceinline__ int group_prologue(CSite &P, Lds &L, int8_t *out, boo
   if (P.pro == PRO_RMSNORM_DYNQ8) {
     // layer_fixed.py:1262-1278 in sign-magnitude form (rshift_round rounds
     // the magnitude); K <= kStreamNormKMax
+    // sum of squares: a pair's a^2 + b^2 <= 2^31 is exact as a uint32
     uint64_t ss = 0;
 #pragma unroll
     for (int c = 0; c < kPN; ++c)
-      if ((c * kPW + pw) * kChunk < K)
+      if ((c * kPW + pw) * kChunk < K) {
+        const int32_t wd[4] = {X.pc[c].x, X.pc[c].y, X.pc[c].z, X.pc[c].w};
 #pragma unroll
-        for (int j = 0; j < 8; j += 2) {
-          const int32_t a = piece_get(X.pc[c], j), b = piece_get(X.pc[c], j + 1);
-          ss += (uint64_t)((uint32_t)(a * a) + (uint32_t)(b * b));
+        for (int j = 0; j < 4; ++j) {
+          const s16x2 v = __builtin_bit_cast(s16x2, wd[j]);
+          ss += (uint32_t)__builtin_amdgcn_sdot2(v, v, 0, false);
         }
+      }
     ss = wave_sum_u64(ss);
     if (lane == 0) L.pss[pw] = (int64_t)ss;
     psync(L, ps, pw, lane);
@@ -617,14 +648,22 @@ __device__ __forceinline__ int group_prologue(CSite &P, Lds &L, int8_t *out, boo
     rsqrt_q(ss, 2 * P.in_f + (31 - __clz(K)), L.rsqrt, &r, &e);
     const int s1 = 30 - e;
     const int32_t one = P.one_plus ? (1 << 14) : 0;
-    const int rs = s1 < 0 ? 0 : (s1 > 63 ? 63 : s1);
-    const int ls = s1 < 0 ? (-s1 > 63 ? 63 : -s1) : 0;
-    const uint64_t half1 = rs > 0 ? ((uint64_t)1 << (rs - 1)) : 0;
-    const bool right = s1 >= 0;
-    // r < 2^31 (a Q30 reciprocal square root), |x| <= 2^15; for in_f within
-    // 0..40 (checked on the host) the left shift is at most 17, so |x| * r
-    // shifted stays below 2^63
-    const uint32_t r32 = (uint32_t)r;
+    // In double precision, exactly (doubles hold integers below 2^53, and
+    // these operations round nothing below that):
+    //   m = |x| * r < 2^15 * 2^31; rshift_round of a magnitude by s > 0 is
+    //   floor(m * 2^-s + 1/2) (m * 2^-s + 1/2 < 2^52 has no bits below
+    //   2^-s), a shift by s <= 0 is m * 2^-s, which may round above 2^53 --
+    //   but y is then clipped to 2^32 - 1 (rounding keeps it >= 2^32), and
+    //   below 2^32 it is exact (in_f within 0..40 is checked on the host, so
+    //   the left shift is at most 17);
+    //   q = (y * |w + one| + 8192) >> 14 = floor(y * |w + one| * 2^-14 + 1/2),
+    //   y * |w + one| < 2^32 * 2^16.
+    // A magnitude of 2^32 or more saturates the int16 result for any nonzero
+    // scale exactly as 2^32 - 1 does, hence the clip of y.
+    const double dr = (double)(uint32_t)r;
+    const double dscale = s1 >= 0 ? __builtin_ldexp(1.0, -min(s1, 63))
+                                  : __builtin_ldexp(1.0, min(-s1, 63));
+    const double dhalf = s1 > 0 ? 0.5 : 0.0;
 #pragma unroll
     for (int c = 0; c < kPN; ++c) {
       const int base = (c * kPW + pw) * kChunk + lane * 8;
@@ -633,28 +672,29 @@ __device__ __forceinline__ int group_prologue(CSite &P, Lds &L, int8_t *out, boo
         for (int j = 0; j < 8; ++j) {
           const int32_t xv = piece_get(X.pc[c], j);
           const int32_t sc = (int32_t)piece_get(X.wv[c], j) + one;
-          const uint64_t mag = (uint64_t)(uint32_t)abs(xv) * (uint64_t)r32;
-          uint64_t ym = right ? ((mag + half1) >> rs) : (mag << ls);
-          // y is clipped to [-2^32, 2^32 - 1]; a magnitude of 2^32 or more
-          // saturates the int16 result below for any nonzero scale, exactly
-          // as 2^32 - 1 does, so the product can be formed in 32 x 32 bits
-          ym = ym < 0xFFFFFFFFull ? ym : 0xFFFFFFFFull;
-          const uint64_t q = ((uint64_t)(uint32_t)ym * (uint64_t)(uint32_t)abs(sc) + 8192u) >> 14;
+          const double m = __builtin_fabs((double)xv) * dr;
+          const double y = __builtin_fmin(__builtin_floor(__builtin_fma(m, dscale, dhalf)),
+                                          4294967295.0);
+          const double w14 = (double)abs(sc) * 0x1p-14;
+          const double qd = __builtin_fmin(__builtin_floor(__builtin_fma(y, w14, 0.5)), 65535.0);
           const bool neg = (xv < 0) != (sc < 0);
-          const int32_t q32 = q > 65535u ? 65535 : (int32_t)q;
-          const int32_t qm = min(q32, 32767 + (int32_t)neg);
+          const int32_t qm = min((int32_t)qd, 32767 + (int32_t)neg);
           piece_set(X.pc[c], j, (int16_t)(neg ? -qm : qm));
         }
         if (exports && P.xn_out && base < K) *(int4 *)(P.xn_out + base) = X.pc[c];
       }
     }
   }
-  int32_t mx = 0;
+  u16x2 mx2 = (u16x2)(0);
 #pragma unroll
   for (int c = 0; c < kPC; ++c)
-    if ((c * kPW + pw) * kChunk < K)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) mx = max(mx, abs((int32_t)piece_get(X.pc[c], j)));
+    if ((c * kPW + pw) * kChunk < K) {
+      mx2 = __builtin_elementwise_max(mx2, abs2(X.pc[c].x));
+      mx2 = __builtin_elementwise_max(mx2, abs2(X.pc[c].y));
+      mx2 = __builtin_elementwise_max(mx2, abs2(X.pc[c].z));
+      mx2 = __builtin_elementwise_max(mx2, abs2(X.pc[c].w));
+    }
+  int32_t mx = max((int32_t)mx2.x, (int32_t)mx2.y);
   mx = wave_max_i32(mx);
   if (lane == 0) L.pmx[pw] = mx;
   psync(L, ps, pw, lane);
@@ -665,20 +705,14 @@ __device__ __forceinline__ int group_prologue(CSite &P, Lds &L, int8_t *out, boo
   // bitlen(max) - 7, or one more when rounding carries past 127
   int e = mx > 127 ? 25 - __clz(mx) : 0;
   if (e > 0 && ((mx + (1 << (e - 1))) >> e) > 127) ++e;
-  const int32_t half = (1 << e) >> 1;
+  const u16x2 half2 = (u16x2)((unsigned short)((1 << e) >> 1));
+  const u16x2 e2 = (u16x2)((unsigned short)e);
 #pragma unroll
   for (int c = 0; c < kPC; ++c) {
     const int base = (c * kPW + pw) * kChunk + lane * 8;
     if ((c * kPW + pw) * kChunk < K) {
-      uint32_t lo = 0, hi = 0;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int32_t v = piece_get(X.pc[c], j);
-        const int32_t qm = min((abs(v) + half) >> e, 127);
-        const uint32_t b8 = (uint32_t)(uint8_t)(int8_t)(v < 0 ? -qm : qm);
-        if (j < 4) lo |= b8 << (8 * j);
-        else       hi |= b8 << (8 * (j - 4));
-      }
+      const uint32_t lo = pack4(dynq2(X.pc[c].x, half2, e2), dynq2(X.pc[c].y, half2, e2));
+      const uint32_t hi = pack4(dynq2(X.pc[c].z, half2, e2), dynq2(X.pc[c].w, half2, e2));
       // -8 * sum of the x8 met by the offset-form low nibbles of one
       // (group, quarter): 32 consecutive elements = the 4 lanes of a DPP quad
       int t4 = __builtin_amdgcn_sdot4((int)lo, 0x01010101, 0, false);
