@@ -401,6 +401,143 @@ def chained_leg(ctx, stream, args):
     return st, out
 
 
+def c0_leg(ctx, stream, args, copies=64):
+    """C0 (one 4096 x 4096 W4A8 matvec: DYNQ8 of an N(0,1) Q8.7 vector with
+    1 % outliers, MOVY int16 out) over `copies` distinct resident matrices,
+    8,650,752 B each (553 MB in all, beyond the 256 MB Infinity Cache, so
+    every launch reads cold weights), back to back: replayed as a HIP graph
+    of one GEMV launch per matrix, and as one persistent launch of all of
+    them.  Per-matrix kernel times are dispatch-recorded events around each
+    launch of an eagerly submitted pass.  Every output is kept for the
+    oracle check."""
+    import numpy as np
+    import torch
+    from fable5_llm_amd import _native as N
+    from fable5_llm_amd import stream9b as S
+    from fable5_llm_amd.engine import Plan
+    dev = torch.device("cuda", ctx.device)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed + 11)
+    K = nrows = S.H
+    m = S.Mat("c0", nrows, K, S.RS_F, N.EPI_MOVY_I16)
+    x = S.synth_x16(gen, K, S.RS_F)
+    plan = Plan(ctx)
+    ws, outs = [], []
+    for _ in range(copies):
+        img = S.synth_image(gen, nrows, K)
+        torch.cuda.synchronize(dev)
+        ws.append(ctx.upload(img, nrows, K, S.sh_for_k(K)))
+        outs.append(torch.zeros(nrows, dtype=torch.int16, device=dev))
+        plan.add_site([ws[-1]], [m.epi], [m.p0(S.RS_F)], [outs[-1]], x, prologue=N.PRO_DYNQ8)
+    ctx.sync()
+
+    class _P:   # what time_steps needs of a stream
+        pass
+    st = _P()
+    st.run, st.plan, st.profile = plan.run, plan, plan.profile
+    out = {"matrix": "4096x4096", "copies": copies, "bytes_per_matrix": m.bytes,
+           "bytes_resident": m.bytes * copies}
+    for name, mode in (("graph", N.PLAN_GRAPH), ("persistent", N.PLAN_PERSISTENT)):
+        plan.set_mode(mode)
+        plan.set_fences(N.FENCE_AUTO)
+        tm = time_steps(st, ctx, stream, max(10, args.steps), args.warmup)
+        us = tm["ms_per_step"] * 1e3 / copies
+        leg = {"us_per_matrix": round(us, 3), "value": round(m.bytes / (us * 1e-6) / 1e9, 1),
+               "unit": "GB/s", "pct_of_peak_hbm": round(100 * m.bytes / (us * 1e-6) / 1e9 /
+                                                        PEAK_HBM_GBS, 1)}
+        if name == "graph":
+            per = np.array([plan.profile() for _ in range(5)]).reshape(-1) * 1e3
+            leg["kernel_us_p10_p50_p90"] = [round(float(np.percentile(per, q)), 3)
+                                            for q in (10, 50, 90)]
+            leg["kernel_value"] = round(float(m.bytes / (np.median(per) * 1e-6) / 1e9), 1)
+            leg["note"] = ("one gemv_kernel launch per matrix in a HIP graph; us_per_matrix "
+                           "includes the launch gaps, kernel_us_* are the launches alone")
+        else:
+            leg["note"] = "all copies in one stream_kernel launch (no site waits)"
+        out[name] = leg
+    ctx.sync()
+    keep = (x.cpu().numpy(), [np.frombuffer(w.download(), dtype=np.uint8) for w in ws[:8]],
+            [o.cpu().numpy() for o in outs[:8]], m.p0(S.RS_F))
+    plan.close()
+    for w in ws:
+        w.free()
+    return out, keep
+
+
+def c0_check(keep):
+    """The C0 leg's first 8 outputs against the oracle."""
+    import numpy as np
+    from oracle import cfast, law
+    x16, imgs, outs, p0 = keep
+    x8, e = law.dyn_quant_i8(x16)
+    bad = 0
+    for img, o in zip(imgs, outs):
+        y = cfast.matvec_y32_img(img, 4096, 4096, 7, x8, 0)
+        bad += int(not np.array_equal(o.astype(np.int64),
+                                      np.asarray(law.movy(y, p0 - e, law.MOVY_INT16), np.int64)))
+    return "bit-exact" if bad == 0 else f"MISMATCH in {bad} matrices"
+
+
+def read_ceiling_leg(ctx, gib=4, launches=20):
+    """The measured HBM read ceiling: a plain read of `gib` GiB with the
+    weight stream's 16-byte non-temporal loads (w4a8_read_ceiling), at a few
+    grid sizes; the best median is reported."""
+    import numpy as np
+    import torch
+    buf = torch.empty(gib << 30, dtype=torch.uint8, device=torch.device("cuda", ctx.device))
+    best = None
+    for per_cu in (4, 8, 16):
+        ms, nbytes = ctx.read_ceiling(buf, launches, grid=per_cu * ctx.num_cu)
+        ms, nbytes = ctx.read_ceiling(buf, launches, grid=per_cu * ctx.num_cu)   # warm
+        gbs = nbytes / (float(np.median(ms)) * 1e-3) / 1e9
+        if best is None or gbs > best["value"]:
+            best = {"value": round(gbs, 1), "unit": "GB/s", "bytes": nbytes,
+                    "grid": per_cu * ctx.num_cu, "pct_of_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 1),
+                    "kernel": "read_kernel (16-byte non-temporal loads, XOR-folded)"}
+    del buf
+    return best
+
+
+def cpu_per_config(st, host):
+    """CPU baselines per configuration, on the stream's own matrices: C0 one
+    4096 x 4096 (layer 0's in_z), C1 the FFN set (layer 0's gate and up,
+    12288 x 4096, and down, 4096 x 12288), C2 the 248,320-row head.  Each by
+    the C oracle with OpenMP on every host core (repeated for >= 0.5 s) and
+    by the numpy restatement on one thread (once)."""
+    import numpy as np
+    from fable5_llm_amd.stream9b import sh_for_k
+    from oracle import cfast, law
+    def find(name):
+        for si, s in enumerate(st.sites):
+            for mi, m in enumerate(s.mats):
+                if m.name == name:
+                    return m, host[si]["imgs"][mi]
+        raise KeyError(name)
+    rng = np.random.default_rng(5)
+    cfgs = {"C0": [find("L0.in_z")], "C1": [find("L0.gate"), find("L0.up"), find("L0.down")],
+            "C2": [find("lm_head")]}
+    out = {}
+    for c, mats in cfgs.items():
+        xs = {m.K: rng.integers(-127, 128, m.K).astype(np.int8) for m, _ in mats}
+        nbytes = sum(m.bytes for m, _ in mats)
+        n, t = 0, 0.0
+        while t < 0.5:
+            t0 = time.perf_counter()
+            for m, img in mats:
+                cfast.matvec_y32_img(img, m.nrows, m.K, sh_for_k(m.K), xs[m.K], 0)
+            t += time.perf_counter() - t0
+            n += 1
+        t0 = time.perf_counter()
+        for m, img in mats:
+            law.matvec_y32_image(img.tobytes(), m.nrows, m.K, sh_for_k(m.K), xs[m.K])
+        tn = time.perf_counter() - t0
+        out[c] = {"bytes": nbytes,
+                  "c_openmp": {"ms": round(t / n * 1e3, 3),
+                               "gbs": round(nbytes * n / t / 1e9, 2), "cores": cfast.num_threads()},
+                  "numpy_1thread": {"ms": round(tn * 1e3, 1), "gbs": round(nbytes / tn / 1e9, 4)}}
+    return out
+
+
 def chain_check(st):
     """The chained stream's last run against the oracle run site after site
     (each site fed from the oracle's own output of its producer)."""
@@ -426,6 +563,7 @@ def cpu_baseline(st, min_seconds, keep=(), keep_ffn=None, keep_head=None):
         passes += 1
     bad = sc.compare(st, host, ref)
     ys = [r["ys"] for r in ref]
+    per_config = cpu_per_config(st, host)
     # single-threaded numpy restatement on one 4096 x 4096 matrix (sample)
     from oracle import law
     s0 = st.sites[1]
@@ -451,6 +589,7 @@ def cpu_baseline(st, min_seconds, keep=(), keep_ffn=None, keep_head=None):
         "batched_parity": batched_check(st, keep) if keep else None,
         "ffn_parity": ffn_check(st, keep_ffn) if keep_ffn else None,
         "head_parity": head_check(ys, keep_head) if keep_head else None,
+        "per_config": per_config,
     }
 
 
@@ -481,6 +620,8 @@ def main():
                          "or only where it shares a buffer with one")
     ap.add_argument("--no-ordered", action="store_true",
                     help="skip timing the same plan strictly in order (graph mode)")
+    ap.add_argument("--no-c0", action="store_true",
+                    help="skip the C0 leg (4096x4096 over 64 cold copies) and the read ceiling")
     ap.add_argument("--no-chain", action="store_true",
                     help="skip the chained decode step (every site reads an earlier "
                          "site's output)")
@@ -552,6 +693,12 @@ def main():
                     "the previous one completes; one gemv_kernel launch per site"}
         st.plan.set_mode(mode)
 
+    c0 = keep_c0 = None
+    if not args.no_c0:
+        log("C0 leg: 4096x4096 over 64 cold copies")
+        c0, keep_c0 = c0_leg(ctx, stream, args)
+        log("read ceiling")
+        line_ceiling = read_ceiling_leg(ctx)
     chained = stc = None
     if not args.no_chain:
         log("chained step")
@@ -620,6 +767,10 @@ def main():
     }
     if ordered:
         line["ordered"] = ordered
+    if c0:
+        line["c0"] = c0
+        line["read_ceiling"] = line_ceiling
+        line["roofline"]["frac_of_read_ceiling"] = round(achieved / line_ceiling["value"], 4)
     if chained:
         # what each fence adds over the independent-input step, same mode
         if persistent:
@@ -648,11 +799,15 @@ def main():
         if stc is not None:
             log("chained parity")
             chained["parity"] = chain_check(stc)
+        if keep_c0 is not None:
+            c0["parity"] = c0_check(keep_c0)
     if stc is not None:
         stc.close()
     st.close()
     ctx.close()
-    print(json.dumps(line), flush=True)
+    def plain(o):   # numpy scalars and arrays in the line
+        return o.item() if hasattr(o, "item") and getattr(o, "size", 1) == 1 else o.tolist()
+    print(json.dumps(line, default=plain), flush=True)
 
 
 if __name__ == "__main__":

@@ -35,6 +35,7 @@ SIGNATURES = {
     "w4a8_ctx_info": [_P, _P, _P],
     "w4a8_ctx_set_grid": [_P, _I32],
     "w4a8_tables": [_P, _P, _P],
+    "w4a8_read_ceiling": [_P, _P, _I64, _I32, _I32, _P],
     "w4a8_weights_upload": [_P, _P, _I64, _I32, _I32, ctypes.POINTER(_P)],
     "w4a8_weights_upload_async": [_P, _P, _I64, _I32, _I32, ctypes.POINTER(_P)],
     "w4a8_weights_download": [_P, _P, _P],

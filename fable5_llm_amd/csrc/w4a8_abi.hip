@@ -395,6 +395,32 @@ int w4a8_ctx_info(const w4a8_ctx *c, int32_t *num_cu, int32_t *grid) {
   return W4A8_OK;
 }
 
+int w4a8_read_ceiling(w4a8_ctx *c, const void *d_buf, int64_t nbytes, int32_t grid, int32_t n,
+                      float *ms) {
+  if (!c || !d_buf || !ms || n < 1 || nbytes < 16 || nbytes % 16 || grid < 0)
+    return fail(W4A8_E_ARG, "w4a8_read_ceiling: bad argument");
+  DeviceGuard g(c->device);
+  if (grid == 0) grid = 8 * c->num_cu;
+  uint32_t *sink = nullptr;
+  HIP_TRY(hipMalloc(&sink, sizeof(uint32_t) * (size_t)grid));
+  std::vector<hipEvent_t> ev(2 * (size_t)n, nullptr);
+  int rc = W4A8_OK;
+  for (auto &e : ev)
+    if (!rc && hipEventCreate(&e) != hipSuccess) rc = fail(W4A8_E_HIP, "hipEventCreate");
+  for (int i = 0; !rc && i < n; ++i)
+    if (launch_read(d_buf, nbytes, sink, grid, c->stream, ev[2 * i], ev[2 * i + 1]) !=
+        hipSuccess)
+      rc = fail(W4A8_E_HIP, "read_kernel launch");
+  if (!rc && hipStreamSynchronize(c->stream) != hipSuccess) rc = fail(W4A8_E_HIP, "sync");
+  for (int i = 0; !rc && i < n; ++i)
+    if (hipEventElapsedTime(&ms[i], ev[2 * i], ev[2 * i + 1]) != hipSuccess)
+      rc = fail(W4A8_E_HIP, "hipEventElapsedTime");
+  for (auto &e : ev)
+    if (e) (void)hipEventDestroy(e);
+  (void)hipFree(sink);
+  return rc;
+}
+
 int w4a8_ctx_set_grid(w4a8_ctx *c, int32_t grid) {
   if (!c || grid < 0) return fail(W4A8_E_ARG, "bad ctx/grid");
   c->grid_override = grid;

@@ -147,6 +147,10 @@ struct GemvParams {
 
 // launchers (all asynchronous on `s`)
 hipError_t launch_fill_i32(int32_t *p, int32_t v, int64_t n, hipStream_t s);
+// reads nbytes (a multiple of 16) of buf once; sink: grid words.  start /
+// stop (optional) are recorded by the dispatch itself
+hipError_t launch_read(const void *buf, int64_t nbytes, uint32_t *sink, int grid,
+                       hipStream_t s, hipEvent_t start, hipEvent_t stop);
 hipError_t launch_repack(const uint8_t *img, int64_t nrows, const Layout &L,
                          int64_t stride, uint8_t *dst, hipStream_t s);
 hipError_t launch_unpack(const uint8_t *src, int64_t nrows, const Layout &L,

@@ -681,6 +681,41 @@ static int blocks_for(int64_t n, int threads, int cap) {
   return (int)(b > cap ? cap : b);
 }
 
+// The HBM read ceiling: every 16-byte piece of buf read once with
+// non-temporal loads (the weight stream's access), XOR-folded so that no
+// load can be dropped, one word per workgroup into sink.  Grid-stride, each
+// thread keeping 8 loads in flight.
+__global__ __launch_bounds__(256) void read_kernel(const uint4 *__restrict__ buf, int64_t n16,
+                                                   uint32_t *__restrict__ sink) {
+  const int64_t stride = (int64_t)gridDim.x * 256 * 8;
+  uint32_t acc = 0;
+  for (int64_t base = (int64_t)blockIdx.x * 256 * 8 + threadIdx.x; base < n16; base += stride) {
+    uint4 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int64_t i = base + (int64_t)k * 256;
+      v[k] = i < n16 ? ldg16_nt((const uint8_t *)(buf + i)) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+  }
+  __shared__ uint32_t red[256];
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t a = 0;
+    for (int i = 0; i < 256; ++i) a ^= red[i];
+    sink[blockIdx.x] = a;
+  }
+}
+
+hipError_t launch_read(const void *buf, int64_t nbytes, uint32_t *sink, int grid,
+                       hipStream_t s, hipEvent_t start, hipEvent_t stop) {
+  hipExtLaunchKernelGGL(read_kernel, dim3(grid), dim3(256), 0, s, start, stop, 0,
+                        (const uint4 *)buf, nbytes / 16, sink);
+  return hipGetLastError();
+}
+
 hipError_t launch_fill_i32(int32_t *p, int32_t v, int64_t n, hipStream_t s) {
   hipLaunchKernelGGL(fill_i32_kernel, dim3(blocks_for(n, 256, 4096)), dim3(256),
                      0, s, p, v, n);

@@ -132,6 +132,16 @@ class Context:
         N.check(N.lib().w4a8_tables(self.h, _ptr(r), _ptr(s)))
         return r, s
 
+    def read_ceiling(self, buf, n, grid=0):
+        """Kernel ms of each of n launches reading the device tensor `buf`
+        once (16-byte non-temporal loads): the measured HBM read ceiling."""
+        _dev(buf, 16, "buf")
+        nbytes = (buf.numel() * buf.element_size()) // 16 * 16
+        ms = np.zeros(n, dtype=np.float32)
+        N.check(N.lib().w4a8_read_ceiling(self.h, _dptr(buf), nbytes, int(grid), int(n),
+                                          _ptr(ms)), "read_ceiling")
+        return ms, nbytes
+
     # ------------------------------------------------------------ weights
     def upload(self, img, nrows, K, sh):
         """img: row image (bytes / uint8 array on the host, or a uint8 torch

@@ -88,6 +88,14 @@ int w4a8_ctx_set_grid(w4a8_ctx *ctx, int32_t grid);
    uses: fixedpoint.py:42-53 and 128-142 (ROMs roms/rsqrt_rom.hex,
    roms/sigmoid_rom.hex) */
 int w4a8_tables(w4a8_ctx *ctx, int32_t *rsqrt512, int32_t *sigmoid257);
+/* no counterpart in the reference: the measured HBM read ceiling the
+   kernels' roofline fractions can be read against -- n launches, each
+   reading the nbytes (a multiple of 16, >= 16) at d_buf once with the
+   weight stream's 16-byte non-temporal loads over `grid` workgroups of 256
+   threads (0: 8 per CU); ms[i] = kernel time of launch i (dispatch-recorded
+   events).  Synchronous. */
+int w4a8_read_ceiling(w4a8_ctx *ctx, const void *d_buf, int64_t nbytes, int32_t grid,
+                      int32_t n, float *ms);
 
 /* ---- weights (replaces the DDR weight image + WBASE/WBEATS/SHAPE CSRs,
  *      w4a8_ref.py:349-370, matvec_chan.sv:12-49) ----------------------- */
