@@ -34,6 +34,7 @@ SIGNATURES = {
     "w4a8_ctx_sync": [_P],
     "w4a8_ctx_info": [_P, _P, _P],
     "w4a8_ctx_set_grid": [_P, _I32],
+    "w4a8_ctx_set_spin_limit": [_P, ctypes.c_uint32, ctypes.c_uint32],
     "w4a8_tables": [_P, _P, _P],
     "w4a8_read_ceiling": [_P, _P, _I64, _I32, _I32, _P],
     "w4a8_weights_upload": [_P, _P, _I64, _I32, _I32, ctypes.POINTER(_P)],

@@ -33,6 +33,7 @@ struct w4a8_ctx {
   size_t chain_cap = 0;
   int32_t *d_topk_flags = nullptr;   // TOPK-32 look-back flags (kTopkFlagWords)
   int32_t topk_epoch = 0;            // epoch of the last TOPK-32 launch
+  uint32_t spin_grid = 0, spin_lds = 0;   // polls before bounded waits give up (0: defaults)
   int32_t h_tables[kTableLen];
 };
 
@@ -419,6 +420,13 @@ int w4a8_read_ceiling(w4a8_ctx *c, const void *d_buf, int64_t nbytes, int32_t gr
     if (e) (void)hipEventDestroy(e);
   (void)hipFree(sink);
   return rc;
+}
+
+int w4a8_ctx_set_spin_limit(w4a8_ctx *c, uint32_t grid_polls, uint32_t lds_polls) {
+  if (!c) return fail(W4A8_E_ARG, "null ctx");
+  c->spin_grid = grid_polls;
+  c->spin_lds = lds_polls;
+  return W4A8_OK;
 }
 
 int w4a8_ctx_set_grid(w4a8_ctx *c, int32_t grid) {
@@ -838,7 +846,8 @@ static int topk_launch(w4a8_ctx *c, const int32_t *d_y, int64_t n, void *scratch
     c->topk_epoch = 0;
   }
   const int32_t epoch = ++c->topk_epoch;
-  HIP_TRY(launch_topk32(d_y, n, scratch, c->d_topk_flags, epoch, d_out, c->d_err, c->stream));
+  HIP_TRY(launch_topk32(d_y, n, scratch, c->d_topk_flags, epoch, d_out, c->d_err, c->stream,
+                        c->spin_grid));
   // a captured launch replays this epoch with its own clear; the next eager
   // launch clears the flags first
   if (cs != hipStreamCaptureStatusNone) c->topk_epoch = 0;
@@ -1269,6 +1278,8 @@ static int plan_launch_persistent(w4a8_plan *p, hipStream_t s, hipEvent_t e0,
   sp.err = p->ctx->d_err;
   sp.result = p->head_result;
   sp.trace = trace;
+  sp.grid_spin = p->ctx->spin_grid;
+  sp.lds_spin = p->ctx->spin_lds;
   HIP_TRY(launch_stream(sp, p->G, s, p->mode == W4A8_PLAN_PERSISTENT_COOP, p->dependent, e0,
                         e1));
   // A captured launch replays this epoch with its own fill; the memory holds

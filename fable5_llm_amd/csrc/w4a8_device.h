@@ -189,9 +189,10 @@ __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)"
 constexpr uint32_t kLdsSpin = 1u << 20;   // polls before an LDS wait gives up
 
 // the wavefront waits until the LDS word at p is at least v; false if it
-// gave up after kLdsSpin polls
-__device__ __forceinline__ bool lds_wait_ge(const int32_t *p, int32_t v) {
-  for (uint32_t n = 0; n < kLdsSpin; ++n) {
+// gave up after `spin` polls
+__device__ __forceinline__ bool lds_wait_ge(const int32_t *p, int32_t v,
+                                            uint32_t spin = kLdsSpin) {
+  for (uint32_t n = 0; n < spin; ++n) {
     if (lds_read_i32(p) >= v) return true;
     __builtin_amdgcn_s_sleep(1);
   }

@@ -185,6 +185,9 @@ struct StreamParams {
                             // workgroup that arrives last
   uint64_t *trace;          // optional: nsites + 1 wall-clock stamps taken by
                             // workgroup 0 as it starts each site, and at its end
+  uint32_t grid_spin;       // polls before a wait for other workgroups gives up
+                            // (err bit 1); 0: the kernel's default
+  uint32_t lds_spin;        // ... a wait within the workgroup (err bit 2); 0: default
 };
 // one workgroup per CU; `cooperative`: through the cooperative launch API.
 // `dependent`: the kernel built for plans with dependent sites (any site
@@ -227,7 +230,8 @@ constexpr int kTopkFlagWords = 2 * kTopkMaxChunks + kTopkMaxChunks / kTopkSuper;
 constexpr int32_t kTopkEpochMax = 1 << 29;
 size_t topk_scratch_bytes(int64_t n);
 hipError_t launch_topk32(const int32_t *y, int64_t n, void *scratch, int32_t *flags,
-                         int32_t epoch, int32_t *out, int32_t *err, hipStream_t s);
+                         int32_t epoch, int32_t *out, int32_t *err, hipStream_t s,
+                         uint32_t spin = 0);   // polls before a wait gives up; 0: default
 // MOVX: int8 values in int16 words -> x window, tail to a 4-byte word
 // zeroed; bit 4 of err for a value outside int8
 hipError_t launch_movx(const int16_t *src, int64_t n, int8_t *dst, int32_t *err,

@@ -145,14 +145,15 @@ __device__ __forceinline__ void lds_barrier() {
 // after which no wait of the workgroup polls again, so a launch always
 // drains quickly.
 template <bool kAtLeast = false>
-__device__ __forceinline__ void lds_wait_eq(Lds &L, const int32_t *p, int v, int lane) {
+__device__ __forceinline__ void lds_wait_eq(Lds &L, const int32_t *p, int v, int lane,
+                                            uint32_t lspin) {
   if (lane == 0) {
     uint32_t n = 0;
     for (;;) {
       const int32_t cur = lds_read_i32(p);
       if ((kAtLeast ? cur >= v : cur == v) || lds_read_i32(&L.abort) != 0) break;
       __builtin_amdgcn_s_sleep(1);
-      if (++n > kLdsSpin) {
+      if (++n > lspin) {
         lds_write_i32(&L.abort, 1);
         lds_or_i32(&L.err, 4);
         break;
@@ -243,10 +244,10 @@ __device__ __forceinline__ void issue_block(BlockRegs &R, CSite *sites, int nsit
 
 // ------------------------------------------------------------- tiles
 // Add this wavefront's share of tile kt; true if it completed the tile.
-__device__ __forceinline__ bool tile_add(Lds &L, int kt, int64_t p, int contributors,
+__device__ __forceinline__ bool tile_add(Lds &L, int kt, int64_t p, int contributors, uint32_t lspin,
                                          int lane) {
   const int slot = kt & (kTSlots - 1);
-  lds_wait_eq(L, &L.tgen[slot], kt, lane);
+  lds_wait_eq(L, &L.tgen[slot], kt, lane, lspin);
   // rows: lanes 4r..4r+3 hold the 4 k-quarters of row r
   p = (int64_t)((uint64_t)p + dpp_u64<0xB1, 0xF>((uint64_t)p));
   p = (int64_t)((uint64_t)p + dpp_u64<0x4E, 0xF>((uint64_t)p));
@@ -308,17 +309,18 @@ __device__ __forceinline__ void tile_epilogue(Lds &L, int kt, CJob &J, int tl, i
 // completes them, which is waited for here too, so that no wavefront still
 // reads this site's activations once this returns.
 template <bool kDep>
-__device__ void ctrl_serve(CSite &P, Lds &L, int kt0, int r, int G, int lane, uint32_t stamp) {
+__device__ void ctrl_serve(CSite &P, Lds &L, int kt0, int r, int G, int lane, uint32_t stamp,
+                           uint32_t lspin) {
   const int first = (r + P.tile_rot) % G;
   for (int i = 0, t = first; t < P.total_tiles; ++i, t += G) {
     CJob &J = P.job[job_of(P, t)];
     const int kt = kt0 + i, slot = kt & (kTSlots - 1);
     if (J.epi == EPI_ARGMAX) {
       // later argmax tiles may have reused and freed the slot since
-      lds_wait_eq<true>(L, &L.tgen[slot], kt + kTSlots, lane);
+      lds_wait_eq<true>(L, &L.tgen[slot], kt + kTSlots, lane, lspin);
       continue;
     }
-    lds_wait_eq(L, &L.tready[slot], kt + 1, lane);
+    lds_wait_eq(L, &L.tready[slot], kt + 1, lane, lspin);
     if (kDep && J.stamped && lane < kTileRows / 2) {
       // rows 2l and 2l + 1 (int16 epilogues); nrows is even
       const int row = (t - J.tile0) * kTileRows + 2 * lane;
@@ -367,7 +369,8 @@ __device__ void ctrl_serve(CSite &P, Lds &L, int kt0, int r, int G, int lane, ui
 }
 
 // all G workgroups have stored flag value >= v (bounded; bit 1 of err)
-__device__ void grid_wait(uint32_t *flags, int G, uint32_t v, int lane, int32_t *err) {
+__device__ void grid_wait(uint32_t *flags, int G, uint32_t v, int lane, int32_t *err,
+                          uint32_t gspin) {
   uint32_t n = 0;
   for (;;) {
     bool ok = true;
@@ -375,7 +378,7 @@ __device__ void grid_wait(uint32_t *flags, int G, uint32_t v, int lane, int32_t 
       ok = ok && __hip_atomic_load(flags + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= v;
     if (__all(ok)) break;
     __builtin_amdgcn_s_sleep(1);
-    if (++n > kGridSpin) {
+    if (++n > gspin) {
       if (lane == 0) atomicOr(err, 2);
       break;
     }
@@ -393,12 +396,12 @@ struct PSync {
 };
 
 // barrier of the 3 prologue wavefronts only (bounded), through L.psync
-__device__ __forceinline__ void psync(Lds &L, PSync &ps, int pw, int lane) {
+__device__ __forceinline__ void psync(Lds &L, PSync &ps, int pw, int lane, uint32_t lspin) {
   ++ps.phase;
   wait_lds();
   if (lane == 0) lds_write_i32(&L.psync[pw], ps.phase);
   bool done = false;
-  for (uint32_t n = 0; n < kLdsSpin && !done; ++n)
+  for (uint32_t n = 0; n < lspin && !done; ++n)
     done = __all(lds_read_i32(&L.psync[lane % kPW]) >= ps.phase);
   ps.ok = ps.ok && done;
 }
@@ -481,7 +484,7 @@ __device__ __forceinline__ void pro_issue(ProX &X, CSite &P, int pw, int lane) {
 // 8 int16.  The RMSNorm weights are loaded first, as in pro_issue.
 // Bounded: false if the words never all arrived (err bit 1).
 __device__ __forceinline__ bool pro_issue_stamped(ProX &X, CSite &P, uint32_t stamp, int pw,
-                                                  int lane, int32_t *err) {
+                                                  int lane, int32_t *err, uint32_t gspin) {
   const int K = P.K;
   const int wlen = P.pro == PRO_RMSNORM_DYNQ8 ? 2 * K : 0;
   const __amdgpu_buffer_rsrc_t rw =
@@ -493,7 +496,7 @@ __device__ __forceinline__ bool pro_issue_stamped(ProX &X, CSite &P, uint32_t st
   const __amdgpu_buffer_rsrc_t rx =
       __builtin_amdgcn_make_buffer_rsrc((void *)P.x_stamped, (short)0, 4 * K, kBufDword3);
   bool ok = false;
-  for (uint32_t n = 0; n < kGridSpin && !ok; ++n) {
+  for (uint32_t n = 0; n < gspin && !ok; ++n) {
     if (n > 0) __builtin_amdgcn_s_sleep(2);
     bool mine = true;
 #pragma unroll
@@ -573,7 +576,8 @@ __device__ __forceinline__ uint32_t pack4(uint32_t a, uint32_t b) {
 // output); returns e_x.  Chunks past K are skipped.
 template <bool kLds, bool kDep>
 __device__ __forceinline__ int group_prologue(CSite &P, Lds &L, int8_t *out, bool exports,
-                                              int pw, int lane, PSync &ps, ProX &X) {
+                                              int pw, int lane, PSync &ps, ProX &X,
+                                              uint32_t lspin) {
   const int K = P.K;
   if (P.pro == PRO_X8) {
 #pragma unroll
@@ -638,7 +642,7 @@ __device__ __forceinline__ int group_prologue(CSite &P, Lds &L, int8_t *out, boo
       }
     ss = wave_sum_u64(ss);
     if (lane == 0) L.pss[pw] = (int64_t)ss;
-    psync(L, ps, pw, lane);
+    psync(L, ps, pw, lane, lspin);
     ss = 0;
 #pragma unroll
     for (int w = 0; w < kPW; ++w) ss += (uint64_t)L.pss[w];
@@ -697,7 +701,7 @@ __device__ __forceinline__ int group_prologue(CSite &P, Lds &L, int8_t *out, boo
   int32_t mx = max((int32_t)mx2.x, (int32_t)mx2.y);
   mx = wave_max_i32(mx);
   if (lane == 0) L.pmx[pw] = mx;
-  psync(L, ps, pw, lane);
+  psync(L, ps, pw, lane, lspin);
   mx = 0;
 #pragma unroll
   for (int w = 0; w < kPW; ++w) mx = max(mx, L.pmx[w]);
@@ -733,13 +737,13 @@ __device__ __forceinline__ int group_prologue(CSite &P, Lds &L, int8_t *out, boo
 // store of the three wavefronts complete -- e_x and the site's flag.
 template <bool kDep>
 __device__ PSync compute_publish(CSite &P, Lds &L, int8_t *stg, uint32_t *flag, uint32_t epoch,
-                                 int pw, int lane, PSync ps) {
+                                 int pw, int lane, PSync ps, uint32_t lspin) {
   ProX X;
   pro_issue<kDep>(X, P, pw, lane);
-  const int e = group_prologue<false, kDep>(P, L, stg, true, pw, lane, ps, X);
+  const int e = group_prologue<false, kDep>(P, L, stg, true, pw, lane, ps, X, lspin);
   if (pw == 0 && lane == 0) store_coherent((int32_t *)(stg + kXB), (int32_t)e);
   wait_vm_all();
-  psync(L, ps, pw, lane);
+  psync(L, ps, pw, lane, lspin);
   if (pw == 0 && lane == 0) store_coherent(flag, epoch);
   return ps;
 }
@@ -747,8 +751,8 @@ __device__ PSync compute_publish(CSite &P, Lds &L, int8_t *stg, uint32_t *flag, 
 // the wavefront waits until site s's activations are staged in this launch
 // (bounded; bit 1 of err, as for the grid-wide wait)
 __device__ __forceinline__ bool wait_staged(const uint32_t *flag, uint32_t epoch, int lane,
-                                            int32_t *err) {
-  for (uint32_t n = 0; n < kGridSpin; ++n) {
+                                            int32_t *err, uint32_t gspin) {
+  for (uint32_t n = 0; n < gspin; ++n) {
     if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= epoch) return true;
     __builtin_amdgcn_s_sleep(1);
   }
@@ -770,11 +774,11 @@ __device__ __forceinline__ void load_staged(const int8_t *stg, int8_t *xb, int K
 
 // the wavefront waits until all prologue wavefronts have written site s's
 // activations into buffer b (bounded, like lds_wait_eq)
-__device__ __forceinline__ void wait_ready(Lds &L, int b, int s, int lane) {
+__device__ __forceinline__ void wait_ready(Lds &L, int b, int s, int lane, uint32_t lspin) {
   for (uint32_t n = 0;; ++n) {
     if (__all(lds_read_i32(&L.ready[b][lane % kPW]) == s)) break;
     if (lds_read_i32(&L.abort) != 0) break;
-    if (n > kLdsSpin) {
+    if (n > lspin) {
       if (lane == 0) {
         lds_write_i32(&L.abort, 1);
         lds_or_i32(&L.err, 4);
@@ -787,8 +791,8 @@ __device__ __forceinline__ void wait_ready(Lds &L, int b, int s, int lane) {
 }
 
 // the wavefront waits until every weight wavefront has moved past site t
-__device__ __forceinline__ bool wait_weights_past(Lds &L, int t, int lane) {
-  for (uint32_t n = 0; n < kLdsSpin; ++n) {
+__device__ __forceinline__ bool wait_weights_past(Lds &L, int t, int lane, uint32_t lspin) {
+  for (uint32_t n = 0; n < lspin; ++n) {
     if (__all(lds_read_i32(&L.wsite[lane & (kCW - 1)]) > t)) return true;
     if (lds_read_i32(&L.abort) != 0) return false;
     __builtin_amdgcn_s_sleep(1);
@@ -832,7 +836,8 @@ __device__ void head_arrive(const StreamParams &S, int G, uint64_t best) {
 template <bool kDep>
 __device__ __forceinline__ void prologue_role(const GemvParams *sites_arg, int nsites, int r,
                                            int G, int wave, uint32_t *done, int8_t *stage,
-                                           uint32_t epoch, int32_t *err) {
+                                           uint32_t epoch, int32_t *err, uint32_t gspin,
+                                           uint32_t lspin) {
   Lds &L = g_lds;
   CSite *sites = (CSite *)uniform_ptr(sites_arg);
   done = (uint32_t *)uniform_ptr(done);
@@ -858,7 +863,7 @@ __device__ __forceinline__ void prologue_role(const GemvParams *sites_arg, int n
   for (int s = r; s < nsites; s += G)
     if (sites[s].fence_at == 0)
       ps = compute_publish<kDep>(sites[s], L, stage + (size_t)s * kStageBytes, sflag + s, epoch,
-                           pw, lane, ps);
+                           pw, lane, ps, lspin);
   for (int s = 0; s < nsites; ++s) {
     // lane-derived addresses are recomputed per site from an opaque copy
     // of the thread index, so the compiler does not keep them live
@@ -874,19 +879,20 @@ __device__ __forceinline__ void prologue_role(const GemvParams *sites_arg, int n
       // straight into its LDS buffer: one read of the inputs after the
       // grid-wide wait, instead of a staged copy that would first have to
       // be computed, published and flagged by one CU
-      if (s >= kNB) ok = wait_weights_past(L, s - kNB, lane) && ok;
-      ok = lds_wait_ge(&L.gridok, P.fence_at) && ok;
+      if (s >= kNB) ok = wait_weights_past(L, s - kNB, lane, lspin) && ok;
+      ok = lds_wait_ge(&L.gridok, P.fence_at, lspin) && ok;
       ProX X;
       if (P.stamp_src >= 0) {
         // no grid-wide wait: the input's own words say when it is whole.
         // Polled once this CU has stored its own share (a CU that polls
         // while others still stream would only add traffic).
-        ok = lds_wait_ge(&L.served, P.stamp_src) && ok;
-        ok = pro_issue_stamped(X, P, fbase + (uint32_t)P.stamp_src + 1u, pw, lane, err) && ok;
+        ok = lds_wait_ge(&L.served, P.stamp_src, lspin) && ok;
+        ok = pro_issue_stamped(X, P, fbase + (uint32_t)P.stamp_src + 1u, pw, lane, err, gspin) &&
+             ok;
       } else {
         pro_issue<kDep>(X, P, pw, lane);
       }
-      const int e = group_prologue<true, kDep>(P, L, L.x[b], s % G == r, pw, lane, ps, X);
+      const int e = group_prologue<true, kDep>(P, L, L.x[b], s % G == r, pw, lane, ps, X, lspin);
       if (lane == 0) {
         if (pw == 0) lds_write_i32(&L.ex[b], e);
         lds_write_i32(&L.ready[b][pw], s);
@@ -894,12 +900,12 @@ __device__ __forceinline__ void prologue_role(const GemvParams *sites_arg, int n
       continue;
     }
     if (s % G == r && P.fence_at > 0) {
-      ok = lds_wait_ge(&L.gridok, P.fence_at) && ok;
+      ok = lds_wait_ge(&L.gridok, P.fence_at, lspin) && ok;
       ps = compute_publish<kDep>(P, L, stage + (size_t)s * kStageBytes, sflag + s, epoch, pw,
-                           lane, ps);
+                           lane, ps, lspin);
     }
-    if (s >= kNB) ok = wait_weights_past(L, s - kNB, lane) && ok;
-    ok = wait_staged(sflag + s, epoch, lane, err) && ok;
+    if (s >= kNB) ok = wait_weights_past(L, s - kNB, lane, lspin) && ok;
+    ok = wait_staged(sflag + s, epoch, lane, err, gspin) && ok;
     load_staged(stg, L.x[b], P.K, pw, lane);
     const int e = __hip_atomic_load((const int32_t *)(stg + kXB), __ATOMIC_RELAXED,
                                     __HIP_MEMORY_SCOPE_AGENT);
@@ -922,7 +928,7 @@ __device__ __forceinline__ void prologue_role(const GemvParams *sites_arg, int n
 // table reads stay scalar loads.
 template <bool kDep>
 __device__ __forceinline__ void weight_role(const GemvParams *sites_arg, int nsites, int r,
-                                            int G, int wave) {
+                                            int G, int wave, uint32_t lspin) {
   Lds &L = g_lds;
   CSite *sites = (CSite *)uniform_ptr(sites_arg);
   nsites = __builtin_amdgcn_readfirstlane(nsites);
@@ -956,7 +962,7 @@ __device__ __forceinline__ void weight_role(const GemvParams *sites_arg, int nsi
       // done with every earlier site; wait for this one's activations
       s_cur = c.s;
       lds_write_i32(&L.wsite[wave], s_cur);
-      wait_ready(L, s_cur % kNB, s_cur, lane_s);
+      wait_ready(L, s_cur % kNB, s_cur, lane_s, lspin);
       e_x = __builtin_amdgcn_readfirstlane(lds_read_i32(&L.ex[s_cur % kNB]));
       contributors = min(sites[s_cur].nblk, kCW);
     }
@@ -969,7 +975,7 @@ __device__ __forceinline__ void weight_role(const GemvParams *sites_arg, int nsi
     const Cursor done = c;
     auto finish_tile = [&]() {
       const int kt = done.kt0 + i;
-      if (tile_add(L, kt, p, contributors, lane_s)) {
+      if (tile_add(L, kt, p, contributors, lspin, lane_s)) {
         const int t = done.first + i * G;
         CJob &J = P.job[job_of(P, t)];
         tile_epilogue(L, kt, J, t - J.tile0, e_x, lane_s);
@@ -1008,6 +1014,9 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
   const int nsites = S.nsites;
   // this launch's completion-flag values are fbase + 1 .. fbase + nsites
   const uint32_t fbase = (S.epoch - 1u) * (uint32_t)(nsites + 1);
+  // polls before a wait gives up: between workgroups, within one
+  const uint32_t gspin = S.grid_spin ? S.grid_spin : kGridSpin;
+  const uint32_t lspin = S.lds_spin ? S.lds_spin : kLdsSpin;
 
   // tables, reduction slots and flags
   const int32_t *tab = sites[0].tables;
@@ -1042,7 +1051,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
       // cursors around their fences
       if (kDep)
         for (int a = s + 1; a < nsites && a <= s + 3; ++a) touch_site(&sites[a]);
-      ctrl_serve<kDep>(P, L, kt0, r, G, lane, fbase + (uint32_t)s + 1u);
+      ctrl_serve<kDep>(P, L, kt0, r, G, lane, fbase + (uint32_t)s + 1u, lspin);
       if (kDep && lane == 0) lds_write_i32(&L.served, s);
       {
         const int first = (r + P.tile_rot) % G;
@@ -1052,14 +1061,15 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
         const uint32_t v = fbase + (uint32_t)(s + 1);
         wait_vm_all();   // this workgroup's outputs of sites <= s are stored
         if (lane == 0) store_coherent(S.done + r, v);
-        grid_wait(S.done, G, v, lane, S.err);
+        grid_wait(S.done, G, v, lane, S.err, gspin);
         if (lane == 0) lds_write_i32(&L.gridok, s + 1);
       }
     }
   } else if (wave >= kPW0) {
-    prologue_role<kDep>(sites_arg, S.nsites, r, G, wave, S.done, S.stage, S.epoch, S.err);
+    prologue_role<kDep>(sites_arg, S.nsites, r, G, wave, S.done, S.stage, S.epoch, S.err,
+                        gspin, lspin);
   } else {
-    weight_role<kDep>(sites_arg, nsites, r, G, wave);
+    weight_role<kDep>(sites_arg, nsites, r, G, wave, lspin);
   }
 
   int tid_e = tid;

@@ -231,8 +231,8 @@ constexpr uint32_t kTkSpin = 1u << 20;   // polls before a wait gives up
 
 // every word w[0..cnt) satisfies pred (bounded; false if it gave up)
 template <typename Pred>
-__device__ bool wait_words(const int32_t *w, int cnt, Pred pred, int lane) {
-  for (uint32_t it = 0; it < kTkSpin; ++it) {
+__device__ bool wait_words(const int32_t *w, int cnt, Pred pred, int lane, uint32_t spin) {
+  for (uint32_t it = 0; it < spin; ++it) {
     bool ok = true;
     for (int j = lane; j < cnt; j += 64) ok = ok && pred(ld_coh32(w + j));
     if (__all(ok)) return true;
@@ -248,7 +248,8 @@ __device__ bool wait_words(const int32_t *w, int cnt, Pred pred, int lane) {
 // zero), written by the last chunk.  Bit 3 of err: a wait gave up.
 __global__ __launch_bounds__(64) void topk_kernel(const int32_t *y, int64_t n, int nchunks,
                                                   int32_t epoch, uint64_t *part, uint64_t *sup,
-                                                  int32_t *flags, int32_t *out, int32_t *err) {
+                                                  int32_t *flags, int32_t *out, int32_t *err,
+                                                  uint32_t spin) {
   __shared__ uint64_t buf[128];
   __shared__ int32_t rows[kTkRows];
   int32_t *pub = flags, *done = flags + kTopkMaxChunks, *spub = flags + 2 * kTopkMaxChunks;
@@ -278,7 +279,7 @@ __global__ __launch_bounds__(64) void topk_kernel(const int32_t *y, int64_t n, i
   // the list of the earlier chunks of this super-chunk ...
   const int s = c / kTopkSuper, c0 = s * kTopkSuper;
   auto is_epoch = [epoch](int32_t v) { return v == epoch; };
-  bool ok = wait_words(pub + c0, c - c0, is_epoch, lane);
+  bool ok = wait_words(pub + c0, c - c0, is_epoch, lane, spin);
   const uint64_t W = top32_lists(part + (int64_t)c0 * kTk, c - c0, up, lane);
   if (c - c0 == kTopkSuper - 1) {
     const uint64_t S = merge32v(W, own, up, lane);   // all lanes take part in a merge
@@ -287,7 +288,7 @@ __global__ __launch_bounds__(64) void topk_kernel(const int32_t *y, int64_t n, i
     if (lane == 0) st_coh32(spub + s, epoch);
   }
   // ... and of the earlier super-chunks: the list before this chunk
-  ok = wait_words(spub, s, is_epoch, lane) && ok;
+  ok = wait_words(spub, s, is_epoch, lane, spin) && ok;
   const uint64_t pre = merge32v(top32_lists(sup, s, up, lane), W, up, lane);
   // replay this chunk's arrivals
   uint64_t L = pre;
@@ -343,7 +344,7 @@ __global__ __launch_bounds__(64) void topk_kernel(const int32_t *y, int64_t n, i
   }
   if (c == nchunks - 1) {
     const uint64_t whole = merge32v(pre, own, up, lane);
-    ok = wait_words(done, c, [epoch](int32_t v) { return (v >> 1) == epoch; }, lane) && ok;
+    ok = wait_words(done, c, [epoch](int32_t v) { return (v >> 1) == epoch; }, lane, spin) && ok;
     int f = ovf;
     for (int j = lane; j < c; j += 64) f |= ld_coh32(done + j) & 1;
     const bool any = __ballot(f != 0) != 0;
@@ -374,12 +375,13 @@ size_t topk_scratch_bytes(int64_t n) {
 }
 
 hipError_t launch_topk32(const int32_t *y, int64_t n, void *scratch, int32_t *flags,
-                         int32_t epoch, int32_t *out, int32_t *err, hipStream_t s) {
+                         int32_t epoch, int32_t *out, int32_t *err, hipStream_t s,
+                         uint32_t spin) {
   const int nchunks = topk_chunks(n);
   if (nchunks > kTopkMaxChunks) return hipErrorInvalidValue;
   uint64_t *part = (uint64_t *)scratch;
   hipLaunchKernelGGL(topk_kernel, dim3(nchunks), dim3(64), 0, s, y, n, nchunks, epoch, part,
-                     part + (size_t)nchunks * kTk, flags, out, err);
+                     part + (size_t)nchunks * kTk, flags, out, err, spin ? spin : kTkSpin);
   return hipGetLastError();
 }
 

@@ -120,6 +120,12 @@ class Context:
                              "torch.cuda.Stream() created for the engine")
         N.check(N.lib().w4a8_ctx_set_stream(self.h, ctypes.c_void_p(s)))
 
+    def set_spin_limit(self, grid_polls=0, lds_polls=0):
+        """Polls before the bounded waits of later persistent-plan and
+        TOPK-32 launches give up (0: the defaults); a wait that gives up is
+        reported as a RuntimeError at the next sync."""
+        N.check(N.lib().w4a8_ctx_set_spin_limit(self.h, int(grid_polls), int(lds_polls)))
+
     def set_grid(self, grid):
         N.check(N.lib().w4a8_ctx_set_grid(self.h, int(grid)))
 

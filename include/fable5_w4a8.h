@@ -84,6 +84,16 @@ int w4a8_ctx_sync(w4a8_ctx *ctx);
 int w4a8_ctx_info(const w4a8_ctx *ctx, int32_t *num_cu, int32_t *grid);
 /* override the GEMV grid size (0 = default); for tuning sweeps */
 int w4a8_ctx_set_grid(w4a8_ctx *ctx, int32_t grid);
+/* no counterpart in the reference: how many polls the context's later
+   persistent-plan and TOPK-32 launches make before a bounded wait gives up
+   -- grid_polls for waits on other workgroups (reported at the next sync as
+   W4A8_E_HIP, "...wait for other workgroups timed out..."; TOPK-32's
+   look-back: "...TOPK-32's wait..."), lds_polls for waits between the
+   wavefronts of one workgroup ("a wait between wavefronts ...").  A wait
+   that gives up lets its kernel run to its end (results undefined), so a
+   caller can exercise these error paths without a hang.  0: the defaults
+   (2^18 and 2^20 polls). */
+int w4a8_ctx_set_spin_limit(w4a8_ctx *ctx, uint32_t grid_polls, uint32_t lds_polls);
 /* the rsqrt seed LUT (512 Q1.15) and sigmoid knots (257 Q15) the device
    uses: fixedpoint.py:42-53 and 128-142 (ROMs roms/rsqrt_rom.hex,
    roms/sigmoid_rom.hex) */
