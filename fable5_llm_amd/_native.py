@@ -64,6 +64,7 @@ SIGNATURES = {
     "w4a8_topk32": [_P, _P, _I64, _P, _P, _P, _P],
     "w4a8_head_topk32": [_P, _P, _I32, _P, _P, _I32, _I32, _P, _P, _P, _P],
     "w4a8_head_topk32_async": [_P, _P, _I32, _P, _P, _I32, _I32, _I32, _P],
+    "w4a8_head_topk32_noalloc_async": [_P, _P, _I32, _P, _P, _I32, _I32, _I32, _P],
     "w4a8_mlp_async": [_P, _P, _P, _P, _I32, _I32, _I32, _P, _P, _I32, _I32, _P, _P],
     "w4a8_plan_create": [_P, ctypes.POINTER(_P)],
     "w4a8_plan_add_site": [_P, _I32, _PP, _P, _P, _PP, _I32, _P, _P, _I32, _I32,

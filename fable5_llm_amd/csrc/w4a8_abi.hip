@@ -7,6 +7,8 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -34,6 +36,7 @@ struct w4a8_ctx {
   int32_t *d_topk_flags = nullptr;   // TOPK-32 look-back flags (kTopkFlagWords)
   int32_t topk_epoch = 0;            // epoch of the last TOPK-32 launch
   uint32_t spin_grid = 0, spin_lds = 0;   // polls before bounded waits give up (0: defaults)
+  uint8_t *d_scratch = nullptr;   // this device's copy of `scratch` (no-alloc entry point)
   int32_t h_tables[kTableLen];
 };
 
@@ -46,6 +49,18 @@ struct w4a8_weights {
   Layout L{};
   size_t bytes = 0;
 };
+
+// ---- device memory of the entry point that allocates nothing
+// w4a8_head_topk32_noalloc_async keeps the head's y32 (at most 2^18 rows,
+// the AMAX32 index range) and TOPK-32's chunk and super-chunk lists here
+// instead of the context's chain buffer.  Every GPU the library runs on
+// holds its own copy, 1.07 MiB, until the process ends; every call on one
+// GPU shares it, so calls that overlap on one GPU race.  Nothing in it has
+// to start at zero: the y32 is written whole before TOPK-32 reads it, and a
+// list is read only after its flag carries the launch's epoch.
+constexpr size_t kScratchY = sizeof(int32_t) << 18;
+constexpr size_t kScratchLists = (size_t)(kTopkMaxChunks + kTopkMaxChunks / kTopkSuper) * 32 * 8;
+static __device__ __align__(256) uint8_t scratch[kScratchY + kScratchLists];
 
 static thread_local std::string g_err;
 
@@ -75,6 +90,24 @@ struct DeviceGuard {
       (void)hipSetDevice(prev);
   }
 };
+
+// The device address of this device's `scratch`, resolved once per device
+// with that device current (the caller's DeviceGuard).  The array's name is
+// only a host-side stand-in: host code passes this address, never the name.
+int scratch_address(int device, uint8_t **out) {
+  static std::mutex mu;
+  static std::map<int, uint8_t *> addr;
+  std::lock_guard<std::mutex> lk(mu);
+  auto it = addr.find(device);
+  if (it == addr.end()) {
+    void *p = nullptr;
+    HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail(W4A8_E_HIP, "hipGetSymbolAddress(scratch) gave a null address");
+    it = addr.emplace(device, (uint8_t *)p).first;
+  }
+  *out = it->second;
+  return W4A8_OK;
+}
 
 int64_t wire_stride(int32_t K) {
   const int ng = K / kGroup;
@@ -350,6 +383,7 @@ int w4a8_ctx_create(int32_t device, w4a8_ctx **out) {
       rc = fail(W4A8_E_HIP, hipGetErrorString(e));
       break;
     }
+    rc = scratch_address(device, &c->d_scratch);
   } while (0);
   if (rc) {
     w4a8_ctx_destroy(c);
@@ -836,7 +870,7 @@ int w4a8_matmul_y32_multi_async(w4a8_ctx *c, int32_t n, const w4a8_weights *cons
 // earlier launches; they are cleared (by a kernel, so that a captured graph
 // clears them on every replay) when the stream is being captured -- a graph
 // replays one fixed epoch -- and before the epoch grows too large.
-static int topk_launch(w4a8_ctx *c, const int32_t *d_y, int64_t n, void *scratch,
+static int topk_launch(w4a8_ctx *c, const int32_t *d_y, int64_t n, void *lists,
                        int32_t *d_out) {
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   HIP_TRY(hipStreamIsCapturing(c->stream, &cs));
@@ -846,12 +880,24 @@ static int topk_launch(w4a8_ctx *c, const int32_t *d_y, int64_t n, void *scratch
     c->topk_epoch = 0;
   }
   const int32_t epoch = ++c->topk_epoch;
-  HIP_TRY(launch_topk32(d_y, n, scratch, c->d_topk_flags, epoch, d_out, c->d_err, c->stream,
+  HIP_TRY(launch_topk32(d_y, n, lists, c->d_topk_flags, epoch, d_out, c->d_err, c->stream,
                         c->spin_grid));
   // a captured launch replays this epoch with its own clear; the next eager
   // launch clears the flags first
   if (cs != hipStreamCaptureStatusNone) c->topk_epoch = 0;
   return W4A8_OK;
+}
+
+// The head's y32 into buf[0, yb), then TOPK-32 with its lists at buf + yb
+// (yb = the y32's bytes rounded up to 256).
+static int head_topk_launch(w4a8_ctx *c, GemvParams &P, const w4a8_weights *w, uint8_t *buf,
+                            int32_t *d_out) {
+  const size_t yb = ((size_t)w->nrows * 4 + 255) & ~(size_t)255;
+  int32_t *y = (int32_t *)buf;
+  P.job[0].epi = EPI_Y32;   // the head's raw y32 (shift 0, seq_format.py:2225-2226)
+  P.job[0].out = y;
+  HIP_TRY(launch_gemv(P, grid_for(c, P.total_tiles), c->stream));
+  return topk_launch(c, y, w->nrows, buf + yb, d_out);
 }
 
 int w4a8_head_topk32_async(w4a8_ctx *c, const w4a8_weights *w, int32_t prologue,
@@ -864,11 +910,25 @@ int w4a8_head_topk32_async(w4a8_ctx *c, const w4a8_weights *w, int32_t prologue,
   const size_t yb = ((size_t)w->nrows * 4 + 255) & ~(size_t)255;
   DeviceGuard g(c->device);
   if ((rc = ensure_chain(c, yb + topk_scratch_bytes(w->nrows)))) return rc;
-  int32_t *y = (int32_t *)c->d_chain;
-  P.job[0].epi = EPI_Y32;   // the head's raw y32 (shift 0, seq_format.py:2225-2226)
-  P.job[0].out = y;
-  HIP_TRY(launch_gemv(P, grid_for(c, P.total_tiles), c->stream));
-  return topk_launch(c, y, w->nrows, c->d_chain + yb, d_out);
+  return head_topk_launch(c, P, w, c->d_chain, d_out);
+}
+
+int w4a8_head_topk32_noalloc_async(w4a8_ctx *c, const w4a8_weights *w, int32_t prologue,
+                                   const void *d_x, const int16_t *d_norm_w, int32_t in_f,
+                                   int32_t one_plus, int32_t e_x, int32_t *d_out) {
+  if (!c || !w || !d_out) return fail(W4A8_E_ARG, "null argument");
+  const size_t yb = ((size_t)w->nrows * 4 + 255) & ~(size_t)255;
+  if (w->nrows > (1 << 18) || yb > kScratchY ||
+      topk_scratch_bytes(w->nrows) > kScratchLists)
+    return fail(W4A8_E_RANGE, "a head of " + std::to_string(w->nrows) +
+                                  " rows exceeds the static scratch's 2^18 rows (" +
+                                  std::to_string(kScratchY + kScratchLists) + " bytes)");
+  if (!c->d_scratch) return fail(W4A8_E_HIP, "head_topk32_noalloc: no scratch address");
+  GemvParams P;
+  int rc = head_params(c, P, w, prologue, d_x, d_norm_w, in_f, one_plus, e_x);
+  if (rc) return rc;
+  DeviceGuard g(c->device);
+  return head_topk_launch(c, P, w, c->d_scratch, d_out);
 }
 
 int w4a8_topk32(w4a8_ctx *c, const int32_t *y32, int64_t n, int32_t *vals, int32_t *rows,

@@ -301,6 +301,18 @@ class Context:
             self.h, w.h, int(prologue), _dptr(x), _dptr(norm_w), int(in_f),
             1 if one_plus else 0, int(e_x), _dptr(out)), "head_topk32")
 
+    def head_topk32_noalloc_async(self, w, x, out, prologue=N.PRO_DYNQ8, e_x=0, norm_w=None,
+                                  in_f=0, one_plus=False):
+        """head_topk32_async without any device allocation: the y32 and the
+        lists live in the library's static per-GPU array (heads of at most
+        2^18 rows); calls that overlap on one GPU race."""
+        _dev(x, _x_bytes(prologue, w.K), "x")
+        _dev(norm_w, 2 * w.K, "norm_w", required=False)
+        _dev(out, 66 * 4, "out")
+        N.check(N.lib().w4a8_head_topk32_noalloc_async(
+            self.h, w.h, int(prologue), _dptr(x), _dptr(norm_w), int(in_f),
+            1 if one_plus else 0, int(e_x), _dptr(out)), "head_topk32_noalloc")
+
     def matmul_y32(self, w, x8):
         x = np.ascontiguousarray(np.asarray(x8, dtype=np.int8))
         assert x.ndim == 2 and x.shape[1] == w.K

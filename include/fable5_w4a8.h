@@ -230,6 +230,18 @@ int w4a8_head_topk32_async(w4a8_ctx *ctx, const w4a8_weights *w,
                            int32_t prologue, const void *d_x,
                            const int16_t *d_norm_w, int32_t in_f,
                            int32_t one_plus, int32_t e_x, int32_t *d_out);
+/* w4a8_head_topk32_async that allocates nothing: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The head's y32 and TOPK-32's lists live in a static device array of
+ * 1.07 MiB per GPU (held until the process ends) instead of the context's
+ * chain buffer; heads over 2^18 rows are refused with W4A8_E_RANGE.  Every
+ * call on one GPU shares that array, from every context: calls that overlap
+ * on one GPU race. */
+int w4a8_head_topk32_noalloc_async(w4a8_ctx *ctx, const w4a8_weights *w,
+                                   int32_t prologue, const void *d_x,
+                                   const int16_t *d_norm_w, int32_t in_f,
+                                   int32_t one_plus, int32_t e_x, int32_t *d_out);
 
 /* ---- the SwiGLU FFN block on device buffers ---------------------------
  * One decoder layer's MLP (gen_layer_script.py:2166-2190 mlp_block;
