@@ -14,8 +14,10 @@ from oracle import law
 from oracle.fixtures import script_tags
 from oracle.seq_model import SeqOracle, load_images
 from tests.helpers import rand_w4_m, write_fixture_artifacts
-from tests.seq_streams import (I16_ADDR, PAIRS_ADDR, X_ADDR, movx, movy, mvgo,
-                               script_stream, swin_stage, v_record_stream, xrf_write)
+from tests.seq_streams import (I16_ADDR, PAIRS_ADDR, SEQ_STREAMS, X_ADDR, LayerShim,
+                               golden_plan, golden_streams, golden_wids, movx, movy, mvgo,
+                               script_stream, swin_stage, v_record_stream,
+                               write_golden_artifacts, xrf_write)
 
 pytestmark = pytest.mark.gpu
 
@@ -248,6 +250,33 @@ def test_host_write_after_swin_wins(engine, scripts, tmp_path):
         for r in swin_stage(a + 2, [21]):
             m.step(r)
         assert list(m.read_scratch(a, 4)) == [11, -7, 21, 14]
+
+
+@pytest.mark.parametrize("name", SEQ_STREAMS)
+def test_reference_stream_on_device(engine, tmp_path, name):
+    """A stream the reference's encoder wrote (one channel, one channel with
+    no-wait MVGOs and FENCE, four channels with the head interleaved) run by
+    SeqMachine, the head's AMAX32 commands applied by the test over the
+    staged pairs each MOVY leaves: the scratch the reference's executor left,
+    word for word, and its AMAX32 index and value
+    (tests/golden/make_seq_fixtures.py)."""
+    z = golden_streams()
+    prefix = write_golden_artifacts(tmp_path, z)
+    with Artifacts(engine, prefix) as art, \
+            S.SeqMachine(engine, art, plan=golden_plan(z, name)) as m:
+        for wid in golden_wids(z):
+            m.write_scratch(int(z[f"w{wid}_meta"][6]), z[f"w{wid}_x8"])
+        shim = LayerShim(m.read_pairs)
+        n = 0
+        for r in S.unpack_stream(z[f"{name}_rec"].tobytes()):
+            n += 1
+            if not shim.take(r) and not m.step(r):
+                break
+        want = z[f"{name}_mem"]
+        got = m.read_scratch(0, want.size).astype(np.int64)
+    assert n == z[f"{name}_rec"].size // 16
+    assert np.array_equal(got, want), np.flatnonzero(got != want)[:10]
+    assert [shim.amax.idx, shim.amax.val] == list(z[f"{name}_amax"]) and shim.ncmd == 5
 
 
 def _emb_artifacts(tmp_path, ntok=40, width=1024):
