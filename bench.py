@@ -164,13 +164,18 @@ def batched_leg(st, ctx, batches, steps, warmup, seed):
     """The FFN matrices of the stream (32 x gate, up: 12288 x 4096; down:
     4096 x 12288; 2.49 GB, far beyond the 256 MB Infinity Cache) through the
     batched int8-MFMA kernel, B tokens per pass: per-token x16 in Q8.7
-    (N(0,1), 1 % outliers), DYNQ8 per token on the GPU, then one
-    w4a8_matmul_y32_multi_async launch per site (a layer's gate and up share
-    their tokens' x8 and one launch; its down takes another).  Returns the
-    timings and, for the checker, layer 0's inputs and outputs."""
+    (N(0,1), 1 % outliers), DYNQ8 per token on the GPU, then
+      * one matmul plan over all 96 matrices: ONE launch per pass, each
+        matrix writing its own y32 (the leg's value), and
+      * one w4a8_matmul_y32_multi_async launch per site (a layer's gate and
+        up share their tokens' x8 and one launch; its down takes another:
+        64 launches per pass), for comparison.
+    Returns the timings and, for the checker, layer 0's inputs and the
+    plan's outputs."""
     import numpy as np
     import torch
     from fable5_llm_amd import stream9b
+    from fable5_llm_amd.engine import MatmulPlan
     dev = torch.device("cuda", ctx.device)
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed + 7)
@@ -184,7 +189,7 @@ def batched_leg(st, ctx, batches, steps, warmup, seed):
             rows = [ctx.dynq8(stream9b.synth_x16(gen, K, stream9b.RS_F).cpu().numpy())[0]
                     for _ in range(B)]
             x8[K] = torch.from_numpy(np.stack(rows)).to(dev)
-        # one output per matrix position in its site (gate and up write apart)
+        # per-site launches: one output per matrix position in its site
         y = {(mi, st.sites[si].mats[mi].nrows): None for si, mi in ffn}
         y = {k: torch.empty((B, k[1]), dtype=torch.int32, device=dev) for k in y}
         sites = {}
@@ -203,27 +208,41 @@ def batched_leg(st, ctx, batches, steps, warmup, seed):
                                        [x8[m.K] for m in ms],
                                        [y[(mi, m.nrows)] for mi, m in zip(mis, ms)])
 
-        ms, ms_eager, how = time_passes(ctx, one_pass, stream, steps, warmup)
+        ms_site, _eager, how_site = time_passes(ctx, one_pass, stream, steps, warmup)
+        # the plan: every matrix its own output
+        yp = {}
+        plan = MatmulPlan(ctx, B)
+        for si, mi in ffn:
+            m = st.sites[si].mats[mi]
+            yp[(si, mi)] = torch.empty((B, m.nrows), dtype=torch.int32, device=dev)
+            plan.add(st.weights[si][mi], x8[m.K], yp[(si, mi)])
+        plan.run()      # writes its device table
+        ctx.sync()
+        ms, ms_eager, how = time_passes(ctx, plan.run, stream, steps, warmup)
         gbs = nbytes / (ms * 1e-3) / 1e9
         tops = ops / (ms * 1e-3) / 1e12
+        gbs_site = nbytes / (ms_site * 1e-3) / 1e9
         out.append({"B": B, "matrices": len(ffn), "ms_per_pass": round(ms, 4),
                     "ms_per_pass_eager": round(ms_eager, 4), "timing": how,
                     "value": round(gbs, 1), "unit": "GB/s",
                     "pct_of_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 1),
                     "tops": round(tops, 2),
                     "mfma_util_pct": round(100.0 * tops / PEAK_INT8_TOPS, 2),
-                    "bytes_per_pass": nbytes, "kernel": "matmul_kernel",
-                    "launches_per_pass": len(sites)})
-        # layer 0's gate, up and down with their outputs, for the checker
-        for si in dict.fromkeys(si for si, _ in ffn[:3]):
-            ms = [st.sites[si].mats[mi] for mi in sites[si]]
-            ctx.matmul_multi_async([st.weights[si][mi] for mi in sites[si]],
-                                   [x8[m.K] for m in ms],
-                                   [y[(mi, m.nrows)] for mi, m in zip(sites[si], ms)])
+                    "bytes_per_pass": nbytes, "kernel": "matmul_kernel (matmul plan)",
+                    "launches_per_pass": 1,
+                    "per_site_launches": {"launches_per_pass": len(sites),
+                                          "ms_per_pass": round(ms_site, 4),
+                                          "value": round(gbs_site, 1), "timing": how_site,
+                                          "pct_of_peak_hbm":
+                                              round(100.0 * gbs_site / PEAK_HBM_GBS, 1)}})
+        # layer 0's gate, up and down from the plan's last run, for the checker
+        plan.run()
         ctx.sync()
         for si, mi in ffn[:3]:
             m = st.sites[si].mats[mi]
-            keep.append((B, si, mi, x8[m.K].cpu().numpy(), y[(mi, m.nrows)].cpu().numpy()))
+            keep.append((B, si, mi, x8[m.K].cpu().numpy(), yp[(si, mi)].cpu().numpy()))
+        plan.close()
+        del yp
     return out, keep
 
 

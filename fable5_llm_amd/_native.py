@@ -61,6 +61,10 @@ SIGNATURES = {
     "w4a8_head_argmax_async": [_P, _P, _I32, _P, _P, _I32, _I32, _I32, _P],
     "w4a8_matmul_y32_async": [_P, _P, _P, _I32, _P],
     "w4a8_matmul_y32_multi_async": [_P, _I32, _P, _P, _I32, _P],
+    "w4a8_mplan_create": [_P, _I32, ctypes.POINTER(_P)],
+    "w4a8_mplan_add": [_P, _P, _P, _P],
+    "w4a8_mplan_run": [_P],
+    "w4a8_mplan_destroy": [_P],
     "w4a8_topk32": [_P, _P, _I64, _P, _P, _P, _P],
     "w4a8_head_topk32": [_P, _P, _I32, _P, _P, _I32, _I32, _P, _P, _P, _P],
     "w4a8_head_topk32_async": [_P, _P, _I32, _P, _P, _I32, _I32, _I32, _P],

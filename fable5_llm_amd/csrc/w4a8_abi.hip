@@ -865,6 +865,77 @@ int w4a8_matmul_y32_multi_async(w4a8_ctx *c, int32_t n, const w4a8_weights *cons
   return W4A8_OK;
 }
 
+// ------------------------------------------------------------ matmul plan
+// Up to kMmPlanJobs matrices for the same B tokens, their records in a
+// device table written at the first run after the last add: one launch of
+// matmul_kernel per run, the weight stream running on across every matrix.
+struct w4a8_mplan {
+  w4a8_ctx *ctx = nullptr;
+  int32_t B = 0;
+  std::vector<MmJobSpec> jobs;
+  void *d_table = nullptr;
+  MmPlanCfg cfg{};
+  bool built = false;
+};
+
+int w4a8_mplan_create(w4a8_ctx *c, int32_t B, w4a8_mplan **out) {
+  if (!c || !out) return fail(W4A8_E_ARG, "null argument");
+  if (B < 1 || B > 64) return fail(W4A8_E_RANGE, "batch must be 1..64");
+  w4a8_mplan *p = new w4a8_mplan();
+  p->ctx = c;
+  p->B = B;
+  *out = p;
+  return W4A8_OK;
+}
+
+int w4a8_mplan_add(w4a8_mplan *p, const w4a8_weights *w, const int8_t *d_x8, int32_t *d_y32) {
+  if (!p || !w || !d_x8 || !d_y32) return fail(W4A8_E_ARG, "null weights / x8 / y32");
+  if (!aligned16(d_x8)) return fail(W4A8_E_ARG, "x8 must be 16-byte aligned");
+  if ((int)p->jobs.size() >= kMmPlanJobs)
+    return fail(W4A8_E_RANGE, "matmul plan: at most " + std::to_string(kMmPlanJobs) +
+                                  " matrices");
+  p->jobs.push_back(MmJobSpec{w->d, (int32_t)w->nrows, w->L, w->sh, d_x8, d_y32});
+  p->built = false;
+  return W4A8_OK;
+}
+
+int w4a8_mplan_run(w4a8_mplan *p) {
+  if (!p) return fail(W4A8_E_ARG, "null plan");
+  if (p->jobs.empty()) return fail(W4A8_E_ARG, "matmul plan has no matrices");
+  w4a8_ctx *c = p->ctx;
+  DeviceGuard g(c->device);
+  const int n = (int)p->jobs.size();
+  if (!p->built) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    HIP_TRY(hipStreamIsCapturing(c->stream, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+      return fail(W4A8_E_ARG, "matmul plan: run it once before capturing it (the first "
+                              "run after an add writes its device table)");
+    std::vector<uint8_t> host(matmul_job_bytes() * (size_t)n);
+    HIP_TRY(matmul_plan_prepare(p->jobs.data(), n, p->B, host.data(), &p->cfg));
+    HIP_TRY(hipStreamSynchronize(c->stream));   // an earlier run may still read the table
+    if (p->d_table) HIP_TRY(hipFree(p->d_table));
+    p->d_table = nullptr;
+    HIP_TRY(hipMalloc(&p->d_table, host.size()));
+    HIP_TRY(hipMemcpy(p->d_table, host.data(), host.size(), hipMemcpyHostToDevice));
+    p->built = true;
+  }
+  HIP_TRY(launch_matmul_plan(p->d_table, n, p->cfg, c->d_err, c->stream));
+  return W4A8_OK;
+}
+
+int w4a8_mplan_destroy(w4a8_mplan *p) {
+  if (!p) return W4A8_OK;
+  int rc = W4A8_OK;
+  if (p->d_table) {
+    DeviceGuard g(p->ctx->device);
+    if (hipStreamSynchronize(p->ctx->stream) != hipSuccess || hipFree(p->d_table) != hipSuccess)
+      rc = fail(W4A8_E_HIP, "matmul plan: freeing its table failed");
+  }
+  delete p;
+  return rc;
+}
+
 // ------------------------------------------------------------ TOPK-32
 // One TOPK-32 launch on the context's stream.  Flags hold the epochs of
 // earlier launches; they are cleared (by a kernel, so that a captured graph

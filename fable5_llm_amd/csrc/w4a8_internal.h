@@ -251,6 +251,19 @@ struct MmJobSpec {
 };
 hipError_t launch_matmul_multi(const MmJobSpec *jobs, int n, int32_t B, int32_t *err,
                                hipStream_t s);
+// A matmul plan: up to kMmPlanJobs matrices for the same B tokens in one
+// launch, their records in a device table (matmul_job_bytes() each) that
+// matmul_plan_prepare writes on the host, with the launch shape in cfg.
+constexpr int kMmPlanJobs = 128;
+struct MmPlanCfg {
+  int32_t B, CT, G, tmx, ctxt, R, nl, slot_bytes;
+  size_t lds;
+};
+size_t matmul_job_bytes();
+hipError_t matmul_plan_prepare(const MmJobSpec *jobs, int n, int32_t B, void *table,
+                               MmPlanCfg *cfg);
+hipError_t launch_matmul_plan(const void *d_table, int n, const MmPlanCfg &cfg,
+                              int32_t *err, hipStream_t s);
 hipError_t launch_matmul(const uint8_t *w, int32_t nrows, const Layout &L,
                          int32_t sh, const int8_t *x8, int32_t B,
                          int32_t *y32, int32_t *err, hipStream_t s);

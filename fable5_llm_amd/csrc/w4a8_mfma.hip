@@ -67,7 +67,8 @@ struct MmJob {
 };
 
 struct MmParams {
-  MmJob job[kMmJobs];
+  MmJob job[kMmJobs];   // the jobs, when they travel in the parameters ...
+  const MmJob *tab;     // ... or a device table of njobs (a matmul plan)
   int32_t njobs;
   int32_t B, CT;
   int32_t R;            // LDS slots
@@ -87,10 +88,11 @@ struct MmFlags {
   int32_t pad[2];
   // this workgroup's schedule: job j has nmine[j] of its tiles, global
   // rounds rbase[j] .. rbase[j + 1] - 1 and steps sbase[j] .. sbase[j + 1] - 1
-  int32_t nmine[kMmJobs];
-  int32_t rbase[kMmJobs + 1];
-  int32_t sbase[kMmJobs + 1];
+  int32_t nmine[kMmPlanJobs];
+  int32_t rbase[kMmPlanJobs + 1];
+  int32_t sbase[kMmPlanJobs + 1];
 };
+static_assert(kMmPlanJobs <= 128, "the schedule scan takes two jobs a lane");
 constexpr int kFlagBytes = (int)((sizeof(MmFlags) + 255) / 256 * 256);
 
 __device__ __forceinline__ int cvt_lo16(uint32_t w) {
@@ -188,29 +190,18 @@ struct MmCur {
     rho = kb = RHO = 0;
     while (j < njobs && F.rbase[j + 1] == 0) ++j;
   }
-  __device__ void next(const MmFlags &F, const MmParams &P) {
-    if (++kb < P.job[j].nblk) return;
+  // nblk: blocks of the current job
+  __device__ void next(const MmFlags &F, int njobs, int nblk) {
+    if (++kb < nblk) return;
     kb = 0;
     ++rho;
     ++RHO;
-    while (j < P.njobs && RHO == F.rbase[j + 1]) {
+    while (j < njobs && RHO == F.rbase[j + 1]) {
       ++j;
       rho = 0;
     }
   }
 };
-
-// job and position of global step s (s < sbase[njobs])
-__device__ __forceinline__ int mm_job_of_step(const MmFlags &F, int njobs, int s) {
-  int j = 0;
-  while (j + 1 < njobs && s >= F.sbase[j + 1]) ++j;
-  return j;
-}
-__device__ __forceinline__ int mm_job_of_round(const MmFlags &F, int njobs, int RHO) {
-  int j = 0;
-  while (j + 1 < njobs && RHO >= F.rbase[j + 1]) ++j;
-  return j;
-}
 
 // Put group 8 kb + w of tile j of round rho in flight: a buffer load whose
 // range is empty (no memory access, zeros) when there is no such tile or
@@ -239,9 +230,20 @@ __device__ __forceinline__ uint4 mm_issue(const MmJob &J, int r, int G, int w, i
 template <int TMX, int CTX>
 constexpr int mm_depth() { return TMX >= 4 ? 4 : 8; }
 
-template <int TMX, int CTX>
+template <int TMX, int CTX, bool kTab>
 __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
   extern __shared__ __align__(16) uint8_t smem[];
+  // job j (j uniform): from the parameters, or from the plan's device table
+  // read as constant memory, so that its fields come in by scalar loads and
+  // no wait for them counts the weight pieces in flight
+  typedef const __attribute__((address_space(4))) MmJob CJob;
+  auto JOB = [&](int j) -> const MmJob & {
+    const int ju = __builtin_amdgcn_readfirstlane(j);
+    if constexpr (kTab)
+      return *(const MmJob *)((CJob *)P.tab + ju);
+    else
+      return P.job[ju];
+  };
   MmFlags &F = *(MmFlags *)smem;
   int64_t *tables = (int64_t *)(smem + kFlagBytes);   // [2][TMX][CTX][4][64]
   uint8_t *ring = smem + kFlagBytes + 2 * TMX * CTX * 4 * 64 * 8;
@@ -258,26 +260,53 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
   if (tid == 0) {
     F.abort = 0;
     F.err = 0;
-    F.rbase[0] = F.sbase[0] = 0;
-    for (int j = 0; j < P.njobs; ++j) {
-      const MmJob &J = P.job[j];
-      const int nm = r < J.ntiles ? (J.ntiles - 1 - r) / G + 1 : 0;
-      const int nr = (nm + J.tm - 1) / J.tm;
-      F.nmine[j] = nm;
-      F.rbase[j + 1] = F.rbase[j] + nr;
-      F.sbase[j + 1] = F.sbase[j] + nr * J.nblk;
-    }
+  }
+  // thread j: job j's tiles, rounds and steps on this workgroup ...
+  if (tid < P.njobs) {
+    const MmJob &J = kTab ? P.tab[tid] : P.job[tid];
+    const int nm = r < J.ntiles ? (J.ntiles - 1 - r) / G + 1 : 0;
+    const int nr = (nm + J.tm - 1) / J.tm;
+    F.nmine[tid] = nm;
+    F.rbase[tid + 1] = nr;
+    F.sbase[tid + 1] = nr * J.nblk;
   }
   for (int i = tid; i < 2 * TMX * CTX * 4 * 64; i += kMThreads) tables[i] = 0;
+  __syncthreads();
+  // ... and wavefront 0's prefix sums of them (lane l: jobs 2l, 2l + 1)
+  if (wave == 0) {
+    const int j0 = 2 * lane, j1 = 2 * lane + 1;
+    const int a0 = j0 < P.njobs ? F.rbase[j0 + 1] : 0, b0 = j0 < P.njobs ? F.sbase[j0 + 1] : 0;
+    const int a1 = j1 < P.njobs ? F.rbase[j1 + 1] : 0, b1 = j1 < P.njobs ? F.sbase[j1 + 1] : 0;
+    int sa = a0 + a1, sb = b0 + b1;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int ta = __shfl_up(sa, o), tb = __shfl_up(sb, o);
+      if (lane >= o) {
+        sa += ta;
+        sb += tb;
+      }
+    }
+    const int ea = sa - a0 - a1, eb = sb - b0 - b1;   // before job j0
+    if (j0 < P.njobs) {
+      F.rbase[j0 + 1] = ea + a0;
+      F.sbase[j0 + 1] = eb + b0;
+    }
+    if (j1 < P.njobs) {
+      F.rbase[j1 + 1] = sa;
+      F.sbase[j1 + 1] = sb;
+    }
+    if (lane == 0) F.rbase[0] = F.sbase[0] = 0;
+  }
   __syncthreads();
   const int nrounds = F.rbase[P.njobs], nsteps = F.sbase[P.njobs];
 
   if (wave == kMStore) {
     // round rho's sums are complete once all 8 group wavefronts have added
     bool ok = true;
+    int jb = 0;
     for (int RHO = 0; RHO < nrounds; ++RHO) {
-      const int jb = mm_job_of_round(F, P.njobs, RHO);
-      const MmJob &J = P.job[jb];
+      while (RHO >= F.rbase[jb + 1]) ++jb;   // rounds ascend: the job advances
+      const MmJob &J = JOB(jb);
       const int rho = RHO - F.rbase[jb];
       const int tb = RHO & 1, nt = round_tiles(J, F.nmine[jb], rho);
       int64_t *tbl = tables + tb * (TMX * CTX * 4 * 64);
@@ -339,9 +368,10 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
     // loader l: steps l, l + nl, ...
     const int l = wave - kMW;
     if (l < P.nl) {
+      int jb = 0;
       for (int s = l; s < nsteps; s += P.nl) {
-        const int jb = mm_job_of_step(F, P.njobs, s);
-        const MmJob &J = P.job[jb];
+        while (s >= F.sbase[jb + 1]) ++jb;   // steps ascend: the job advances
+        const MmJob &J = JOB(jb);
         const int ls = s - F.sbase[jb];
         const int rho = ls / J.nblk, kb = ls - rho * J.nblk;
         const int slot = s % P.R;
@@ -385,12 +415,12 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
     cur.start(F, P.njobs);
     auto fill = [&](uint4 (&slot)[TMX][D], const int d) {
       const bool any = f.RHO < nrounds;
-      const MmJob &J = P.job[any ? f.j : 0];
+      const MmJob &J = JOB(any ? f.j : 0);
       const int nt = any ? round_tiles(J, F.nmine[f.j], f.rho) : 0;
 #pragma unroll
       for (int j = 0; j < TMX; ++j)
         slot[j][d] = mm_issue(J, r, G, w, lane, f.rho, f.kb, j, j < nt);
-      if (any) f.next(F, P);
+      if (any) f.next(F, P.njobs, J.nblk);
     };
 #pragma unroll
     for (int d = 0; d < D; ++d) fill(wr, d);
@@ -399,7 +429,8 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
 #pragma unroll
       for (int d = 0; d < D; ++d) {
         if (s >= nsteps) goto finished;
-        const int nt = round_tiles(P.job[cur.j], F.nmine[cur.j], cur.rho);
+        const MmJob &JC = JOB(cur.j);
+        const int nt = round_tiles(JC, F.nmine[cur.j], cur.rho);
         const int slot = s % P.R;
         mm_wait_word<false>(F, &F.ready[slot], s, lane);
         const uint8_t *sb = ring + (size_t)slot * P.slot_bytes;
@@ -442,7 +473,7 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
         fill(wr, d);
         wait_lds();   // this wavefront's reads of the slot are done
         if (lane == 0) lds_write_i32(&F.done[w], s);
-        if (cur.kb == P.job[cur.j].nblk - 1) {
+        if (cur.kb == JC.nblk - 1) {
           // end of round RHO: add this wavefront's sums into its table
           const int tb = cur.RHO & 1;
           int64_t *tbl = tables + tb * (TMX * CTX * 4 * 64);
@@ -460,7 +491,7 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
           wait_lds();   // the adds are done before the count
           if (lane == 0) mm_lds_add_rtn(&F.tcnt[tb], 1);
         }
-        cur.next(F, P);
+        cur.next(F, P.njobs, JC.nblk);
         ++s;
       }
     }
@@ -473,24 +504,23 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
   }
 }
 
-}  // namespace
-
-hipError_t launch_matmul_multi(const MmJobSpec *jobs, int n, int32_t B, int32_t *err,
-                               hipStream_t s) {
-  if (n < 1 || n > kMmJobs || B < 1 || B > 64) return hipErrorInvalidValue;
-  MmParams P{};
-  P.njobs = n;
-  P.B = B;
-  P.CT = (B + 15) / 16;
-  P.err = err;
-  int tmx = P.CT == 1 ? 4 : (P.CT == 2 ? 2 : 1);
+// The jobs' records and the launch shape for B tokens: the grid (one
+// workgroup per CU at most), tiles per round (TMX) and column tiles of 16
+// tokens (CTX) of the kernel instance, the LDS ring and its loaders.
+static hipError_t mm_setup(const MmJobSpec *jobs, int n, int32_t B, MmJob *out,
+                           MmPlanCfg &c) {
+  if (n < 1 || B < 1 || B > 64) return hipErrorInvalidValue;
+  c.B = B;
+  c.CT = (B + 15) / 16;
+  int tmx = c.CT == 1 ? 4 : (c.CT == 2 ? 2 : 1);
   int dev = 0, ncu = 256;
   if (hipGetDevice(&dev) == hipSuccess)
     (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
   int maxt = 1;
   for (int j = 0; j < n; ++j) {
-    MmJob &J = P.job[j];
+    MmJob &J = out[j];
     const MmJobSpec &q = jobs[j];
+    J = MmJob{};
     J.W = q.w;
     J.x8 = q.x8;
     J.y32 = q.y32;
@@ -508,56 +538,108 @@ hipError_t launch_matmul_multi(const MmJobSpec *jobs, int n, int32_t B, int32_t 
   // weight pipeline of the one-tile kernels
   int maxper = 1;
   for (int j = 0; j < n; ++j) {
-    const int per = (P.job[j].ntiles + G - 1) / G;
+    const int per = (out[j].ntiles + G - 1) / G;
     maxper = per > maxper ? per : maxper;
   }
   if (maxper == 1) tmx = 1;
-  const int ctxt = tmx == 4 ? 1 : (tmx == 2 ? 2 : (P.CT <= 2 ? P.CT : 4));
+  const int ctxt = tmx == 4 ? 1 : (tmx == 2 ? 2 : (c.CT <= 2 ? c.CT : 4));
   const int table_bytes = 2 * tmx * ctxt * 4 * 64 * 8;
-  P.slot_bytes = 16 * P.CT * kXRow + tmx * 256;
+  c.slot_bytes = 16 * c.CT * kXRow + tmx * 256;
   const int avail = kLdsBytes - kFlagBytes - table_bytes;
-  P.R = avail / P.slot_bytes;
-  if (P.R > kRingMax) P.R = kRingMax;
-  if (P.R < 2) return hipErrorInvalidValue;
-  P.nl = P.R - 1 < kML ? P.R - 1 : kML;   // >= 1: R >= 2
+  c.R = avail / c.slot_bytes;
+  if (c.R > kRingMax) c.R = kRingMax;
+  if (c.R < 2) return hipErrorInvalidValue;
+  c.nl = c.R - 1 < kML ? c.R - 1 : kML;   // >= 1: R >= 2
   // rounds of tm tiles: as many tiles per round as the workgroups' shares
   // of the job allow, at most tmx
   for (int j = 0; j < n; ++j) {
-    const int per = (P.job[j].ntiles + G - 1) / G;
-    P.job[j].tm = per < tmx ? per : tmx;
+    const int per = (out[j].ntiles + G - 1) / G;
+    out[j].tm = per < tmx ? per : tmx;
   }
-  const size_t lds = (size_t)kFlagBytes + table_bytes + (size_t)P.R * P.slot_bytes;
+  c.G = G;
+  c.tmx = tmx;
+  c.ctxt = ctxt;
+  c.lds = (size_t)kFlagBytes + table_bytes + (size_t)c.R * c.slot_bytes;
+  return hipSuccess;
+}
+
+template <bool kTab>
+static hipError_t mm_set_lds_limit() {
+  hipError_t e = hipFuncSetAttribute((const void *)matmul_kernel<4, 1, kTab>,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+  if (e == hipSuccess)
+    e = hipFuncSetAttribute((const void *)matmul_kernel<2, 2, kTab>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+  if (e == hipSuccess)
+    e = hipFuncSetAttribute((const void *)matmul_kernel<1, 4, kTab>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+  if (e == hipSuccess)
+    e = hipFuncSetAttribute((const void *)matmul_kernel<1, 1, kTab>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+  if (e == hipSuccess)
+    e = hipFuncSetAttribute((const void *)matmul_kernel<1, 2, kTab>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+  return e;
+}
+
+template <bool kTab>
+static hipError_t mm_launch(const MmParams &P, const MmPlanCfg &c, hipStream_t s) {
   // dynamic LDS beyond the default limit: allowed once per process
-  static const hipError_t attr = [] {
-    hipError_t e = hipFuncSetAttribute((const void *)matmul_kernel<4, 1>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-    if (e == hipSuccess)
-      e = hipFuncSetAttribute((const void *)matmul_kernel<2, 2>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-    if (e == hipSuccess)
-      e = hipFuncSetAttribute((const void *)matmul_kernel<1, 4>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-    if (e == hipSuccess)
-      e = hipFuncSetAttribute((const void *)matmul_kernel<1, 1>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-    if (e == hipSuccess)
-      e = hipFuncSetAttribute((const void *)matmul_kernel<1, 2>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-    return e;
-  }();
+  static const hipError_t attr = mm_set_lds_limit<kTab>();
   if (attr != hipSuccess) return attr;
-  if (tmx == 4) {
-    hipLaunchKernelGGL((matmul_kernel<4, 1>), dim3(G), dim3(kMThreads), lds, s, P);
-  } else if (tmx == 2) {
-    hipLaunchKernelGGL((matmul_kernel<2, 2>), dim3(G), dim3(kMThreads), lds, s, P);
-  } else if (ctxt == 1) {
-    hipLaunchKernelGGL((matmul_kernel<1, 1>), dim3(G), dim3(kMThreads), lds, s, P);
-  } else if (ctxt == 2) {
-    hipLaunchKernelGGL((matmul_kernel<1, 2>), dim3(G), dim3(kMThreads), lds, s, P);
+  const dim3 g(c.G), b(kMThreads);
+  if (c.tmx == 4) {
+    hipLaunchKernelGGL((matmul_kernel<4, 1, kTab>), g, b, c.lds, s, P);
+  } else if (c.tmx == 2) {
+    hipLaunchKernelGGL((matmul_kernel<2, 2, kTab>), g, b, c.lds, s, P);
+  } else if (c.ctxt == 1) {
+    hipLaunchKernelGGL((matmul_kernel<1, 1, kTab>), g, b, c.lds, s, P);
+  } else if (c.ctxt == 2) {
+    hipLaunchKernelGGL((matmul_kernel<1, 2, kTab>), g, b, c.lds, s, P);
   } else {
-    hipLaunchKernelGGL((matmul_kernel<1, 4>), dim3(G), dim3(kMThreads), lds, s, P);
+    hipLaunchKernelGGL((matmul_kernel<1, 4, kTab>), g, b, c.lds, s, P);
   }
   return hipGetLastError();
+}
+
+static void mm_params(MmParams &P, int n, const MmPlanCfg &c, int32_t *err) {
+  P.njobs = n;
+  P.B = c.B;
+  P.CT = c.CT;
+  P.R = c.R;
+  P.nl = c.nl;
+  P.slot_bytes = c.slot_bytes;
+  P.err = err;
+}
+
+}  // namespace
+
+size_t matmul_job_bytes() { return sizeof(MmJob); }
+
+hipError_t matmul_plan_prepare(const MmJobSpec *jobs, int n, int32_t B, void *table,
+                               MmPlanCfg *cfg) {
+  if (n < 1 || n > kMmPlanJobs || !table || !cfg) return hipErrorInvalidValue;
+  return mm_setup(jobs, n, B, (MmJob *)table, *cfg);
+}
+
+hipError_t launch_matmul_plan(const void *d_table, int n, const MmPlanCfg &cfg, int32_t *err,
+                              hipStream_t s) {
+  if (n < 1 || n > kMmPlanJobs || !d_table) return hipErrorInvalidValue;
+  MmParams P{};
+  mm_params(P, n, cfg, err);
+  P.tab = (const MmJob *)d_table;
+  return mm_launch<true>(P, cfg, s);
+}
+
+hipError_t launch_matmul_multi(const MmJobSpec *jobs, int n, int32_t B, int32_t *err,
+                               hipStream_t s) {
+  if (n < 1 || n > kMmJobs) return hipErrorInvalidValue;
+  MmParams P{};
+  MmPlanCfg c{};
+  hipError_t e = mm_setup(jobs, n, B, P.job, c);
+  if (e != hipSuccess) return e;
+  mm_params(P, n, c, err);
+  return mm_launch<false>(P, c, s);
 }
 
 hipError_t launch_matmul(const uint8_t *w, int32_t nrows, const Layout &L, int32_t sh,

@@ -525,3 +525,43 @@ class Plan:
         if self.h:
             N.lib().w4a8_plan_destroy(self.h)
             self.h = None
+
+
+class MatmulPlan:
+    """Up to 128 matrices for the same B tokens run as ONE batched int8-MFMA
+    launch per run (device tensors x8 [B][K], y32 [B][nrows] per matrix).
+    The first run after an add writes the plan's device table; run it once
+    before capturing it into a graph.  Holds references to its tensors."""
+
+    def __init__(self, ctx, B):
+        self.ctx, self.B = ctx, int(B)
+        h = ctypes.c_void_p()
+        N.check(N.lib().w4a8_mplan_create(ctx.h, self.B, ctypes.byref(h)), "mplan_create")
+        self.h = h
+        self._keep = []
+        self.bytes = 0        # algorithmic weight bytes per run
+        self.nmats = 0
+
+    def add(self, w, x8, y32):
+        if x8.shape[0] != self.B or y32.shape[0] != self.B:
+            raise ValueError(f"matmul plan: x8 and y32 hold the plan's {self.B} tokens")
+        _dev(x8, self.B * w.K, "x8")
+        _dev(y32, 4 * self.B * w.nrows, "y32")
+        N.check(N.lib().w4a8_mplan_add(self.h, w.h, _dptr(x8), _dptr(y32)), "mplan_add")
+        self._keep += [w, x8, y32]
+        self.bytes += w.wire_bytes
+        self.nmats += 1
+
+    def run(self):
+        N.check(N.lib().w4a8_mplan_run(self.h), "mplan_run")
+
+    def close(self):
+        if self.h:
+            N.lib().w4a8_mplan_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()

@@ -207,6 +207,21 @@ int w4a8_matmul_y32_multi_async(w4a8_ctx *ctx, int32_t n,
                                 const w4a8_weights *const *w,
                                 const int8_t *const *d_x8, int32_t B,
                                 int32_t *const *d_y32);
+/* A matmul plan: up to 128 matrices for the same B tokens (1..64) in ONE
+ * launch per run (e.g. a pass over a model's 96 FFN matrices), each matrix
+ * i reading its d_x8 [B][K_i] and writing its d_y32 [B][nrows_i], each row
+ * bit-identical to w4a8_matmul_y32_async of that matrix alone.  The first
+ * run after an add writes the plan's device table (so run it once before
+ * capturing it into a graph); runs enqueue on the context stream.  The
+ * weight stream runs on across every matrix of the plan instead of
+ * draining at each launch's end.  No counterpart in the reference (its
+ * engine runs one matrix per MVGO, one token at a time). */
+typedef struct w4a8_mplan w4a8_mplan;
+int w4a8_mplan_create(w4a8_ctx *ctx, int32_t B, w4a8_mplan **out);
+int w4a8_mplan_add(w4a8_mplan *plan, const w4a8_weights *w, const int8_t *d_x8,
+                   int32_t *d_y32);
+int w4a8_mplan_run(w4a8_mplan *plan);
+int w4a8_mplan_destroy(w4a8_mplan *plan);
 
 /* ---- TOPK-32 over the LM head -----------------------------------------
  * The layer_topk32 block's contract (docs/SEQ_ISA.md B8): the head's raw

@@ -390,3 +390,73 @@ def test_matmul_multi_matches_per_token(engine, B):
     finally:
         for w in ws:
             w.free()
+
+
+@pytest.mark.parametrize("B", [1, 8, 17, 32, 64])
+def test_matmul_plan_one_launch(engine, B):
+    """A matmul plan of 40 matrices (more than one launch of the per-launch
+    path holds; shapes from 40 x 256 to 4096 x 12288, several sharing x8)
+    in one launch: every output equal to the per-launch path's (itself
+    checked per token above) and the oracle's on three tokens; a second run
+    on overwritten outputs and graph replays give the same."""
+    import torch
+    from fable5_llm_amd.engine import MatmulPlan
+    rng = np.random.default_rng(4100 + B)
+    dev = torch.device("cuda", 0)
+    base = [(12288, 4096), (4096, 12288), (40, 256), (100, 1024), (33, 3584), (2048, 2048),
+            (777, 4096), (16, 128)]
+    shapes = [base[i % len(base)] for i in range(40)]
+    ws, imgs = {}, {}
+    for N_, K in set(shapes):
+        img, _ = rand_image(rng, N_, K)
+        imgs[(N_, K)] = img
+        ws[(N_, K)] = engine.upload(img, N_, K, law.sh_for_k(K))
+    xk = {K: torch.from_numpy(rng.integers(-128, 128, (B, K)).astype(np.int8)).to(dev)
+          for K in {k for _, k in shapes}}
+    ys = [torch.full((B, N_), 0x5A5A5A5A, dtype=torch.int32, device=dev) for N_, _ in shapes]
+    ref = [torch.zeros_like(y) for y in ys]
+    plan = MatmulPlan(engine, B)
+    try:
+        for (N_, K), y in zip(shapes, ys):
+            plan.add(ws[(N_, K)], xk[K], y)
+        for i in range(0, len(shapes), 16):
+            sl = shapes[i:i + 16]
+            engine.matmul_multi_async([ws[s] for s in sl], [xk[k] for _, k in sl], ref[i:i + 16])
+        plan.run()
+        engine.sync()
+        want = [r.cpu().numpy() for r in ref]
+        for i, (N_, K) in enumerate(shapes):
+            got = ys[i].cpu().numpy()
+            assert np.array_equal(got, want[i]), i
+            for b in sorted({0, B // 2, B - 1}):
+                o = cfast.matvec_y32_img(imgs[(N_, K)], N_, K, law.sh_for_k(K),
+                                         xk[K][b].cpu().numpy())
+                assert np.array_equal(got[b], o), (i, b)
+        for y in ys:
+            y.fill_(-1)
+        torch.cuda.synchronize()
+        plan.run()
+        engine.sync()
+        assert all(np.array_equal(y.cpu().numpy(), w) for y, w in zip(ys, want))
+        side = torch.cuda.Stream()
+        g = torch.cuda.CUDAGraph()
+        try:
+            with torch.cuda.graph(g, stream=side):
+                engine.set_stream(side)
+                plan.run()
+        finally:
+            engine.set_stream(None)
+        for _ in range(2):
+            for y in ys:
+                y.fill_(-1)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert all(np.array_equal(y.cpu().numpy(), w) for y, w in zip(ys, want))
+        with pytest.raises(AssertionError, match="at most 128"):
+            for _ in range(100):
+                plan.add(ws[(16, 128)], xk[128], ys[7])
+    finally:
+        plan.close()
+        for w in ws.values():
+            w.free()
