@@ -121,6 +121,11 @@ __device__ __forceinline__ int32_t mm_lds_add_rtn(int32_t *p, int32_t v) {
                : "=v"(old) : "v"(lds_off(p)), "v"(v) : "memory");
   return old;
 }
+// an LDS write that does not wait for itself (nor for earlier LDS work: a
+// wavefront's LDS instructions execute in order)
+__device__ __forceinline__ void mm_lds_post(int32_t *p, int32_t v) {
+  asm volatile("ds_write_b32 %0, %1" :: "v"(lds_off(p)), "v"(v) : "memory");
+}
 __device__ __forceinline__ void mm_lds_or(int32_t *p, int32_t v) {
   asm volatile("ds_or_b32 %0, %1" :: "v"(lds_off(p)), "v"(v) : "memory");
 }
@@ -181,38 +186,67 @@ __device__ __forceinline__ int round_tiles(const MmJob &J, int nmine, int rho) {
 }
 
 // Position in this workgroup's schedule: job j, its round rho and block kb;
-// RHO and S count rounds and steps over all jobs.  Jobs with no tile on this
-// workgroup are skipped.
+// RHO counts rounds over all jobs.  Jobs with no tile on this workgroup are
+// skipped.  The fields of job j that a step needs stay in registers, so the
+// job table and the schedule in LDS are read only when the job changes (a
+// read on every step puts its latency on every step).
 struct MmCur {
   int j, rho, kb, RHO;
-  __device__ void start(const MmFlags &F, int njobs) {
+  int rend;                // first round past job j
+  int nblk, tm, nmine, nt, NG, K;
+  const uint8_t *W;
+  const int8_t *x8;
+  int64_t tile_bytes;
+  template <class JobF>
+  __device__ void load(const MmFlags &F, int njobs, JobF &JOB) {
+    if (j >= njobs) return;
+    const MmJob &J = JOB(j);
+    nblk = J.nblk;
+    tm = J.tm;
+    NG = J.NG;
+    K = J.K;
+    W = J.W;
+    x8 = J.x8;
+    tile_bytes = J.tile_bytes;
+    nmine = __builtin_amdgcn_readfirstlane(F.nmine[j]);
+    rend = __builtin_amdgcn_readfirstlane(F.rbase[j + 1]);
+    nt = min(tm, nmine - rho * tm);
+  }
+  template <class JobF>
+  __device__ void start(const MmFlags &F, int njobs, JobF &JOB) {
     j = 0;
     rho = kb = RHO = 0;
+    nt = 0;
+    W = nullptr;
     while (j < njobs && F.rbase[j + 1] == 0) ++j;
+    load(F, njobs, JOB);
   }
-  // nblk: blocks of the current job
-  __device__ void next(const MmFlags &F, int njobs, int nblk) {
+  template <class JobF>
+  __device__ void next(const MmFlags &F, int njobs, JobF &JOB) {
     if (++kb < nblk) return;
     kb = 0;
     ++rho;
     ++RHO;
-    while (j < njobs && RHO == F.rbase[j + 1]) {
-      ++j;
-      rho = 0;
+    if (RHO < rend) {
+      nt = min(tm, nmine - rho * tm);
+      return;
     }
+    rho = 0;
+    while (j < njobs && RHO == F.rbase[j + 1]) ++j;
+    load(F, njobs, JOB);
   }
 };
 
-// Put group 8 kb + w of tile j of round rho in flight: a buffer load whose
-// range is empty (no memory access, zeros) when there is no such tile or
-// group, so every step issues the same loads.
-__device__ __forceinline__ uint4 mm_issue(const MmJob &J, int r, int G, int w, int lane,
-                                          int rho, int kb, int j, bool real) {
-  const uint8_t *base = J.W;
+// Put group 8 kb + w of tile j of the cursor's round in flight: a buffer
+// load whose range is empty (no memory access, zeros) when there is no such
+// tile or group, so every step issues the same loads.
+__device__ __forceinline__ uint4 mm_issue(const MmCur &C, int r, int G, int w, int lane, int j,
+                                          bool real) {
+  const uint8_t *base = C.W;
   int len = 0;
-  if (real && 8 * kb + w < J.NG) {
-    const int64_t t = (int64_t)r + (int64_t)G * (rho * J.tm + j);
-    base = J.W + t * J.tile_bytes + (int64_t)kb * kBlockBytes + kScaleChunk +
+  if (real && 8 * C.kb + w < C.NG) {
+    const int64_t t = (int64_t)r + (int64_t)G * (C.rho * C.tm + j);
+    base = C.W + t * C.tile_bytes + (int64_t)C.kb * kBlockBytes + kScaleChunk +
            (int64_t)w * kGroupChunk;
     len = kGroupChunk;
   }
@@ -368,33 +402,33 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
     // loader l: steps l, l + nl, ...
     const int l = wave - kMW;
     if (l < P.nl) {
-      int jb = 0;
+      MmCur lc;   // step s of this loader
+      lc.start(F, P.njobs, JOB);
+      for (int i = 0; i < l && i < nsteps; ++i) lc.next(F, P.njobs, JOB);
+      int slot = l;   // s % R (l < nl < R)
       for (int s = l; s < nsteps; s += P.nl) {
-        while (s >= F.sbase[jb + 1]) ++jb;   // steps ascend: the job advances
-        const MmJob &J = JOB(jb);
-        const int ls = s - F.sbase[jb];
-        const int rho = ls / J.nblk, kb = ls - rho * J.nblk;
-        const int slot = s % P.R;
         // the slot's previous step has been consumed by every group wavefront
         if (s >= P.R &&
             !mm_wait(F, [&] { return lds_read_i32(&F.done[lane & (kMW - 1)]) >= s - P.R; }))
           break;
         uint8_t *sb = ring + (size_t)slot * P.slot_bytes;
-        const int kbytes = min(1024, J.K - kb * 1024);   // multiple of 128
+        const int kbytes = min(1024, lc.K - lc.kb * 1024);   // multiple of 128
         for (int tok = 0; tok < P.B; ++tok) {
           const int8_t *src = 16 * lane < kbytes
-                                  ? J.x8 + (int64_t)tok * J.K + kb * 1024 + 16 * lane
-                                  : J.x8;   // nothing to copy: any mapped address
+                                  ? lc.x8 + (int64_t)tok * lc.K + lc.kb * 1024 + 16 * lane
+                                  : lc.x8;   // nothing to copy: any mapped address
           dma16(src, lds_off(sb + tok * kXRow));
         }
-        const int nt = round_tiles(J, F.nmine[jb], rho);
-        for (int j = 0; j < nt; ++j) {
-          const int64_t t = (int64_t)r + (int64_t)G * (rho * J.tm + j);
-          dma4(J.W + t * J.tile_bytes + (int64_t)kb * kBlockBytes + 4 * lane,
+        for (int j = 0; j < lc.nt; ++j) {
+          const int64_t t = (int64_t)r + (int64_t)G * (lc.rho * lc.tm + j);
+          dma4(lc.W + t * lc.tile_bytes + (int64_t)lc.kb * kBlockBytes + 4 * lane,
                lds_off(sb + 16 * P.CT * kXRow + 256 * j));
         }
         mm_wait_vm_all();
         if (lane == 0) lds_write_i32(&F.ready[slot], s);
+        for (int i = 0; i < P.nl && s + 1 + i < nsteps; ++i) lc.next(F, P.njobs, JOB);
+        slot += P.nl;
+        if (slot >= P.R) slot -= P.R;
       }
     }
   } else {
@@ -411,28 +445,24 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
     // wr[j][d]: tile j's piece of the step s with s % D == d
     uint4 wr[TMX][D];
     MmCur f, cur;   // next step to put in flight; the step being computed
-    f.start(F, P.njobs);
-    cur.start(F, P.njobs);
+    f.start(F, P.njobs, JOB);
+    cur.start(F, P.njobs, JOB);
     auto fill = [&](uint4 (&slot)[TMX][D], const int d) {
       const bool any = f.RHO < nrounds;
-      const MmJob &J = JOB(any ? f.j : 0);
-      const int nt = any ? round_tiles(J, F.nmine[f.j], f.rho) : 0;
 #pragma unroll
-      for (int j = 0; j < TMX; ++j)
-        slot[j][d] = mm_issue(J, r, G, w, lane, f.rho, f.kb, j, j < nt);
-      if (any) f.next(F, P.njobs, J.nblk);
+      for (int j = 0; j < TMX; ++j) slot[j][d] = mm_issue(f, r, G, w, lane, j, any && j < f.nt);
+      if (any) f.next(F, P.njobs, JOB);
     };
 #pragma unroll
     for (int d = 0; d < D; ++d) fill(wr, d);
-    int s = 0;
+    int s = 0, slot = 0;   // slot = s % R
+    int rdy = -1;          // the slot's ready word, read during the step before
     for (;;) {
 #pragma unroll
       for (int d = 0; d < D; ++d) {
         if (s >= nsteps) goto finished;
-        const MmJob &JC = JOB(cur.j);
-        const int nt = round_tiles(JC, F.nmine[cur.j], cur.rho);
-        const int slot = s % P.R;
-        mm_wait_word<false>(F, &F.ready[slot], s, lane);
+        const int nt = cur.nt;
+        if (rdy != s) mm_wait_word<false>(F, &F.ready[slot], s, lane);
         const uint8_t *sb = ring + (size_t)slot * P.slot_bytes;
         // this group's activations for the step's tokens: lane (c, q) feeds
         // token 16 ct + c, k = 128 w + 32 q + [0, 32)
@@ -469,11 +499,17 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
             }
           }
         }
+        // the next slot's ready word, read now so that its latency passes
+        // under this step's remaining work
+        typedef volatile __attribute__((address_space(3))) int32_t lds_i32;
+        rdy = __builtin_amdgcn_readfirstlane(
+            *(lds_i32 *)(lds_void_t *)&F.ready[slot + 1 == P.R ? 0 : slot + 1]);
         // refill this step's registers with the step D ahead
         fill(wr, d);
-        wait_lds();   // this wavefront's reads of the slot are done
-        if (lane == 0) lds_write_i32(&F.done[w], s);
-        if (cur.kb == JC.nblk - 1) {
+        // the slot is free: its reads were issued before this write, and
+        // LDS instructions of a wavefront execute in order
+        if (lane == 0) mm_lds_post(&F.done[w], s);
+        if (cur.kb == cur.nblk - 1) {
           // end of round RHO: add this wavefront's sums into its table
           const int tb = cur.RHO & 1;
           int64_t *tbl = tables + tb * (TMX * CTX * 4 * 64);
@@ -491,8 +527,9 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
           wait_lds();   // the adds are done before the count
           if (lane == 0) mm_lds_add_rtn(&F.tcnt[tb], 1);
         }
-        cur.next(F, P.njobs, JC.nblk);
+        cur.next(F, P.njobs, JOB);
         ++s;
+        if (++slot == P.R) slot = 0;
       }
     }
   finished:;
