@@ -876,6 +876,10 @@ struct w4a8_mplan {
   void *d_table = nullptr;
   MmPlanCfg cfg{};
   bool built = false;
+  uint8_t *d_part = nullptr;  // the K-split jobs' slice sums
+  void *d_fin = nullptr;      // their finishing records
+  int nfin = 0;
+  int64_t fin_max = 0;        // the largest B * nrows among them
 };
 
 int w4a8_mplan_create(w4a8_ctx *c, int32_t B, w4a8_mplan **out) {
@@ -912,25 +916,55 @@ int w4a8_mplan_run(w4a8_mplan *p) {
       return fail(W4A8_E_ARG, "matmul plan: run it once before capturing it (the first "
                               "run after an add writes its device table)");
     std::vector<uint8_t> host(matmul_job_bytes() * (size_t)n);
-    HIP_TRY(matmul_plan_prepare(p->jobs.data(), n, p->B, host.data(), &p->cfg));
-    HIP_TRY(hipStreamSynchronize(c->stream));   // an earlier run may still read the table
-    if (p->d_table) HIP_TRY(hipFree(p->d_table));
-    p->d_table = nullptr;
+    std::vector<int32_t> ns(n);
+    HIP_TRY(matmul_plan_prepare(p->jobs.data(), n, p->B, host.data(), &p->cfg, ns.data()));
+    HIP_TRY(hipStreamSynchronize(c->stream));   // an earlier run may still read the tables
+    for (void *q : {(void *)p->d_table, (void *)p->d_part, p->d_fin})
+      if (q) HIP_TRY(hipFree(q));
+    p->d_table = p->d_fin = nullptr;
+    p->d_part = nullptr;
+    // a K-split job's slices store their sums to part [ns][B][nrows] int64
+    std::vector<size_t> off(n, 0);
+    size_t part = 0;
+    for (int j = 0; j < n; ++j) {
+      if (ns[j] <= 1) continue;
+      off[j] = part;
+      part += ((size_t)ns[j] * p->B * (size_t)p->jobs[j].nrows * 8 + 255) & ~(size_t)255;
+    }
+    p->nfin = 0;
+    p->fin_max = 0;
+    if (part) {
+      HIP_TRY(hipMalloc(&p->d_part, part));
+      for (int j = 0; j < n; ++j) {
+        if (ns[j] <= 1) continue;
+        matmul_plan_bind(host.data(), j, (int64_t *)(p->d_part + off[j]));
+        const int64_t e = (int64_t)p->B * p->jobs[j].nrows;
+        p->fin_max = e > p->fin_max ? e : p->fin_max;
+      }
+      std::vector<uint8_t> fin(matmul_finish_bytes() * (size_t)n);
+      p->nfin = matmul_finish_prepare(host.data(), n, p->B, fin.data());
+      HIP_TRY(hipMalloc(&p->d_fin, fin.size()));
+      HIP_TRY(hipMemcpy(p->d_fin, fin.data(), fin.size(), hipMemcpyHostToDevice));
+    }
     HIP_TRY(hipMalloc(&p->d_table, host.size()));
     HIP_TRY(hipMemcpy(p->d_table, host.data(), host.size(), hipMemcpyHostToDevice));
     p->built = true;
   }
   HIP_TRY(launch_matmul_plan(p->d_table, n, p->cfg, c->d_err, c->stream));
+  HIP_TRY(launch_matmul_finish(p->d_fin, p->nfin, p->fin_max, c->d_err, c->stream));
   return W4A8_OK;
 }
 
 int w4a8_mplan_destroy(w4a8_mplan *p) {
   if (!p) return W4A8_OK;
   int rc = W4A8_OK;
-  if (p->d_table) {
+  if (p->d_table || p->d_part || p->d_fin) {
     DeviceGuard g(p->ctx->device);
-    if (hipStreamSynchronize(p->ctx->stream) != hipSuccess || hipFree(p->d_table) != hipSuccess)
-      rc = fail(W4A8_E_HIP, "matmul plan: freeing its table failed");
+    if (hipStreamSynchronize(p->ctx->stream) != hipSuccess ||
+        (p->d_table && hipFree(p->d_table) != hipSuccess) ||
+        (p->d_part && hipFree(p->d_part) != hipSuccess) ||
+        (p->d_fin && hipFree(p->d_fin) != hipSuccess))
+      rc = fail(W4A8_E_HIP, "matmul plan: freeing its buffers failed");
   }
   delete p;
   return rc;

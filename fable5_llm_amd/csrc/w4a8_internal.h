@@ -260,8 +260,20 @@ struct MmPlanCfg {
   size_t lds;
 };
 size_t matmul_job_bytes();
+// ns[j] (out): job j's K slices; a job with ns[j] > 1 needs its reduction
+// buffers (zero) bound to its record before the first launch
 hipError_t matmul_plan_prepare(const MmJobSpec *jobs, int n, int32_t B, void *table,
-                               MmPlanCfg *cfg);
+                               MmPlanCfg *cfg, int32_t *ns);
+// part: int64 [ns][B][nrows], the slices' sums (overwritten by every launch)
+void matmul_plan_bind(void *table, int j, int64_t *part);
+// The split jobs' finishing records (matmul_finish_bytes() each, at most n)
+// from a bound table; returns their count.  launch_matmul_finish, after each
+// launch of the plan, adds the slices and stores y32 (max_n: the largest
+// B * nrows among them).
+size_t matmul_finish_bytes();
+int matmul_finish_prepare(const void *table, int n, int32_t B, void *fin);
+hipError_t launch_matmul_finish(const void *d_fin, int nf, int64_t max_n, int32_t *err,
+                                hipStream_t s);
 hipError_t launch_matmul_plan(const void *d_table, int n, const MmPlanCfg &cfg,
                               int32_t *err, hipStream_t s);
 hipError_t launch_matmul(const uint8_t *w, int32_t nrows, const Layout &L,

@@ -36,6 +36,8 @@
 // job boundaries, so the weight stream does not drain between matrices.  Every wait between wavefronts is bounded: a wait that gives
 // up sets bit 2 of the error word and an abort word, after which no wait of
 // the workgroup polls again, so a launch always drains.
+#include <vector>
+
 #include "w4a8_device.h"
 
 namespace w4a8 {
@@ -63,7 +65,26 @@ struct MmJob {
   int64_t tile_bytes;
   int32_t nrows, ntiles, NG, nblk, sh, K;
   int32_t tm;           // tiles per round
-  int32_t pad;
+  int32_t ns;           // K slices (1: none), see the split below
+  int64_t *part;        // split: [ns][B][nrows] each slice's sums (16 p)
+};
+
+// A split job (ns > 1; a matrix with at most one tile per workgroup) cuts
+// K into ns slices of nblk / ns blocks.  Workgroup r takes slice r % ns of
+// row tiles r / ns, r / ns + G / ns, ...: its rounds' tiles share one copy
+// of the slice's activations, and a workgroup reads only its slice, the
+// same one on every workgroup of its XCD (r % 8, with ns dividing 8).  Each
+// slice stores its sums to part; matmul_finish_kernel adds the ns slices,
+// rounds, checks and stores y32 after the launch.
+struct MmSlice {
+  int tr, tg, kb0, nbs;   // first row tile, row-tile stride, first block, blocks
+  __device__ MmSlice(const MmJob &J, int r, int G) {
+    const int ns = J.ns;
+    tr = r / ns;
+    tg = G / ns;
+    nbs = J.nblk / ns;
+    kb0 = (r - tr * ns) * nbs;
+  }
 };
 
 struct MmParams {
@@ -191,9 +212,10 @@ __device__ __forceinline__ int round_tiles(const MmJob &J, int nmine, int rho) {
 // job table and the schedule in LDS are read only when the job changes (a
 // read on every step puts its latency on every step).
 struct MmCur {
-  int j, rho, kb, RHO;
+  int j, rho, kb, RHO;     // kb: block of the slice (kb0 + kb of the matrix)
   int rend;                // first round past job j
   int nblk, tm, nmine, nt, NG, K;
+  int tr, tg, kb0;         // the workgroup's slice (MmSlice; nblk = its blocks)
   const uint8_t *W;
   const int8_t *x8;
   int64_t tile_bytes;
@@ -201,7 +223,11 @@ struct MmCur {
   __device__ void load(const MmFlags &F, int njobs, JobF &JOB) {
     if (j >= njobs) return;
     const MmJob &J = JOB(j);
-    nblk = J.nblk;
+    const MmSlice S(J, (int)blockIdx.x, (int)gridDim.x);
+    tr = S.tr;
+    tg = S.tg;
+    kb0 = S.kb0;
+    nblk = S.nbs;
     tm = J.tm;
     NG = J.NG;
     K = J.K;
@@ -244,9 +270,10 @@ __device__ __forceinline__ uint4 mm_issue(const MmCur &C, int r, int G, int w, i
                                           bool real) {
   const uint8_t *base = C.W;
   int len = 0;
-  if (real && 8 * C.kb + w < C.NG) {
-    const int64_t t = (int64_t)r + (int64_t)G * (C.rho * C.tm + j);
-    base = C.W + t * C.tile_bytes + (int64_t)C.kb * kBlockBytes + kScaleChunk +
+  const int kb = C.kb0 + C.kb;
+  if (real && 8 * kb + w < C.NG) {
+    const int64_t t = (int64_t)C.tr + (int64_t)C.tg * (C.rho * C.tm + j);
+    base = C.W + t * C.tile_bytes + (int64_t)kb * kBlockBytes + kScaleChunk +
            (int64_t)w * kGroupChunk;
     len = kGroupChunk;
   }
@@ -262,7 +289,7 @@ __device__ __forceinline__ uint4 mm_issue(const MmCur &C, int r, int G, int w, i
 // steps in flight per group wavefront: TMX pieces each (one tile a round,
 // as for a matrix with no more tiles than workgroups, goes 8 steps deep)
 template <int TMX, int CTX>
-constexpr int mm_depth() { return TMX >= 4 ? 4 : 8; }
+constexpr int mm_depth() { return TMX >= 3 ? 4 : 8; }
 
 template <int TMX, int CTX, bool kTab>
 __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
@@ -298,11 +325,12 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
   // thread j: job j's tiles, rounds and steps on this workgroup ...
   if (tid < P.njobs) {
     const MmJob &J = kTab ? P.tab[tid] : P.job[tid];
-    const int nm = r < J.ntiles ? (J.ntiles - 1 - r) / G + 1 : 0;
+    const MmSlice S(J, r, G);
+    const int nm = S.tr < J.ntiles ? (J.ntiles - 1 - S.tr) / S.tg + 1 : 0;
     const int nr = (nm + J.tm - 1) / J.tm;
     F.nmine[tid] = nm;
     F.rbase[tid + 1] = nr;
-    F.sbase[tid + 1] = nr * J.nblk;
+    F.sbase[tid + 1] = nr * S.nbs;
   }
   for (int i = tid; i < 2 * TMX * CTX * 4 * 64; i += kMThreads) tables[i] = 0;
   __syncthreads();
@@ -351,7 +379,8 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
       const int q = lane >> 4, c = lane & 15;
       // the job's fields, read once (kept in registers across the stores)
       int32_t *const yj = J.y32;
-      const int32_t nrj = J.nrows, shj = J.sh, tmj = J.tm;
+      const int32_t nrj = J.nrows, shj = J.sh, tmj = J.tm, nsj = J.ns;
+      const MmSlice S(J, r, G);
       const int64_t half = shj > 0 ? (int64_t)1 << (shj - 1) : 0;
       // every table entry read at once, then rounded, checked and stored
       int64_t tot[TMX][CTX][4];
@@ -370,23 +399,45 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
           for (int e = 0; e < 4; ++e)
             tbl[((jj * CTX + ct) * 4 + e) * 64 + lane] = 0;
       bool ovf = false;
+      // y = rshift_round(tot / 16, sh) (tot = 16 p): the magnitude rounded
+      // half up, checked and stored
+      auto put = [&](int64_t tt, int32_t *yp) {
+        const int64_t v = tt >> 4;
+        const int64_t m = ((v < 0 ? -v : v) + half) >> shj;
+        const int64_t y = v < 0 ? -m : m;
+        ovf = ovf || y > 2147483647LL || y < -2147483647LL;
+        *yp = (int32_t)y;
+      };
+      if (nsj == 1) {
 #pragma unroll
-      for (int ct = 0; ct < CTX; ++ct) {
-        const int tok = ct * 16 + c;
-        int32_t *const yt = yj + (int64_t)tok * nrj;
+        for (int ct = 0; ct < CTX; ++ct) {
+          const int tok = ct * 16 + c;
+          int32_t *const yt = yj + (int64_t)tok * nrj;
 #pragma unroll
-        for (int jj = 0; jj < TMX; ++jj) {
-          const int64_t row0 = ((int64_t)r + (int64_t)G * (rho * tmj + jj)) * kTileRows + 4 * q;
+          for (int jj = 0; jj < TMX; ++jj) {
+            const int64_t row0 =
+                ((int64_t)S.tr + (int64_t)S.tg * (rho * tmj + jj)) * kTileRows + 4 * q;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            // y = rshift_round(tot / 16, sh): the magnitude rounded half up
-            const int64_t v = tot[jj][ct][e] >> 4;   // tot = 16 p
-            const int64_t m = ((v < 0 ? -v : v) + half) >> shj;
-            const int64_t y = v < 0 ? -m : m;
-            if (jj < nt && ct < P.CT && tok < P.B && row0 + e < nrj) {
-              ovf = ovf || y > 2147483647LL || y < -2147483647LL;
-              yt[row0 + e] = (int32_t)y;
-            }
+            for (int e = 0; e < 4; ++e)
+              if (jj < nt && ct < P.CT && tok < P.B && row0 + e < nrj)
+                put(tot[jj][ct][e], yt + row0 + e);
+          }
+        }
+      } else {
+        // this slice's sums to its part of the job's partials, for
+        // matmul_finish_kernel
+        int64_t *const pj = J.part + (int64_t)(S.kb0 / S.nbs) * P.B * nrj;
+#pragma unroll
+        for (int ct = 0; ct < CTX; ++ct) {
+          const int tok = ct * 16 + c;
+#pragma unroll
+          for (int jj = 0; jj < TMX; ++jj) {
+            const int64_t row0 =
+                ((int64_t)S.tr + (int64_t)S.tg * (rho * tmj + jj)) * kTileRows + 4 * q;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (jj < nt && ct < P.CT && tok < P.B && row0 + e < nrj)
+                pj[(int64_t)tok * nrj + row0 + e] = tot[jj][ct][e];
           }
         }
       }
@@ -412,16 +463,17 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
             !mm_wait(F, [&] { return lds_read_i32(&F.done[lane & (kMW - 1)]) >= s - P.R; }))
           break;
         uint8_t *sb = ring + (size_t)slot * P.slot_bytes;
-        const int kbytes = min(1024, lc.K - lc.kb * 1024);   // multiple of 128
+        const int kb = lc.kb0 + lc.kb;
+        const int kbytes = min(1024, lc.K - kb * 1024);   // multiple of 128
         for (int tok = 0; tok < P.B; ++tok) {
           const int8_t *src = 16 * lane < kbytes
-                                  ? lc.x8 + (int64_t)tok * lc.K + lc.kb * 1024 + 16 * lane
+                                  ? lc.x8 + (int64_t)tok * lc.K + kb * 1024 + 16 * lane
                                   : lc.x8;   // nothing to copy: any mapped address
           dma16(src, lds_off(sb + tok * kXRow));
         }
         for (int j = 0; j < lc.nt; ++j) {
-          const int64_t t = (int64_t)r + (int64_t)G * (lc.rho * lc.tm + j);
-          dma4(lc.W + t * lc.tile_bytes + (int64_t)lc.kb * kBlockBytes + 4 * lane,
+          const int64_t t = (int64_t)lc.tr + (int64_t)lc.tg * (lc.rho * lc.tm + j);
+          dma4(lc.W + t * lc.tile_bytes + (int64_t)kb * kBlockBytes + 4 * lane,
                lds_off(sb + 16 * P.CT * kXRow + 256 * j));
         }
         mm_wait_vm_all();
@@ -541,11 +593,34 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
   }
 }
 
+// The rows of a split job: y32[tok][row] = rshift_round(sum over the ns
+// slices of part / 16, sh), checked as the direct path checks it.
+struct MmFinish {
+  const int64_t *part;   // [ns][B][nrows]
+  int32_t *y32;          // [B][nrows]
+  int64_t n;             // B * nrows
+  int32_t ns, sh;
+};
+
+__global__ __launch_bounds__(256) void matmul_finish_kernel(const MmFinish *fin, int32_t *err) {
+  const MmFinish &F = fin[blockIdx.y];
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= F.n) return;
+  int64_t tt = 0;
+  for (int k = 0; k < F.ns; ++k) tt += __builtin_nontemporal_load(F.part + k * F.n + i);
+  const int64_t half = F.sh > 0 ? (int64_t)1 << (F.sh - 1) : 0;
+  const int64_t v = tt >> 4;
+  const int64_t m = ((v < 0 ? -v : v) + half) >> F.sh;
+  const int64_t y = v < 0 ? -m : m;
+  if (y > 2147483647LL || y < -2147483647LL) atomicOr(err, 1);
+  F.y32[i] = (int32_t)y;
+}
+
 // The jobs' records and the launch shape for B tokens: the grid (one
 // workgroup per CU at most), tiles per round (TMX) and column tiles of 16
 // tokens (CTX) of the kernel instance, the LDS ring and its loaders.
 static hipError_t mm_setup(const MmJobSpec *jobs, int n, int32_t B, MmJob *out,
-                           MmPlanCfg &c) {
+                           MmPlanCfg &c, bool split) {
   if (n < 1 || B < 1 || B > 64) return hipErrorInvalidValue;
   c.B = B;
   c.CT = (B + 15) / 16;
@@ -568,18 +643,34 @@ static hipError_t mm_setup(const MmJobSpec *jobs, int n, int32_t B, MmJob *out,
     J.nblk = q.L.nblk;
     J.sh = q.sh;
     J.K = q.L.K;
+    J.ns = 1;
     maxt = J.ntiles > maxt ? J.ntiles : maxt;
   }
   const int G = maxt < ncu ? maxt : ncu;
-  // one tile per workgroup in every job: rounds of one tile, with the deeper
-  // weight pipeline of the one-tile kernels
-  int maxper = 1;
+  // A matrix with at most one tile per workgroup and enough tiles to give
+  // every workgroup one K slice of one (a 4096-row down projection on 256
+  // workgroups) is split into ns K slices when the caller has reduction
+  // buffers for it (a plan): ns = 4 for up to 16 tokens, 2 for up to 32.
+  const int ns_want = c.CT == 1 ? 4 : (c.CT == 2 ? 2 : 1);
+  std::vector<int> per(n);
   for (int j = 0; j < n; ++j) {
-    const int per = (out[j].ntiles + G - 1) / G;
-    maxper = per > maxper ? per : maxper;
+    MmJob &J = out[j];
+    per[j] = (J.ntiles + G - 1) / G;
+    if (split && ns_want > 1 && per[j] == 1 && J.nblk % ns_want == 0 && G % ns_want == 0 &&
+        J.ntiles * ns_want >= G) {
+      J.ns = ns_want;
+      per[j] = (J.ntiles + G / ns_want - 1) / (G / ns_want);
+    }
   }
+  // one tile per workgroup in every job: rounds of one tile, with the deeper
+  // weight pipeline of the one-tile kernels; three a workgroup at 17..32
+  // tokens (as a 12288-row matrix has on 256 workgroups): rounds of three, so
+  // that one copy of a block's activations serves all three
+  int maxper = 1;
+  for (int j = 0; j < n; ++j) maxper = per[j] > maxper ? per[j] : maxper;
   if (maxper == 1) tmx = 1;
-  const int ctxt = tmx == 4 ? 1 : (tmx == 2 ? 2 : (c.CT <= 2 ? c.CT : 4));
+  else if (c.CT == 2 && maxper == 3) tmx = 3;
+  const int ctxt = tmx == 4 ? 1 : (tmx >= 2 ? c.CT : (c.CT <= 2 ? c.CT : 4));
   const int table_bytes = 2 * tmx * ctxt * 4 * 64 * 8;
   c.slot_bytes = 16 * c.CT * kXRow + tmx * 256;
   const int avail = kLdsBytes - kFlagBytes - table_bytes;
@@ -589,10 +680,7 @@ static hipError_t mm_setup(const MmJobSpec *jobs, int n, int32_t B, MmJob *out,
   c.nl = c.R - 1 < kML ? c.R - 1 : kML;   // >= 1: R >= 2
   // rounds of tm tiles: as many tiles per round as the workgroups' shares
   // of the job allow, at most tmx
-  for (int j = 0; j < n; ++j) {
-    const int per = (out[j].ntiles + G - 1) / G;
-    out[j].tm = per < tmx ? per : tmx;
-  }
+  for (int j = 0; j < n; ++j) out[j].tm = per[j] < tmx ? per[j] : tmx;
   c.G = G;
   c.tmx = tmx;
   c.ctxt = ctxt;
@@ -606,6 +694,9 @@ static hipError_t mm_set_lds_limit() {
                                      hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
   if (e == hipSuccess)
     e = hipFuncSetAttribute((const void *)matmul_kernel<2, 2, kTab>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+  if (e == hipSuccess)
+    e = hipFuncSetAttribute((const void *)matmul_kernel<3, 2, kTab>,
                             hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
   if (e == hipSuccess)
     e = hipFuncSetAttribute((const void *)matmul_kernel<1, 4, kTab>,
@@ -627,6 +718,8 @@ static hipError_t mm_launch(const MmParams &P, const MmPlanCfg &c, hipStream_t s
   const dim3 g(c.G), b(kMThreads);
   if (c.tmx == 4) {
     hipLaunchKernelGGL((matmul_kernel<4, 1, kTab>), g, b, c.lds, s, P);
+  } else if (c.tmx == 3) {
+    hipLaunchKernelGGL((matmul_kernel<3, 2, kTab>), g, b, c.lds, s, P);
   } else if (c.tmx == 2) {
     hipLaunchKernelGGL((matmul_kernel<2, 2, kTab>), g, b, c.lds, s, P);
   } else if (c.ctxt == 1) {
@@ -654,9 +747,38 @@ static void mm_params(MmParams &P, int n, const MmPlanCfg &c, int32_t *err) {
 size_t matmul_job_bytes() { return sizeof(MmJob); }
 
 hipError_t matmul_plan_prepare(const MmJobSpec *jobs, int n, int32_t B, void *table,
-                               MmPlanCfg *cfg) {
-  if (n < 1 || n > kMmPlanJobs || !table || !cfg) return hipErrorInvalidValue;
-  return mm_setup(jobs, n, B, (MmJob *)table, *cfg);
+                               MmPlanCfg *cfg, int32_t *ns) {
+  if (n < 1 || n > kMmPlanJobs || !table || !cfg || !ns) return hipErrorInvalidValue;
+  const hipError_t e = mm_setup(jobs, n, B, (MmJob *)table, *cfg, true);
+  for (int j = 0; e == hipSuccess && j < n; ++j) ns[j] = ((const MmJob *)table)[j].ns;
+  return e;
+}
+
+void matmul_plan_bind(void *table, int j, int64_t *part) { ((MmJob *)table)[j].part = part; }
+
+size_t matmul_finish_bytes() { return sizeof(MmFinish); }
+
+int matmul_finish_prepare(const void *table, int n, int32_t B, void *fin) {
+  int nf = 0;
+  for (int j = 0; j < n; ++j) {
+    const MmJob &J = ((const MmJob *)table)[j];
+    if (J.ns <= 1) continue;
+    MmFinish &f = ((MmFinish *)fin)[nf++];
+    f.part = J.part;
+    f.y32 = J.y32;
+    f.n = (int64_t)B * J.nrows;
+    f.ns = J.ns;
+    f.sh = J.sh;
+  }
+  return nf;
+}
+
+hipError_t launch_matmul_finish(const void *d_fin, int nf, int64_t max_n, int32_t *err,
+                                hipStream_t s) {
+  if (nf < 1) return hipSuccess;
+  const dim3 g((unsigned)((max_n + 255) / 256), (unsigned)nf);
+  hipLaunchKernelGGL(matmul_finish_kernel, g, dim3(256), 0, s, (const MmFinish *)d_fin, err);
+  return hipGetLastError();
 }
 
 hipError_t launch_matmul_plan(const void *d_table, int n, const MmPlanCfg &cfg, int32_t *err,
@@ -673,7 +795,7 @@ hipError_t launch_matmul_multi(const MmJobSpec *jobs, int n, int32_t B, int32_t 
   if (n < 1 || n > kMmJobs) return hipErrorInvalidValue;
   MmParams P{};
   MmPlanCfg c{};
-  hipError_t e = mm_setup(jobs, n, B, P.job, c);
+  hipError_t e = mm_setup(jobs, n, B, P.job, c, false);
   if (e != hipSuccess) return e;
   mm_params(P, n, c, err);
   return mm_launch<false>(P, c, s);

@@ -398,13 +398,16 @@ def test_matmul_plan_one_launch(engine, B):
     path holds; shapes from 40 x 256 to 4096 x 12288, several sharing x8)
     in one launch: every output equal to the per-launch path's (itself
     checked per token above) and the oracle's on three tokens; a second run
-    on overwritten outputs and graph replays give the same."""
+    on overwritten outputs and graph replays give the same.  Up to 32 tokens
+    the 4096- and 4000-row matrices (and at 17..32 the 2048-row one) run
+    split into K slices whose sums meet across workgroups, so the reruns and
+    replays also check that a run leaves its reduction buffers zero."""
     import torch
     from fable5_llm_amd.engine import MatmulPlan
     rng = np.random.default_rng(4100 + B)
     dev = torch.device("cuda", 0)
     base = [(12288, 4096), (4096, 12288), (40, 256), (100, 1024), (33, 3584), (2048, 2048),
-            (777, 4096), (16, 128)]
+            (777, 4096), (16, 128), (4000, 12288)]
     shapes = [base[i % len(base)] for i in range(40)]
     ws, imgs = {}, {}
     for N_, K in set(shapes):
