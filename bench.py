@@ -160,6 +160,11 @@ def time_passes(ctx, one_pass, stream, steps, warmup):
     return timed(g.replay), eager, "HIP graph of one pass"
 
 
+def _plain(o):
+    """numpy scalars and arrays in a JSON line"""
+    return o.item() if hasattr(o, "item") and getattr(o, "size", 1) == 1 else o.tolist()
+
+
 def batched_leg(st, ctx, batches, steps, warmup, seed):
     """The FFN matrices of the stream (32 x gate, up: 12288 x 4096; down:
     4096 x 12288; 2.49 GB, far beyond the 256 MB Infinity Cache) through the
@@ -228,7 +233,11 @@ def batched_leg(st, ctx, batches, steps, warmup, seed):
                     "pct_of_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 1),
                     "tops": round(tops, 2),
                     "mfma_util_pct": round(100.0 * tops / PEAK_INT8_TOPS, 2),
-                    "bytes_per_pass": nbytes, "kernel": "matmul_kernel (matmul plan)",
+                    "mfma_util_basis": "algorithmic int8 ops / time / 5.0 POP/s; matrix-core "
+                                       "busy cycles (SQ_VALU_MFMA_BUSY_CYCLES) in "
+                                       "profiles/matmul_kernel_ffn_b8_b32.md",
+                    "bytes_per_pass": nbytes,
+                    "kernel": "matmul_kernel + matmul_finish_kernel (matmul plan)",
                     "launches_per_pass": 1,
                     "per_site_launches": {"launches_per_pass": len(sites),
                                           "ms_per_pass": round(ms_site, 4),
@@ -650,6 +659,8 @@ def main():
     ap.add_argument("--batch", default="8,32",
                     help="token counts B for the batched int8-MFMA leg over the FFN "
                          "matrices (comma-separated, each <= 64; empty: skip)")
+    ap.add_argument("--only-batched", action="store_true",
+                    help="run the batched leg alone (for profiling it) and print its results")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -688,6 +699,15 @@ def main():
     ctx.sync()
     t_build = time.perf_counter() - t_build
     tot = stream9b.totals(st.sites)
+    if args.only_batched:
+        batches = [int(b) for b in args.batch.split(",") if b.strip()]
+        log("batched leg alone")
+        res, keep = batched_leg(st, ctx, batches, args.steps, args.warmup, args.seed)
+        print(json.dumps({"batched": res, "batched_parity": batched_check(st, keep)},
+                         default=_plain), flush=True)
+        st.close()
+        ctx.close()
+        return
 
     import numpy as np
     log("timing the headline step")
@@ -824,9 +844,7 @@ def main():
         stc.close()
     st.close()
     ctx.close()
-    def plain(o):   # numpy scalars and arrays in the line
-        return o.item() if hasattr(o, "item") and getattr(o, "size", 1) == 1 else o.tolist()
-    print(json.dumps(line, default=plain), flush=True)
+    print(json.dumps(line, default=_plain), flush=True)
 
 
 if __name__ == "__main__":
