@@ -256,12 +256,21 @@ def batched_leg(st, ctx, batches, steps, warmup, seed):
 
 
 def ffn_leg(st, ctx, steps, warmup):
-    """One decoder layer's FFN block per call (w4a8_mlp_async: RMSNorm ->
-    DYNQ8 -> gate SILU32 / up SHIFT32W -> EMUL32 -> DYNQ8 -> down -> residual
-    ADD) for each of the stream's 32 layers in turn: 77.9 MB of weights per
-    call, 2.49 GB per pass.  Returns the timing and, for the checker, layer
-    0's input and outputs."""
+    """The stream's 32 decoder-layer FFN blocks (RMSNorm -> DYNQ8 -> gate
+    SILU32 / up SHIFT32W -> EMUL32 -> DYNQ8 -> down -> residual ADD), each
+    on its own layer's input: 77.9 MB of weights per block, 2.49 GB per
+    pass, timed three ways:
+      * one persistent plan, each layer's down site right after its gate and
+        up site (waiting for the EMUL32 product's words): the leg's value;
+      * the same plan with each layer's down site after the next layer's
+        gate and up site (the product is complete before it is needed);
+      * w4a8_mlp_async per layer (two launches each), as one HIP graph.
+    Every layer's block output and residual must be identical across the
+    three.  Returns the timings and, for the checker, layer 0's input and
+    outputs."""
     import torch
+    from fable5_llm_amd import _native as N
+    from fable5_llm_amd.engine import Plan
     dev = torch.device("cuda", ctx.device)
     stream = torch.cuda.current_stream(dev)
     layers = []
@@ -273,29 +282,92 @@ def ffn_leg(st, ctx, steps, warmup):
             d = down.mats[0]
             p0s = [g.p0(s.in_f), u.p0(s.in_f), d.p0(down.in_f)]
             x, nw = st.inputs[si]
-            y = torch.empty(d.nrows, dtype=torch.int16, device=dev)
-            res = torch.empty(d.nrows, dtype=torch.int16, device=dev)
             nbytes = g.bytes + u.bytes + d.bytes
             layers.append((si, st.weights[si][0], st.weights[si][1], st.weights[si + 1][0],
-                           p0s, x, nw, s, y, res, nbytes))
+                           p0s, x, nw, s, nbytes))
+    nbytes = sum(l[-1] for l in layers)
+    outs = {}
+
+    def new_outs(tag):
+        outs[tag] = [(torch.empty(l[3].nrows, dtype=torch.int16, device=dev),
+                      torch.empty(l[3].nrows, dtype=torch.int16, device=dev)) for l in layers]
+        return outs[tag]
+
+    o_l = new_outs("launches")
 
     def one_pass():
-        for (_si, wg, wu, wd, p0s, x, nw, s, y, res, _b) in layers:
+        for (_si, wg, wu, wd, p0s, x, nw, s, _b), (y, res) in zip(layers, o_l):
             ctx.mlp_async(wg, wu, wd, p0s, x, norm_w=nw, in_f=s.in_f,
                           one_plus=s.one_plus, mlp_out=y, res_out=res)
 
-    ms, ms_eager, how = time_passes(ctx, one_pass, stream, steps, warmup)
-    nbytes = sum(l[-1] for l in layers)
-    si, wg, wu, wd, p0s, x, nw, s, y, res, _ = layers[0]
-    keep = (si, p0s, x.cpu().numpy(), nw.cpu().numpy(), y.cpu().numpy(), res.cpu().numpy())
-    return {"layers": len(layers), "ms_per_pass": round(ms, 4),
-            "ms_per_pass_eager": round(ms_eager, 4), "timing": how,
-            "us_per_layer": round(ms * 1e3 / len(layers), 2),
-            "value": round(nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s",
-            "pct_of_peak_hbm": round(100.0 * nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 1),
-            "bytes_per_pass": nbytes, "launches_per_layer": 2,
-            "chain": "RMSNorm->DYNQ8->gate SILU32 + up SHIFT32W (one launch); "
-                     "EMUL32->DYNQ8->down SHIFT32->residual ADD (one launch)"}, keep
+    ms_l, ms_l_eager, how_l = time_passes(ctx, one_pass, stream, steps, warmup)
+
+    def plan_of(interleave):
+        o = new_outs("interleaved" if interleave else "in_order")
+        plan = Plan(ctx)
+        if not interleave:
+            for (_si, wg, wu, wd, p0s, x, nw, s, _b), (y, res) in zip(layers, o):
+                plan.add_mlp(wg, wu, wd, p0s, x, norm_w=nw, in_f=s.in_f, one_plus=s.one_plus,
+                             mlp_out=y, res_out=res)
+        else:
+            tmp = [(torch.empty(l[1].nrows, dtype=torch.int16, device=dev),
+                    torch.empty(l[1].nrows, dtype=torch.int32, device=dev)) for l in layers]
+
+            def up(i):
+                _si, wg, wu, _wd, p0s, x, nw, s, _b = layers[i]
+                plan.add_site([wg, wu], [N.EPI_SILU32, N.EPI_MOVY_P32], p0s[:2], list(tmp[i]),
+                              x, prologue=N.PRO_RMSNORM_DYNQ8, norm_w=nw, in_f=s.in_f,
+                              one_plus=s.one_plus)
+
+            def down(i):
+                _si, _wg, _wu, wd, p0s, x, _nw, _s, _b = layers[i]
+                plan.add_site_emul_res(wd, p0s[2], tmp[i][0], tmp[i][1], x, o[i][1],
+                                       out=o[i][0])
+            up(0)
+            for i in range(1, len(layers)):
+                up(i)
+                down(i - 1)
+            down(len(layers) - 1)
+            plan._keep.append(tmp)
+        plan.set_mode(N.PLAN_PERSISTENT)
+        plan.set_fences(N.FENCE_AUTO)
+        return plan
+
+    res = {}
+    for tag, inter in (("in_order", False), ("interleaved", True)):
+        plan = plan_of(inter)
+        fenced = plan.fenced()
+        plan.run()
+        ctx.sync()
+        ms, _e, how = time_passes(ctx, plan.run, stream, steps, warmup)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[tag] = {"ms_per_pass": round(ms, 4), "value": round(gbs, 1), "unit": "GB/s",
+                    "pct_of_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 1), "timing": how,
+                    "launches_per_pass": 1,
+                    "waits": {"input": fenced.count(N.WAIT_INPUT),
+                              "grid": fenced.count(N.WAIT_GRID)}}
+        plan.close()
+    same = all(torch.equal(a, b) for tag in ("in_order", "interleaved")
+               for la, lb in zip(outs["launches"], outs[tag]) for a, b in zip(la, lb))
+    gbs_l = nbytes / (ms_l * 1e-3) / 1e9
+    si, wg, wu, wd, p0s, x, nw, s, _ = layers[0]
+    y, r = outs["in_order"][0]
+    keep = (si, p0s, x.cpu().numpy(), nw.cpu().numpy(), y.cpu().numpy(), r.cpu().numpy())
+    io = res["in_order"]
+    return {"layers": len(layers), "ms_per_pass": io["ms_per_pass"],
+            "us_per_layer": round(io["ms_per_pass"] * 1e3 / len(layers), 2),
+            "value": io["value"], "unit": "GB/s", "pct_of_peak_hbm": io["pct_of_peak_hbm"],
+            "bytes_per_pass": nbytes,
+            "kernel": "stream_kernel (persistent plan, fences from buffers)",
+            "interleaved": res["interleaved"],
+            "per_layer_launches": {"ms_per_pass": round(ms_l, 4),
+                                   "ms_per_pass_eager": round(ms_l_eager, 4), "timing": how_l,
+                                   "value": round(gbs_l, 1),
+                                   "pct_of_peak_hbm": round(100.0 * gbs_l / PEAK_HBM_GBS, 1),
+                                   "launches_per_layer": 2},
+            "waits": io["waits"], "outputs_identical_across_the_three": bool(same),
+            "chain": "RMSNorm->DYNQ8->gate SILU32 + up SHIFT32W (one site; EMUL32 formed "
+                     "as stored); EMUL32->DYNQ8->down SHIFT32->residual ADD (one site)"}, keep
 
 
 def head_leg(st, ctx, steps, warmup):

@@ -74,6 +74,8 @@ SIGNATURES = {
     "w4a8_plan_add_site": [_P, _I32, _PP, _P, _P, _PP, _I32, _P, _P, _I32, _I32,
                            _I32, _P, _P, _P],
     "w4a8_plan_add_site_emul": [_P, _I32, _PP, _P, _P, _PP, _P, _P, _P, _P],
+    "w4a8_plan_add_site_emul_res": [_P, _P, _I32, _P, _P, _P, _P, _P],
+    "w4a8_plan_add_mlp": [_P, _P, _P, _P, _I32, _I32, _I32, _P, _P, _I32, _I32, _P, _P],
     "w4a8_plan_add_head": [_P, _P, _I32, _P, _P, _I32, _I32, _I32, _P],
     "w4a8_plan_set_mode": [_P, _I32],
     "w4a8_plan_set_fences": [_P, _I32],

@@ -1176,6 +1176,7 @@ struct w4a8_plan {
   int8_t *d_stage = nullptr;
   uint64_t *d_stamped = nullptr;    // stamped words of outputs read through them
   int64_t stamped_words = 0;
+  std::vector<void *> temps;        // temporaries of the MLP blocks added (w4a8_plan_add_mlp)
   bool dependent = false;           // some site waits for, or forms, others' results
   int G = 0;
   int head_site = -1;
@@ -1215,6 +1216,7 @@ static void step_ranges(const w4a8_plan::Step &st, std::vector<ByteRange> &rd,
     int64_t es = 0;
     switch (J.epi) {
       case EPI_MOVY_I16:
+      case EPI_MOVY_I16_ADD:
       case EPI_SILU32: es = 2; break;
       case EPI_Y32:
       case EPI_MOVY_P32: es = 4; break;
@@ -1222,6 +1224,10 @@ static void step_ranges(const w4a8_plan::Step &st, std::vector<ByteRange> &rd,
       default: es = 0; break;   // EPI_ARGMAX writes the head result below
     }
     add(wr, J.out, es * J.nrows);
+    if (J.epi == EPI_MOVY_I16_ADD) {
+      add(rd, J.res, 2 * (int64_t)J.nrows);
+      add(wr, J.res_out, 2 * (int64_t)J.nrows);
+    }
   }
   add(wr, P.x8_out, P.K);
   add(wr, P.e_x_out, 4);
@@ -1281,8 +1287,13 @@ static StampSrc stamp_source(const std::vector<GemvParams> &sites,
   for (int j = from; j < i; ++j)
     for (int k = 0; k < sites[j].njobs; ++k) {
       const GemvJob &J = sites[j].job[k];
-      if ((J.epi != EPI_MOVY_I16 && J.epi != EPI_SILU32) || J.nrows % 2) continue;
-      const uintptr_t lo = (uintptr_t)J.out, hi = lo + 2 * (uintptr_t)J.nrows;
+      if ((J.epi != EPI_MOVY_I16 && J.epi != EPI_SILU32 && J.epi != EPI_MOVY_I16_ADD) ||
+          J.nrows % 2)
+        continue;
+      // a residual ADD's stamped words carry its res_out
+      const uintptr_t lo = (uintptr_t)(J.epi == EPI_MOVY_I16_ADD ? (const void *)J.res_out
+                                                                  : J.out);
+      const uintptr_t hi = lo + 2 * (uintptr_t)J.nrows;
       if (x.lo >= lo && x.hi <= hi && (x.lo - lo) % 4 == 0) {
         got.site = j;
         got.job = k;
@@ -1514,6 +1525,64 @@ int w4a8_plan_add_site_emul(w4a8_plan *p, int32_t nmat, const w4a8_weights *cons
   return W4A8_OK;
 }
 
+int w4a8_plan_add_site_emul_res(w4a8_plan *p, const w4a8_weights *down, int32_t p0,
+                                int16_t *d_out, const int16_t *d_x, const int32_t *d_x2,
+                                const int16_t *d_res, int16_t *d_res_out) {
+  if (!p || !down || !d_res || !d_res_out) return fail(W4A8_E_ARG, "null argument");
+  if (!d_x2 || !aligned16(d_x2)) return fail(W4A8_E_ARG, "x2 must be a 16-byte aligned pointer");
+  w4a8_plan::Step st{};
+  const int32_t epi = EPI_MOVY_I16;
+  void *out = d_res_out;
+  int rc = site_params(p->ctx, st.P, 1, &down, &epi, &p0, &out, PRO_DYNQ8, d_x, nullptr, 0, 0,
+                       0, nullptr, nullptr, nullptr);
+  if (rc) return rc;
+  st.P.pro = PRO_EMUL_DYNQ8;
+  st.P.x2 = d_x2;
+  st.P.job[0].epi = EPI_MOVY_I16_ADD;
+  st.P.job[0].out = d_out;
+  st.P.job[0].res = d_res;
+  st.P.job[0].res_out = d_res_out;
+  st.grid = grid_for(p->ctx, st.P.total_tiles);
+  st.head = false;
+  st.result = nullptr;
+  p->steps.push_back(st);
+  plan_drop_graph(p);
+  return W4A8_OK;
+}
+
+int w4a8_plan_add_mlp(w4a8_plan *p, const w4a8_weights *gate, const w4a8_weights *up,
+                      const w4a8_weights *down, int32_t p0_gate, int32_t p0_up,
+                      int32_t p0_down, const int16_t *d_x16, const int16_t *d_norm_w,
+                      int32_t in_f, int32_t one_plus, int16_t *d_mlp_out, int16_t *d_res_out) {
+  if (!p || !gate || !up || !down || !d_x16) return fail(W4A8_E_ARG, "null argument");
+  const int64_t H = gate->L.K, FFN = gate->nrows;
+  if (up->L.K != H || up->nrows != FFN || down->L.K != FFN || down->nrows != H)
+    return fail(W4A8_E_ARG, "gate and up must be FFN x H and down H x FFN");
+  if (!d_mlp_out && !d_res_out) return fail(W4A8_E_ARG, "mlp: no output requested");
+  // the layer's temporaries, owned by the plan: sg int16[FFN], u int32[FFN]
+  DeviceGuard g(p->ctx->device);
+  uint8_t *tmp = nullptr;
+  const size_t o_u = ((size_t)2 * FFN + 255) & ~(size_t)255;
+  HIP_TRY(hipMalloc(&tmp, o_u + (size_t)4 * FFN));
+  p->temps.push_back(tmp);
+  int16_t *sg = (int16_t *)tmp;
+  int32_t *u = (int32_t *)(tmp + o_u);
+  const w4a8_weights *gu[2] = {gate, up};
+  const int32_t epi_gu[2] = {EPI_SILU32, EPI_MOVY_P32};
+  const int32_t p0_gu[2] = {p0_gate, p0_up};
+  void *out_gu[2] = {sg, u};
+  int rc = w4a8_plan_add_site(p, 2, gu, epi_gu, p0_gu, out_gu,
+                              d_norm_w ? PRO_RMSNORM_DYNQ8 : PRO_DYNQ8, d_x16, d_norm_w, in_f,
+                              one_plus, 0, nullptr, nullptr, nullptr);
+  if (rc) return rc;
+  if (!d_res_out) {
+    const int32_t epi = EPI_MOVY_I16;
+    void *out = d_mlp_out;
+    return w4a8_plan_add_site_emul(p, 1, &down, &epi, &p0_down, &out, sg, u, nullptr, nullptr);
+  }
+  return w4a8_plan_add_site_emul_res(p, down, p0_down, d_mlp_out, sg, u, d_x16, d_res_out);
+}
+
 int w4a8_plan_add_head(w4a8_plan *p, const w4a8_weights *w, int32_t prologue,
                        const void *d_x, const int16_t *d_norm_w, int32_t in_f,
                        int32_t one_plus, int32_t e_x, int32_t *d_result) {
@@ -1705,6 +1774,7 @@ int w4a8_plan_destroy(w4a8_plan *p) {
   (void)hipStreamSynchronize(p->ctx->stream);
   plan_drop_graph(p);
   if (p->d_partials) (void)hipFree(p->d_partials);
+  for (void *t : p->temps) (void)hipFree(t);
   delete p;
   return W4A8_OK;
 }

@@ -48,8 +48,8 @@ constexpr int kWaves = kWG / 64;
 // 12)) with x int16 (SILU32 of the gate) and x2 int32 (the up projection),
 // i.e. ALU EMUL32 at p0 = 12, then DYNQ8.
 enum Prologue { PRO_X8 = 0, PRO_DYNQ8 = 1, PRO_RMSNORM_DYNQ8 = 2, PRO_EMUL_DYNQ8 = 3 };
-// EPI_MOVY_I16_ADD (gemv_kernel only): EPI_MOVY_I16 into out (when set),
-// and clip16(res[row] + that) into res_out (ALU ADD, the block's residual).
+// EPI_MOVY_I16_ADD: EPI_MOVY_I16 into out (when set), and
+// clip16(res[row] + that) into res_out (ALU ADD, the block's residual).
 enum Epilogue {
   EPI_Y32 = 0, EPI_MOVY_I16 = 1, EPI_MOVY_P32 = 2, EPI_SILU32 = 3,
   EPI_SHIFT_I64 = 4, EPI_ARGMAX = 5, EPI_MOVY_I16_ADD = 6

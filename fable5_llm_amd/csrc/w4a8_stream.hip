@@ -276,7 +276,10 @@ __device__ __forceinline__ void tile_epilogue(Lds &L, int kt, CJob &J, int tl, i
       const int shift = J.p0 - e_x;
       switch (J.epi) {
         case EPI_Y32: outv = y; break;
-        case EPI_MOVY_I16: outv = clamp64(movy_shift(y, shift), -32768, 32767); break;
+        case EPI_MOVY_I16:
+        case EPI_MOVY_I16_ADD:   // the residual ADD is applied as it is stored
+          outv = clamp64(movy_shift(y, shift), -32768, 32767);
+          break;
         case EPI_MOVY_P32:
           outv = clamp64(movy_shift(y, shift), -2147483648LL, 2147483647LL);
           break;
@@ -321,6 +324,26 @@ __device__ void ctrl_serve(CSite &P, Lds &L, int kt0, int r, int G, int lane, ui
       continue;
     }
     lds_wait_eq(L, &L.tready[slot], kt + 1, lane, lspin);
+    const bool add = J.epi == EPI_MOVY_I16_ADD;
+    if (add) {
+      // MOVY int16 into out (when set), and the block's residual ALU ADD
+      // clip16(res + that) into res_out (gen_layer_script.py:1399-1400); the
+      // stamped words, if any, carry the residual
+      if (lane < kTileRows) {
+        const int64_t v = L.tv[slot][lane];
+        const int row = (t - J.tile0) * kTileRows + lane;
+        if (row < J.nrows) {
+          if (J.out) store_coherent((int16_t *)J.out + row, (int16_t)v);
+          const int64_t rv =
+              clamp64(v + __hip_atomic_load(J.res + row, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT),
+                      -32768, 32767);
+          store_coherent(J.res_out + row, (int16_t)rv);
+          L.tv[slot][lane] = rv;
+        }
+      }
+      wait_lds();
+    }
     if (kDep && J.stamped && lane < kTileRows / 2) {
       // rows 2l and 2l + 1 (int16 epilogues); nrows is even
       const int row = (t - J.tile0) * kTileRows + 2 * lane;
@@ -332,7 +355,7 @@ __device__ void ctrl_serve(CSite &P, Lds &L, int kt0, int r, int G, int lane, ui
     if (lane < kTileRows) {
       const int64_t v = L.tv[slot][lane];
       const int row = (t - J.tile0) * kTileRows + lane;
-      if (row < J.nrows) {
+      if (row < J.nrows && !add) {
         switch (J.epi) {
           case EPI_MOVY_I16:
           case EPI_SILU32: store_coherent((int16_t *)J.out + row, (int16_t)v); break;

@@ -474,6 +474,42 @@ class Plan:
         self.nsites += 1
         self.nmats += n
 
+    def add_site_emul_res(self, down, p0, x, x2, res, res_out, out=None):
+        """The SwiGLU product site with the block's residual ADD: down over
+        DYNQ8(EMUL32(x2, x; 12)), MOVY int16 at p0 into out (optional) and
+        clip16(res + that) into res_out."""
+        H = down.nrows
+        _dev(x, 2 * down.K, "x")
+        _dev(x2, 4 * down.K, "x2")
+        _dev(res, 2 * H, "res")
+        _dev(res_out, 2 * H, "res_out")
+        _dev(out, 2 * H, "out", required=False)
+        N.check(N.lib().w4a8_plan_add_site_emul_res(
+            self.h, down.h, int(p0), _dptr(out), _dptr(x), _dptr(x2), _dptr(res),
+            _dptr(res_out)), "plan_add_site_emul_res")
+        self._keep += [down, x, x2, res, res_out, out]
+        self.bytes += down.wire_bytes
+        self.nsites += 1
+        self.nmats += 1
+
+    def add_mlp(self, gate, up, down, p0s, x16, norm_w=None, in_f=0, one_plus=False,
+                mlp_out=None, res_out=None):
+        """A layer's FFN block as two sites (the arguments of
+        Context.mlp_async); its temporaries belong to the plan."""
+        pg, pu, pd = (int(p) for p in p0s)
+        H = gate.K
+        _dev(x16, 2 * H, "x16")
+        _dev(norm_w, 2 * H, "norm_w", required=False)
+        _dev(mlp_out, 2 * H, "mlp_out", required=False)
+        _dev(res_out, 2 * H, "res_out", required=False)
+        N.check(N.lib().w4a8_plan_add_mlp(
+            self.h, gate.h, up.h, down.h, pg, pu, pd, _dptr(x16), _dptr(norm_w), int(in_f),
+            1 if one_plus else 0, _dptr(mlp_out), _dptr(res_out)), "plan_add_mlp")
+        self._keep += [gate, up, down, x16, norm_w, mlp_out, res_out]
+        self.bytes += gate.wire_bytes + up.wire_bytes + down.wire_bytes
+        self.nsites += 2
+        self.nmats += 3
+
     def add_head(self, w, x, result, prologue=N.PRO_DYNQ8, e_x=0, norm_w=None,
                  in_f=0, one_plus=False):
         _dev(x, _x_bytes(prologue, w.K), "x")

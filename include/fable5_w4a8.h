@@ -333,6 +333,25 @@ int w4a8_plan_add_site_emul(w4a8_plan *plan, int32_t nmat,
                             const w4a8_weights *const *w, const int32_t *epilogue,
                             const int32_t *p0, void *const *d_out, const int16_t *d_x,
                             const int32_t *d_x2, int8_t *d_x8_out, int32_t *d_e_x_out);
+/* The SwiGLU product site with the block's residual ADD: down (H x FFN)
+ * over DYNQ8(EMUL32(x2, x; 12)) as w4a8_plan_add_site_emul, MOVY int16 at
+ * p0 into d_out (may be null) and clip16(res + that) into d_res_out; the
+ * down launch of w4a8_mlp_async (gen_layer_script.py:2166-2190,
+ * 1399-1400) as a plan site.  No counterpart in the reference's C
+ * interface (its sequencer issues the block as records). */
+int w4a8_plan_add_site_emul_res(w4a8_plan *plan, const w4a8_weights *down,
+                                int32_t p0, int16_t *d_out, const int16_t *d_x,
+                                const int32_t *d_x2, const int16_t *d_res,
+                                int16_t *d_res_out);
+/* A layer's whole FFN block as two plan sites: w4a8_mlp_async's arguments
+ * (layer_fixed.py:1597-1604 mlp_fx), its temporaries owned by the plan.
+ * In a persistent plan the gate and up site forms the EMUL32 product as it
+ * stores and the down site waits for the product's words. */
+int w4a8_plan_add_mlp(w4a8_plan *plan, const w4a8_weights *gate,
+                      const w4a8_weights *up, const w4a8_weights *down,
+                      int32_t p0_gate, int32_t p0_up, int32_t p0_down,
+                      const int16_t *d_x16, const int16_t *d_norm_w, int32_t in_f,
+                      int32_t one_plus, int16_t *d_mlp_out, int16_t *d_res_out);
 int w4a8_plan_add_head(w4a8_plan *plan, const w4a8_weights *w,
                        int32_t prologue, const void *d_x,
                        const int16_t *d_norm_w, int32_t in_f, int32_t one_plus,
