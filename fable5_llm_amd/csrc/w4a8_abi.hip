@@ -1420,6 +1420,12 @@ static int plan_build_persistent(w4a8_plan *p) {
                                           : nullptr;
     // a site reading a product formed by its producer is a DYNQ8 site of it
     if (src[i].job == kProduct) sites[i].pro = PRO_DYNQ8;
+    // stream_kernel's residual ADD: an EPI_MOVY_I16 job with res_out set
+    for (int k = 0; k < sites[i].njobs; ++k) {
+      GemvJob &J = sites[i].job[k];
+      if (J.epi == EPI_MOVY_I16_ADD) J.epi = EPI_MOVY_I16;
+      else J.res_out = nullptr;
+    }
   }
   p->epoch = 0;
   HIP_TRY(hipMemcpy(p->d_sites, sites.data(), sizeof(GemvParams) * (size_t)n,

@@ -102,7 +102,8 @@ struct GemvJob {
   int32_t p0;         // epilogue shift = p0 - e_x
   int32_t pad_;
   const int16_t *res;   // EPI_MOVY_I16_ADD: residual input
-  int16_t *res_out;     // EPI_MOVY_I16_ADD: residual output
+  int16_t *res_out;     // EPI_MOVY_I16_ADD: residual output (stream_kernel: an
+                        // EPI_MOVY_I16 job with res_out set adds the residual)
   uint64_t *stamped;    // persistent stream, int16 outputs read by a later site
                         // through stamped words: word i = rows 2i, 2i+1 (low 32
                         // bits) and the producing site's stamp (high 32 bits)

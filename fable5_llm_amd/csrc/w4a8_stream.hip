@@ -276,10 +276,7 @@ __device__ __forceinline__ void tile_epilogue(Lds &L, int kt, CJob &J, int tl, i
       const int shift = J.p0 - e_x;
       switch (J.epi) {
         case EPI_Y32: outv = y; break;
-        case EPI_MOVY_I16:
-        case EPI_MOVY_I16_ADD:   // the residual ADD is applied as it is stored
-          outv = clamp64(movy_shift(y, shift), -32768, 32767);
-          break;
+        case EPI_MOVY_I16: outv = clamp64(movy_shift(y, shift), -32768, 32767); break;
         case EPI_MOVY_P32:
           outv = clamp64(movy_shift(y, shift), -2147483648LL, 2147483647LL);
           break;
@@ -304,6 +301,27 @@ __device__ __forceinline__ void tile_epilogue(Lds &L, int kt, CJob &J, int tl, i
 }
 
 // ------------------------------------------------------------- control
+// A residual-ADD tile's stores: MOVY int16 into out (when set), and the
+// block's residual ALU ADD clip16(res + that) into res_out
+// (gen_layer_script.py:1399-1400), whose values replace the tile's in LDS
+// for the stamped words.  Out of line: the other epilogues' store path is
+// the control wavefront's critical path in a chained step.
+__device__ __noinline__ void serve_residual(Lds &L, CJob &J, int slot, int t, int lane) {
+  if (lane < kTileRows) {
+    const int64_t v = L.tv[slot][lane];
+    const int row = (t - J.tile0) * kTileRows + lane;
+    if (row < J.nrows) {
+      if (J.out) store_coherent((int16_t *)J.out + row, (int16_t)v);
+      const int64_t rv = clamp64(
+          v + __hip_atomic_load(J.res + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+          -32768, 32767);
+      store_coherent(J.res_out + row, (int16_t)rv);
+      L.tv[slot][lane] = rv;
+    }
+  }
+  wait_lds();
+}
+
 // Store the outputs of this CU's tiles of site P (tile numbers kt0, ...), and
 // for a job read through stamped words also the words (lanes 0..7: rows
 // 2l, 2l+1 of the tile with `stamp`; each an 8-byte store, which lands
@@ -324,26 +342,9 @@ __device__ void ctrl_serve(CSite &P, Lds &L, int kt0, int r, int G, int lane, ui
       continue;
     }
     lds_wait_eq(L, &L.tready[slot], kt + 1, lane, lspin);
-    const bool add = J.epi == EPI_MOVY_I16_ADD;
-    if (add) {
-      // MOVY int16 into out (when set), and the block's residual ALU ADD
-      // clip16(res + that) into res_out (gen_layer_script.py:1399-1400); the
-      // stamped words, if any, carry the residual
-      if (lane < kTileRows) {
-        const int64_t v = L.tv[slot][lane];
-        const int row = (t - J.tile0) * kTileRows + lane;
-        if (row < J.nrows) {
-          if (J.out) store_coherent((int16_t *)J.out + row, (int16_t)v);
-          const int64_t rv =
-              clamp64(v + __hip_atomic_load(J.res + row, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT),
-                      -32768, 32767);
-          store_coherent(J.res_out + row, (int16_t)rv);
-          L.tv[slot][lane] = rv;
-        }
-      }
-      wait_lds();
-    }
+    // a residual-ADD job reaches this kernel as EPI_MOVY_I16 with res_out
+    const bool add = J.res_out != nullptr;
+    if (add) serve_residual(L, J, slot, t, lane);
     if (kDep && J.stamped && lane < kTileRows / 2) {
       // rows 2l and 2l + 1 (int16 epilogues); nrows is even
       const int row = (t - J.tile0) * kTileRows + 2 * lane;
@@ -1026,7 +1027,11 @@ __device__ __forceinline__ void weight_role(const GemvParams *sites_arg, int nsi
   lds_write_i32(&L.wsite[wave], nsites);
 }
 
-template <bool kDep>
+// kSpin: the context set its own spin limits (a test of the give-up paths);
+// otherwise the limits are the compile-time defaults, which the waits fold
+// in (runtime limits everywhere cost 1 % on the independent-input stream and
+// 5 % on the chained one)
+template <bool kDep, bool kSpin>
 __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
                                                           const GemvParams *__restrict__ sites_arg) {
   CSite *sites = (CSite *)sites_arg;
@@ -1038,8 +1043,8 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
   // this launch's completion-flag values are fbase + 1 .. fbase + nsites
   const uint32_t fbase = (S.epoch - 1u) * (uint32_t)(nsites + 1);
   // polls before a wait gives up: between workgroups, within one
-  const uint32_t gspin = S.grid_spin ? S.grid_spin : kGridSpin;
-  const uint32_t lspin = S.lds_spin ? S.lds_spin : kLdsSpin;
+  const uint32_t gspin = kSpin && S.grid_spin ? S.grid_spin : kGridSpin;
+  const uint32_t lspin = kSpin && S.lds_spin ? S.lds_spin : kLdsSpin;
 
   // tables, reduction slots and flags
   const int32_t *tab = sites[0].tables;
@@ -1112,7 +1117,9 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
 hipError_t launch_stream(const StreamParams &sp, int grid, hipStream_t s, bool cooperative,
                          bool dependent, hipEvent_t start, hipEvent_t stop) {
   const GemvParams *sites = sp.sites;
-  auto kernel = dependent ? stream_kernel<true> : stream_kernel<false>;
+  const bool spin = sp.grid_spin || sp.lds_spin;
+  auto kernel = dependent ? (spin ? stream_kernel<true, true> : stream_kernel<true, false>)
+                          : (spin ? stream_kernel<false, true> : stream_kernel<false, false>);
   if (cooperative) {
     void *args[] = {(void *)&sp, (void *)&sites};
     hipError_t e = start ? hipEventRecord(start, s) : hipSuccess;
@@ -1128,13 +1135,13 @@ hipError_t launch_stream(const StreamParams &sp, int grid, hipStream_t s, bool c
 }
 
 int stream_max_blocks_per_cu() {
-  int n = 0, m = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, stream_kernel<false>, kThreads, 0) !=
-          hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&m, stream_kernel<true>, kThreads, 0) !=
-          hipSuccess)
-    return 1;
-  n = n < m ? n : m;
+  int n = 1 << 30;
+  for (auto k : {stream_kernel<false, false>, stream_kernel<true, false>,
+                 stream_kernel<false, true>, stream_kernel<true, true>}) {
+    int m = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&m, k, kThreads, 0) != hipSuccess) return 1;
+    n = m < n ? m : n;
+  }
   return n < 1 ? 1 : (n > 1 ? 1 : n);
 }
 
