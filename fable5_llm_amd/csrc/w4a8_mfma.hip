@@ -78,12 +78,13 @@ struct MmJob {
 // rounds, checks and stores y32 after the launch.
 struct MmSlice {
   int tr, tg, kb0, nbs;   // first row tile, row-tile stride, first block, blocks
+  // ns is 1, 2 or 4 (the host's choice), so the divisions are shifts
   __device__ MmSlice(const MmJob &J, int r, int G) {
-    const int ns = J.ns;
-    tr = r / ns;
-    tg = G / ns;
-    nbs = J.nblk / ns;
-    kb0 = (r - tr * ns) * nbs;
+    const int l = __builtin_ctz((unsigned)J.ns);
+    tr = r >> l;
+    tg = G >> l;
+    nbs = J.nblk >> l;
+    kb0 = (r & (J.ns - 1)) * nbs;
   }
 };
 
@@ -141,6 +142,10 @@ __device__ __forceinline__ int32_t mm_lds_add_rtn(int32_t *p, int32_t v) {
   asm volatile("s_waitcnt lgkmcnt(0)\n\tds_add_rtn_u32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)"
                : "=v"(old) : "v"(lds_off(p)), "v"(v) : "memory");
   return old;
+}
+// an LDS add that does not wait for itself (nor for earlier LDS work)
+__device__ __forceinline__ void mm_lds_add_post(int32_t *p, int32_t v) {
+  asm volatile("ds_add_u32 %0, %1" :: "v"(lds_off(p)), "v"(v) : "memory");
 }
 // an LDS write that does not wait for itself (nor for earlier LDS work: a
 // wavefront's LDS instructions execute in order)
@@ -576,8 +581,9 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
                   mm_lds_add_u64(&tbl[((jj * CTX + ct) * 4 + e) * 64 + lane], p[jj][ct][e]);
                 p[jj][ct][e] = 0;
               }
-          wait_lds();   // the adds are done before the count
-          if (lane == 0) mm_lds_add_rtn(&F.tcnt[tb], 1);
+          // the count follows the adds in this wavefront's LDS order, so the
+          // store wavefront, seeing it, sees the adds: neither is waited for
+          if (lane == 0) mm_lds_add_post(&F.tcnt[tb], 1);
         }
         cur.next(F, P.njobs, JOB);
         ++s;
