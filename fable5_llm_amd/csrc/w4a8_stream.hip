@@ -516,7 +516,8 @@ __device__ __forceinline__ bool pro_issue_stamped(ProX &X, CSite &P, uint32_t st
 #pragma unroll
   for (int c = 0; c < kPN; ++c) X.wv[c] = vec_load(rw, ((c * kPW + pw) * kChunk + lane * 8) * 2);
   // words past K are out of the buffer's range: they read as zero, so a
-  // chunk past K is taken as arrived
+  // lane whose 8 elements lie past K (K % 8 == 0) takes them as arrived --
+  // per lane, since K need not fill a chunk
   const __amdgpu_buffer_rsrc_t rx =
       __builtin_amdgcn_make_buffer_rsrc((void *)P.x_stamped, (short)0, 4 * K, kBufDword3);
   bool ok = false;
@@ -531,7 +532,7 @@ __device__ __forceinline__ bool pro_issue_stamped(ProX &X, CSite &P, uint32_t st
     }
 #pragma unroll
     for (int c = 0; c < kPC; ++c) {
-      const bool past = (c * kPW + pw) * kChunk >= K;
+      const bool past = (c * kPW + pw) * kChunk + lane * 8 >= K;
       mine = mine && (past || ((uint32_t)X.pc[c].y == stamp && (uint32_t)X.pc[c].w == stamp &&
                                (uint32_t)X.x2[c].y == stamp && (uint32_t)X.x2[c].w == stamp));
     }

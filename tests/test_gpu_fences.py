@@ -100,3 +100,74 @@ def test_dependent_sites(engine, mode, fences):
         plan.close()
         for w in (wA, wB, wC, wD, wH):
             w.free()
+
+
+@pytest.mark.parametrize("kb,pro", [(128, N.PRO_RMSNORM_DYNQ8), (256, N.PRO_DYNQ8),
+                                    (640, N.PRO_DYNQ8), (1152, N.PRO_DYNQ8),
+                                    (2048, N.PRO_RMSNORM_DYNQ8)])
+@pytest.mark.parametrize("mode", [N.PLAN_PERSISTENT, N.PLAN_PERSISTENT_COOP])
+def test_stamped_sites_any_k(engine, kb, pro, mode):
+    """Sites reading an earlier site's output through stamped words when
+    that output (the reader's K) does not fill the prologue's 512-element
+    chunks: A (kb rows) -> B (K = kb) -> LM head (K = 256), each waiting for
+    the words of the one before, bit-exact against the oracle."""
+    from fable5_llm_amd.engine import Plan
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(kb)
+    I16 = N.EPI_MOVY_I16
+
+    def mat(nrows, k):
+        img = S.synth_image(gen, nrows, k, S.CHAIN_LOG2_LO)
+        torch.cuda.synchronize()
+        return engine.upload(img, nrows, k, S.sh_for_k(k)), img.cpu().numpy()
+
+    def ref(img, nrows, k, x16, prologue, norm_w=None):
+        x = x16
+        if prologue == N.PRO_RMSNORM_DYNQ8:
+            x = law.rmsnorm_fx(x16, norm_w, S.RS_F, True)
+        x8, e = law.dyn_quant_i8(x)
+        return cfast.matvec_y32_img(img, nrows, k, S.sh_for_k(k), x8, 0), e
+
+    wA, iA = mat(kb, K)
+    xA = S.synth_x16(gen, K, S.RS_F)
+    outA = torch.full((kb,), 0x5A5A, dtype=torch.int16, device=dev)
+    wB, iB = mat(256, kb)
+    nwB = S.synth_norm_w(gen, kb, True) if pro == N.PRO_RMSNORM_DYNQ8 else None
+    outB = torch.full((256,), 0x5A5A, dtype=torch.int16, device=dev)
+    wH, iH = mat(512, 256)
+    res = torch.zeros(2, dtype=torch.int32, device=dev)
+    p0A = 15 - S.E_SCALE - S.sh_for_k(K)
+    p0B = 15 - S.E_SCALE - S.sh_for_k(kb)
+    plan = Plan(engine)
+    plan.add_site([wA], [I16], [p0A], [outA], xA, prologue=N.PRO_DYNQ8, in_f=S.RS_F)
+    plan.add_site([wB], [I16], [p0B], [outB], outA, prologue=pro, norm_w=nwB, in_f=S.RS_F,
+                  one_plus=True)
+    plan.add_head(wH, outB, res, prologue=N.PRO_DYNQ8)
+    try:
+        plan.set_mode(mode)
+        plan.set_fences(N.FENCE_AUTO)
+        torch.cuda.synchronize()
+        yA, eA = ref(iA, kb, K, xA.cpu().numpy(), N.PRO_DYNQ8)
+        refA = law.movy(yA, p0A - eA, law.MOVY_INT16)
+        yB, eB = ref(iB, 256, kb, np.asarray(refA, np.int16), pro,
+                     None if nwB is None else nwB.cpu().numpy())
+        refB = law.movy(yB, p0B - eB, law.MOVY_INT16)
+        yH, _ = ref(iH, 512, 256, np.asarray(refB, np.int16), N.PRO_DYNQ8)
+        refH = tuple(int(v) for v in law.amax32(yH))
+        for rep in range(2):
+            outA.fill_(0x5A5A)
+            outB.fill_(0x5A5A)
+            res.zero_()
+            torch.cuda.synchronize()
+            plan.run()
+            engine.sync()
+            assert np.array_equal(outA.cpu().numpy().astype(np.int64),
+                                  np.asarray(refA, np.int64)), rep
+            assert np.array_equal(outB.cpu().numpy().astype(np.int64),
+                                  np.asarray(refB, np.int64)), rep
+            assert tuple(res.cpu().numpy().tolist()) == refH, rep
+    finally:
+        plan.close()
+        for w in (wA, wB, wH):
+            w.free()
