@@ -17,7 +17,10 @@ chain of dependent sites).
 
 Prints one JSON line.  `value` = stream bytes / wall time per step.
 `roofline` = the dominant kernel alone: stream bytes / sum of its per-launch
-durations, each launch bracketed by dispatch-recorded HIP events.
+durations, each launch bracketed by dispatch-recorded HIP events (with the
+launches' p10 / p50 / p90).  `config.end_hash` = SHA-256 of the step's end
+state (every output and export), equal after a rerun over cleared outputs
+and, in the `ordered` and `chained` legs, across launch modes.
 `ffn` = one layer's SwiGLU block per call (w4a8_mlp_async) over the 32
 layers, with the residual add.  `head` = the LM head alone, with its
 argmax and with TOPK-32.
@@ -496,6 +499,9 @@ def chained_leg(ctx, stream, args):
                                "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBS, 4),
                                "kernel": "stream_kernel",
                                "avg_launch_us": round(tm["kernel_ms"] * 1e3, 3)}
+            out["end_hash"] = st.digest()
+        else:
+            leg["end_hash_equal"] = st.digest() == out["end_hash"]
         out[name] = leg
     st.plan.set_mode(N.PLAN_PERSISTENT)
     return st, out
@@ -788,6 +794,12 @@ def main():
     kern_ms, nlaunch = tm["kernel_ms"], tm["nlaunch"]
     achieved = st.bytes / (kern_ms * 1e-3) / 1e9
     kernel = "stream_kernel" if persistent else "gemv_kernel"
+    # the step's end state after the timed runs, and after one more run over
+    # cleared outputs: every output written again, identically
+    end_hash = st.digest()
+    st.clear_outputs()
+    st.run()
+    end_hash_rerun = st.digest()
 
     ordered = None
     if not args.no_ordered and persistent:
@@ -800,6 +812,7 @@ def main():
             "mode": "graph", "ms_per_step": round(to["ms_per_step"], 4),
             "value": round(gbs_o, 1), "unit": "GB/s",
             "pct_of_peak_hbm": round(100.0 * gbs_o / PEAK_HBM_GBS, 1),
+            "end_hash_equal": st.digest() == end_hash,
             "note": "the same independent-input plan with every site starting after "
                     "the previous one completes; one gemv_kernel launch per site"}
         st.plan.set_mode(mode)
@@ -843,6 +856,10 @@ def main():
             "matrices": tot["matrices"], "dynq8_sites": tot["sites"],
             "rmsnorm_sites": tot["rmsnorm_sites"], "bytes_per_step": st.bytes,
             "reference_chunks": 1370, "batch": 1,
+            "end_hash": end_hash,
+            "end_hash_rerun_equal": end_hash_rerun == end_hash,
+            "end_hash_of": ("SHA-256 of every output, x8 export and e_x of the step and "
+                            "the head's (index, value), in site order"),
             "fences": args.fences if persistent else "all",
             "launch": (("one launch per step, one workgroup per CU (" +
                         ("cooperative launch API" if args.mode == "cooperative" else
@@ -866,6 +883,8 @@ def main():
             "kernel": kernel,
             "launches_per_step": nlaunch,
             "avg_launch_us": round(kern_ms / nlaunch * 1e3, 3),
+            "launch_us_p10_p50_p90": ([round(float(np.percentile(tm["launch_ms"], q)) * 1e3, 3)
+                                       for q in (10, 50, 90)] if "launch_ms" in tm else None),
             "bytes_per_launch": round(st.bytes / nlaunch),
             "timing": ("median of --steps back-to-back launches, dispatch-recorded HIP "
                        "events, right after the timed steps" if persistent else

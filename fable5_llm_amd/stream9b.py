@@ -332,6 +332,21 @@ class Stream9B:
                 nw.copy_(synth_norm_w(gen, s.K, s.one_plus))
         torch.cuda.synchronize(self.e_x.device)
 
+    def digest(self):
+        """SHA-256 over every output, x8 export and e_x of the step, and the
+        head's (index, value), in site order: the step's end state."""
+        import hashlib
+        import torch
+        torch.cuda.synchronize(self.e_x.device)
+        h = hashlib.sha256()
+        for outs, x8 in zip(self.outs, self.x8):
+            for o in outs:
+                h.update(o.cpu().numpy().tobytes())
+            if x8 is not None:
+                h.update(x8.cpu().numpy().tobytes())
+        h.update(self.e_x.cpu().numpy().tobytes())
+        return h.hexdigest()
+
     def clear_outputs(self, value=0):
         """Overwrite every output, export and the head result (a later run
         must write them all again)."""
