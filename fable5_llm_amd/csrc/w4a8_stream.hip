@@ -14,9 +14,11 @@
 //    refill is the same 9 buffer loads (out of range, so without a memory
 //    access, past the end of the sequence), and a weight wavefront makes no
 //    other global access, so the compiler's count of its outstanding loads
-//    is exact on every path and the wait for one set never waits for the
-//    other.  At its first block of a site it waits only for that site's
-//    activations (an LDS flag), never for the other wavefronts.
+//    is exact on every path.  (Its waits are not minimal: at the loop head
+//    the first set's dot product waits for both sets.  Loads and waits of
+//    our own in inline assembly, one set at a time, measured slower.)  At
+//    its first block of a site it waits only for that site's activations
+//    (an LDS flag), never for the other wavefronts.
 //  * 3 prologue wavefronts compute each site's activations (RMSNorm, DYNQ8:
 //    x8, e_x and the offset corrections) ahead of the weight wavefronts,
 //    into a ring of 6 LDS buffers; a buffer is reused once every weight
