@@ -276,8 +276,7 @@ __device__ __forceinline__ void item_next(Item &c, int nbw) {
 }
 
 // Put a block in flight: always exactly 1 + kGroupsPerBlock loads, so the
-// compiler's count of outstanding loads is the same on every path and a
-// wait for one register set never waits for the other.  The loads are
+// compiler's count of outstanding loads is the same on every path.  The loads are
 // buffer loads whose range ends with the block's data: past the end of the
 // sequence (range 0), and for the missing groups of a short block, they are
 // out of range, return zero and make no memory access.
