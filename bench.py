@@ -609,6 +609,112 @@ def read_ceiling_leg(ctx, gib=4, launches=20):
     return best
 
 
+def site_class(s):
+    """The class of a stream site: its role in the layer and its shapes."""
+    tail = s.name.split(".")[-1]
+    if s.head:
+        return "head"
+    kind = "dn" if any(m.name.endswith("in_qkv") for m in s.mats) or tail == "dn_heads" else \
+        "attn" if tail in ("ln1", "attn_heads") else "ffn"
+    return {"ln1": f"{kind}_ln1", "dn_heads": "dn_heads", "attn_heads": "attn_heads",
+            "ln2": "ffn_gate_up", "swiglu": "ffn_down"}[tail]
+
+
+def per_class(st, ms_sites):
+    """Per site class of the stream: sites, matrices (rows x K), bytes per
+    site, and the median time per site over the class's sites (ms_sites:
+    one time per site, ms)."""
+    import numpy as np
+    out = {}
+    for si, s in enumerate(st.sites):
+        c = out.setdefault(site_class(s), {"sites": 0, "matrices": [
+            f"{m.name.split('.')[-1]} {m.nrows}x{m.K}" for m in s.mats],
+            "bytes_per_site": sum(m.bytes for m in s.mats), "_us": []})
+        c["sites"] += 1
+        c["_us"].append(float(ms_sites[si]) * 1e3)
+    for c in out.values():
+        us = float(np.median(c.pop("_us")))
+        c["us_per_site"] = round(us, 3)
+        c["gbs"] = round(c["bytes_per_site"] / (us * 1e-6) / 1e9, 1)
+        c["pct_of_peak_hbm"] = round(100.0 * c["gbs"] / PEAK_HBM_GBS, 1)
+    return out
+
+
+def class_leg(st, reps=5):
+    """Time per site class of the headline step, two ways: in the persistent
+    launch (workgroup 0's control wavefront stamps the wall clock as it
+    starts each site's stores; the intervals, scaled to the launch's event
+    time, are the per-site times -- sites overlap, so an interval is the
+    time between consecutive sites' ends on that workgroup) and as one
+    gemv_kernel launch per site (dispatch-recorded events around each
+    launch, graph mode).  Medians over `reps` instrumented passes."""
+    import numpy as np
+    from fable5_llm_amd import _native as N
+    out = {}
+    for name, mode in (("persistent", N.PLAN_PERSISTENT), ("per_site_launch", N.PLAN_GRAPH)):
+        st.plan.set_mode(mode)
+        prof = np.median(np.array([st.profile() for _ in range(reps)]), axis=0)
+        out[name] = per_class(st, prof)
+    st.plan.set_mode(N.PLAN_PERSISTENT)
+    out["basis"] = ("persistent: per-site intervals of workgroup 0's wall-clock stamps, scaled to "
+                    "the launch's event time; per_site_launch: one gemv_kernel per site, "
+                    "dispatch-recorded events; medians over 5 instrumented passes, then over "
+                    "the class's sites")
+    return out
+
+
+def seeds_leg(st, ctx, stream, args, seeds, imgs, chain=False):
+    """The step again on other seeded inputs (Stream9B.reseed: every site's
+    own input and RMSNorm weights redrawn; the resident weights stay): per
+    seed, the step time (at least --warmup untimed steps then until steady,
+    then --steps timed), the end hash, and the oracle's bit-exact check of
+    every output.  imgs: the stream's row images (downloaded once)."""
+    from tests import stream_check as sc
+    per = []
+    for seed in seeds:
+        st.reseed(seed)
+        tm = time_steps(st, ctx, stream, args.steps, args.warmup)
+        host = sc.host_inputs(st, imgs)
+        ref, _ = sc.run_cpu_stream(st, host)
+        bad = sc.compare(st, host, ref)
+        per.append({"seed": seed, "ms_per_step": round(tm["ms_per_step"], 4),
+                    "kernel_us": round(tm["kernel_ms"] * 1e3, 2),
+                    "end_hash": st.digest()[:16],
+                    "parity": "bit-exact" if not bad else f"MISMATCH {len(bad)}: {bad[:3]}"})
+    return per
+
+
+def spread_of(values):
+    import numpy as np
+    v = np.asarray(values, dtype=float)
+    return {"min": round(float(v.min()), 4), "median": round(float(np.median(v)), 4),
+            "max": round(float(v.max()), 4),
+            "max_over_min": round(float(v.max() / v.min()), 4)}
+
+
+def cpu_host_info():
+    """The host the CPU baseline ran on: model, logical CPUs, the affinity
+    set this process may use."""
+    model = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    aff = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else []
+    ranges, start = [], None
+    for i, c in enumerate(aff):
+        if start is None:
+            start = c
+        if i + 1 == len(aff) or aff[i + 1] != c + 1:
+            ranges.append(f"{start}-{c}" if c != start else f"{c}")
+            start = None
+    return {"cpu_model": model, "host_cpus": os.cpu_count(),
+            "affinity": ",".join(ranges), "affinity_count": len(aff)}
+
+
 def cpu_per_config(st, host):
     """CPU baselines per configuration, on the stream's own matrices: C0 one
     4096 x 4096 (layer 0's in_z), C1 the FFN set (layer 0's gate and up,
@@ -625,6 +731,7 @@ def cpu_per_config(st, host):
                     return m, host[si]["imgs"][mi]
         raise KeyError(name)
     rng = np.random.default_rng(5)
+    rates = {}   # K -> [bytes, numpy seconds]
     cfgs = {"C0": [find("L0.in_z")], "C1": [find("L0.gate"), find("L0.up"), find("L0.down")],
             "C2": [find("lm_head")]}
     out = {}
@@ -638,35 +745,57 @@ def cpu_per_config(st, host):
                 cfast.matvec_y32_img(img, m.nrows, m.K, sh_for_k(m.K), xs[m.K], 0)
             t += time.perf_counter() - t0
             n += 1
-        t0 = time.perf_counter()
+        tn = 0.0
         for m, img in mats:
+            t0 = time.perf_counter()
             law.matvec_y32_image(img.tobytes(), m.nrows, m.K, sh_for_k(m.K), xs[m.K])
-        tn = time.perf_counter() - t0
+            dt = time.perf_counter() - t0
+            tn += dt
+            by_k = rates.setdefault(m.K, [0, 0.0])
+            by_k[0] += m.bytes
+            by_k[1] += dt
         out[c] = {"bytes": nbytes,
                   "c_openmp": {"ms": round(t / n * 1e3, 3),
                                "gbs": round(nbytes * n / t / 1e9, 2), "cores": cfast.num_threads()},
                   "numpy_1thread": {"ms": round(tn * 1e3, 1), "gbs": round(nbytes / tn / 1e9, 4)}}
+    # C3 by numpy on one thread, extrapolated: the stream's bytes at each K
+    # over the rate measured above for that K (numpy's int64 law is linear in
+    # rows for a given K)
+    c3_s = 0.0
+    stream_bytes = {}
+    for s in st.sites:
+        for m in s.mats:
+            stream_bytes[m.K] = stream_bytes.get(m.K, 0) + m.bytes
+    for K, b in stream_bytes.items():
+        mb, mt = rates[K]
+        c3_s += b * mt / mb
+    out["C3_numpy_1thread_extrapolated"] = {
+        "ms_per_step": round(c3_s * 1e3, 1), "gbs": round(st.bytes / c3_s / 1e9, 4),
+        "basis": "; ".join(f"K={K}: {b:,} B of the stream at {rates[K][0] / rates[K][1] / 1e9:.4f} "
+                           f"GB/s (numpy 1 thread over the {rates[K][0]:,} B of C0-C2 with that K)"
+                           for K, b in sorted(stream_bytes.items()))}
     return out
 
 
-def chain_check(st):
+def chain_check(st, imgs=None):
     """The chained stream's last run against the oracle run site after site
     (each site fed from the oracle's own output of its producer)."""
     from tests import stream_check as sc
-    host = sc.host_inputs(st)
+    host = sc.host_inputs(st, imgs)
     ref, _ = sc.run_cpu_stream(st, host)
     bad = sc.compare(st, host, ref)
     return "bit-exact" if not bad else f"MISMATCH {len(bad)}: {bad[:5]}"
 
 
-def cpu_baseline(st, min_seconds, keep=(), keep_ffn=None, keep_head=None):
+def cpu_baseline(st, min_seconds, keep=(), keep_ffn=None, keep_head=None, imgs=None):
     """Oracle leg: the C restatement over the full stream, repeated until
     `min_seconds` of matvec work; returns its rate and the parity check (of
-    the stream and of the batched leg's kept outputs)."""
+    the stream and of the batched leg's kept outputs).  imgs: the stream's
+    row images, if already downloaded."""
     import numpy as np
     from oracle import cfast
     from tests import stream_check as sc
-    host = sc.host_inputs(st)
+    host = sc.host_inputs(st, imgs)
     ref, total = sc.run_cpu_stream(st, host)
     passes = 1
     while total < min_seconds:
@@ -694,7 +823,7 @@ def cpu_baseline(st, min_seconds, keep=(), keep_ffn=None, keep_head=None):
         "ms_per_step": round(total / passes * 1e3, 2),
         "numpy_1thread_gbs": round(img.size / t_np / 1e9, 4),
         "numpy_sample": "one 4096x4096 matvec_y32 by oracle/law.py (int64 numpy)",
-        "host_cpus": os.cpu_count(),
+        **cpu_host_info(),
         "numpy": np.__version__,
         "parity": "bit-exact" if not bad else f"MISMATCH {len(bad)}: {bad[:5]}",
         "batched_parity": batched_check(st, keep) if keep else None,
@@ -742,6 +871,10 @@ def main():
     ap.add_argument("--batch", default="8,32",
                     help="token counts B for the batched int8-MFMA leg over the FFN "
                          "matrices (comma-separated, each <= 64; empty: skip)")
+    ap.add_argument("--seeds", type=int, default=4,
+                    help="the headline and chained steps on this many input seeds in "
+                         "all (--seed, then --seed + 100, + 200, ...), each checked "
+                         "against the oracle; the spread of their step times is reported")
     ap.add_argument("--only-batched", action="store_true",
                     help="run the batched leg alone (for profiling it) and print its results")
     args = ap.parse_args()
@@ -928,14 +1061,46 @@ def main():
         log("ffn leg")
         line["ffn"], keep_ffn = ffn_leg(st, ctx, min(args.steps, 50),
                                         max(3, args.warmup // 10))
+    log("per site class")
+    line["per_class"] = class_leg(st)
+    imgs = imgs_c = None
     if not args.no_cpu:
+        from tests import stream_check as sc
+        imgs = sc.images(st)
         log("cpu baseline and parity")
-        line["cpu_baseline"] = cpu_baseline(st, args.cpu_seconds, keep, keep_ffn, keep_head)
+        line["cpu_baseline"] = cpu_baseline(st, args.cpu_seconds, keep, keep_ffn, keep_head,
+                                            imgs=imgs)
         if stc is not None:
             log("chained parity")
-            chained["parity"] = chain_check(stc)
+            imgs_c = sc.images(stc)
+            chained["parity"] = chain_check(stc, imgs_c)
         if keep_c0 is not None:
             c0["parity"] = c0_check(keep_c0)
+    if args.seeds > 1 and not args.no_cpu:
+        others = [args.seed + 100 * i for i in range(1, args.seeds)]
+        log(f"headline on seeds {others}")
+        first = {"seed": args.seed, "ms_per_step": round(ms_step, 4),
+                 "kernel_us": round(kern_ms * 1e3, 2), "end_hash": end_hash[:16],
+                 "parity": line["cpu_baseline"]["parity"]}
+        per = [first] + seeds_leg(st, ctx, stream, args, others, imgs)
+        line["seeds"] = {"headline": per,
+                         "ms_per_step_spread": spread_of([p["ms_per_step"] for p in per]),
+                         "kernel_us_spread": spread_of([p["kernel_us"] for p in per]),
+                         "basis": ("Stream9B.reseed(seed): every site's input and RMSNorm "
+                                   "weights redrawn, the resident weights kept; each seed "
+                                   "warmed until steady, --steps timed, every output checked "
+                                   "against the oracle")}
+        if stc is not None:
+            log(f"chained step on seeds {others}")
+            stc.plan.set_mode(N.PLAN_PERSISTENT)
+            firstc = {"seed": args.seed + 1,
+                      "ms_per_step": chained["persistent"]["ms_per_step"],
+                      "kernel_us": chained["persistent"]["roofline"]["avg_launch_us"],
+                      "end_hash": chained["end_hash"][:16], "parity": chained.get("parity")}
+            perc = [firstc] + seeds_leg(stc, ctx, stream, args, [o + 1 for o in others], imgs_c)
+            line["seeds"]["chained"] = perc
+            line["seeds"]["chained_ms_per_step_spread"] = spread_of(
+                [p["ms_per_step"] for p in perc])
     if stc is not None:
         stc.close()
     st.close()

@@ -880,6 +880,9 @@ struct w4a8_mplan {
   void *d_fin = nullptr;      // their finishing records
   int nfin = 0;
   int64_t fin_max = 0;        // the largest B * nrows among them
+  // buffers of earlier builds: a graph the caller captured from an earlier
+  // run still points at them, so they are freed only by destroy
+  std::vector<void *> retired;
 };
 
 int w4a8_mplan_create(w4a8_ctx *c, int32_t B, w4a8_mplan **out) {
@@ -918,9 +921,8 @@ int w4a8_mplan_run(w4a8_mplan *p) {
     std::vector<uint8_t> host(matmul_job_bytes() * (size_t)n);
     std::vector<int32_t> ns(n);
     HIP_TRY(matmul_plan_prepare(p->jobs.data(), n, p->B, host.data(), &p->cfg, ns.data()));
-    HIP_TRY(hipStreamSynchronize(c->stream));   // an earlier run may still read the tables
     for (void *q : {(void *)p->d_table, (void *)p->d_part, p->d_fin})
-      if (q) HIP_TRY(hipFree(q));
+      if (q) p->retired.push_back(q);
     p->d_table = p->d_fin = nullptr;
     p->d_part = nullptr;
     // a K-split job's slices store their sums to part [ns][B][nrows] int64
@@ -958,13 +960,13 @@ int w4a8_mplan_run(w4a8_mplan *p) {
 int w4a8_mplan_destroy(w4a8_mplan *p) {
   if (!p) return W4A8_OK;
   int rc = W4A8_OK;
-  if (p->d_table || p->d_part || p->d_fin) {
+  for (void *q : {(void *)p->d_table, (void *)p->d_part, p->d_fin})
+    if (q) p->retired.push_back(q);
+  if (!p->retired.empty()) {
     DeviceGuard g(p->ctx->device);
-    if (hipStreamSynchronize(p->ctx->stream) != hipSuccess ||
-        (p->d_table && hipFree(p->d_table) != hipSuccess) ||
-        (p->d_part && hipFree(p->d_part) != hipSuccess) ||
-        (p->d_fin && hipFree(p->d_fin) != hipSuccess))
-      rc = fail(W4A8_E_HIP, "matmul plan: freeing its buffers failed");
+    bool ok = hipStreamSynchronize(p->ctx->stream) == hipSuccess;
+    for (void *q : p->retired) ok = hipFree(q) == hipSuccess && ok;
+    if (!ok) rc = fail(W4A8_E_HIP, "matmul plan: freeing its buffers failed");
   }
   delete p;
   return rc;
@@ -1177,6 +1179,10 @@ struct w4a8_plan {
   uint64_t *d_stamped = nullptr;    // stamped words of outputs read through them
   int64_t stamped_words = 0;
   std::vector<void *> temps;        // temporaries of the MLP blocks added (w4a8_plan_add_mlp)
+  // device buffers of earlier builds (site table, flags, staging, stamped
+  // words, head partials): a graph the caller captured from an earlier run
+  // still points at them, so they are freed only by destroy
+  std::vector<void *> retired;
   bool dependent = false;           // some site waits for, or forms, others' results
   int G = 0;
   int head_site = -1;
@@ -1184,10 +1190,9 @@ struct w4a8_plan {
 };
 
 static void plan_drop_persistent(w4a8_plan *p) {
-  if (p->d_sites) (void)hipFree(p->d_sites);
-  if (p->d_done) (void)hipFree(p->d_done);
-  if (p->d_stage) (void)hipFree(p->d_stage);
-  if (p->d_stamped) (void)hipFree(p->d_stamped);
+  for (void *q : {(void *)p->d_sites, (void *)p->d_done, (void *)p->d_stage,
+                  (void *)p->d_stamped})
+    if (q) p->retired.push_back(q);
   p->d_sites = nullptr;
   p->d_done = nullptr;
   p->d_stage = nullptr;
@@ -1577,16 +1582,30 @@ int w4a8_plan_add_mlp(w4a8_plan *p, const w4a8_weights *gate, const w4a8_weights
   const int32_t epi_gu[2] = {EPI_SILU32, EPI_MOVY_P32};
   const int32_t p0_gu[2] = {p0_gate, p0_up};
   void *out_gu[2] = {sg, u};
+  // the block goes in whole or not at all: a failed add takes back what
+  // the block added before it, so the plan's steps stay the caller's sites
+  const size_t n0 = p->steps.size();
+  auto undo = [&](int rc) {
+    if (p->steps.size() != n0) {
+      p->steps.resize(n0);
+      plan_drop_graph(p);
+    }
+    p->temps.pop_back();
+    (void)hipFree(tmp);
+    return rc;
+  };
   int rc = w4a8_plan_add_site(p, 2, gu, epi_gu, p0_gu, out_gu,
                               d_norm_w ? PRO_RMSNORM_DYNQ8 : PRO_DYNQ8, d_x16, d_norm_w, in_f,
                               one_plus, 0, nullptr, nullptr, nullptr);
-  if (rc) return rc;
+  if (rc) return undo(rc);
   if (!d_res_out) {
     const int32_t epi = EPI_MOVY_I16;
     void *out = d_mlp_out;
-    return w4a8_plan_add_site_emul(p, 1, &down, &epi, &p0_down, &out, sg, u, nullptr, nullptr);
+    rc = w4a8_plan_add_site_emul(p, 1, &down, &epi, &p0_down, &out, sg, u, nullptr, nullptr);
+  } else {
+    rc = w4a8_plan_add_site_emul_res(p, down, p0_down, d_mlp_out, sg, u, d_x16, d_res_out);
   }
-  return w4a8_plan_add_site_emul_res(p, down, p0_down, d_mlp_out, sg, u, d_x16, d_res_out);
+  return rc ? undo(rc) : W4A8_OK;
 }
 
 int w4a8_plan_add_head(w4a8_plan *p, const w4a8_weights *w, int32_t prologue,
@@ -1607,10 +1626,7 @@ int w4a8_plan_add_head(w4a8_plan *p, const w4a8_weights *w, int32_t prologue,
     const int cap = (used + st.grid) * 2;
     uint64_t *np_ = nullptr;
     HIP_TRY(hipMalloc(&np_, sizeof(uint64_t) * (size_t)cap));
-    if (p->d_partials) {
-      (void)hipDeviceSynchronize();
-      (void)hipFree(p->d_partials);
-    }
+    if (p->d_partials) p->retired.push_back(p->d_partials);
     p->d_partials = np_;
     p->partials_cap = cap;
     int off = 0;
@@ -1781,6 +1797,7 @@ int w4a8_plan_destroy(w4a8_plan *p) {
   plan_drop_graph(p);
   if (p->d_partials) (void)hipFree(p->d_partials);
   for (void *t : p->temps) (void)hipFree(t);
+  for (void *q : p->retired) (void)hipFree(q);
   delete p;
   return W4A8_OK;
 }

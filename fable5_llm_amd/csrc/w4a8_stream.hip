@@ -887,8 +887,11 @@ __device__ __forceinline__ void prologue_role(const GemvParams *sites_arg, int n
   PSync ps{0, 1};
   uint32_t *sflag = done + stream_flag_site0(G);
   bool ok = true;
+  // (a site whose prologue every CU computes itself -- one reading stamped
+  // words has no fence yet depends on its producer -- is not staged: its
+  // inputs are not written yet)
   for (int s = r; s < nsites; s += G)
-    if (sites[s].fence_at == 0)
+    if (sites[s].fence_at == 0 && !(kDep && sites[s].local_pro))
       ps = compute_publish<kDep>(sites[s], L, stage + (size_t)s * kStageBytes, sflag + s, epoch,
                            pw, lane, ps, lspin);
   for (int s = 0; s < nsites; ++s) {

@@ -100,15 +100,31 @@ def mlp_fx(xn16, qm, rs_f=RS_F_9B):
     """SwiGLU block (layer_fixed.py:1597-1604): gate -> SILU32 (out_f 12),
     up -> SHIFT32W (out_f rs_f), EMUL32 product at p0 12, DYNQ8 -> down ->
     int16, as one device-resident chain (w4a8_mlp_async: gate and up in one
-    launch, then EMUL32, then down).  layer_fixed.py:1602 multiplies the
-    unclipped int64 up value; the engine keeps it as SHIFT32W does
-    (gen_layer_script.py:2176-2186), and the two agree whenever the shifted
-    up value fits int32, i.e. for every right shift of a y32."""
+    launch, then EMUL32, then down).
+
+    layer_fixed.py:1602 multiplies the unclipped int64 up value u; the
+    engine keeps it clipped to int32, as SHIFT32W does
+    (gen_layer_script.py:2176-2186).  The product is the same either way:
+    where |u| >= 2^31 and the SILU32 factor sg is nonzero, |sg * u| and
+    |sg * clip32(u)| are both >= 2^31 - 1, so rshift_round by 12 is
+    >= 2^19 and clip16 saturates both to the same rail (the sign of
+    sg * u); where sg = 0 both are 0.  Left shifts of the y32s (shift =
+    p0 - e_x < 0) are therefore matched as long as the reference's own int64
+    arithmetic is exact: sg * u needs |u| < 2^48, i.e. a left shift of the
+    up projection's y32 (|y32| < 2^31) of at most 17, and the gate and down
+    projections' y32 << s needs s <= 32.  Beyond that numpy's int64 wraps
+    and the reference has no defined result; with e_x <= 9 (DYNQ8 of int16),
+    such p0s are refused with AssertionError."""
     import torch
     ctx = default_context()
-    wg, wu, wd = _weights(qm["gate"]), _weights(qm["up"]), _weights(qm["down"])
     p0s = [(15 - qm[k]["e"] - qm[k]["sh"]) + rs_f - out_f
            for k, out_f in (("gate", 12), ("up", rs_f), ("down", rs_f))]
+    for name, p0, most in zip(("gate", "up", "down"), p0s, (32, 17, 32)):
+        assert 9 - p0 <= most, (
+            f"mlp_fx: the {name} projection's shift p0 - e_x = {p0} - e_x could shift its "
+            f"y32 left by more than {most} bits, where layer_fixed.py:1597-1604's int64 "
+            f"arithmetic wraps")
+    wg, wu, wd = _weights(qm["gate"]), _weights(qm["up"]), _weights(qm["down"])
     dev = torch.device("cuda", ctx.device)
     x = torch.from_numpy(np.ascontiguousarray(xn16, dtype=np.int16)).to(dev)
     y = torch.empty(wd.nrows, dtype=torch.int16, device=dev)

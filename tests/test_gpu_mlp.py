@@ -124,6 +124,47 @@ def test_mlp_fx_dropin_matches_oracle(engine):
         v["dev"].free()
 
 
+@pytest.mark.parametrize("e_up,live", [(11, False), (19, True)])
+def test_mlp_fx_left_shifted_up_matches_oracle(engine, e_up, live):
+    # the up projection's scale exponent makes its shift p0 - e_x negative
+    # (K = 512: sh = 4, p0 = 15 - e - sh = 0 at e = 11, -8 at e = 19; e_x = 5
+    # for these inputs), so u = y32 << s; at e = 19 it leaves int32 for
+    # some rows: the engine's SHIFT32W clip must give the product of the
+    # unclipped int64 u (layer_fixed.py:1597-1604) exactly
+    rng = np.random.default_rng(40 + e_up)
+    q = _mats(rng, 512, 1024)
+    w4, m, _e, sh = q["up"]
+    q["up"] = (w4, m, e_up, sh)
+    qm = {k: {"w4": v[0], "m": v[1], "e": v[2], "sh": v[3]} for k, v in q.items()}
+    xn = activation_x16(rng, 512)
+    try:
+        got = LF.mlp_fx(xn, qm, rs_f=7)
+        ref = law.mlp_fx(xn, q["gate"], q["up"], q["down"], rs_f=7)
+        assert np.array_equal(got, ref)
+        # the case is live: some up values left int32 before the product
+        x8, e_x = law.dyn_quant_i8(xn)
+        y = law.matvec_y32(w4, m, sh, x8).astype(np.int64)
+        s = law.shift_for(e_up, sh, e_x, 7, 7)
+        assert s < 0
+        assert (np.abs(y << np.int64(-s)).max() >= 2 ** 31) == live
+    finally:
+        for v in qm.values():
+            if "dev" in v:
+                v["dev"].free()
+
+
+def test_mlp_fx_refuses_wrapping_shifts(engine):
+    # a left shift of more than 17 bits on the up projection is where the
+    # reference's int64 product could wrap: refused before any device work
+    rng = np.random.default_rng(3)
+    q = _mats(rng, 256, 512)
+    qm = {k: {"w4": v[0], "m": v[1], "e": v[2], "sh": v[3]} for k, v in q.items()}
+    qm["up"]["e"] = 24   # p0 = 15 - 24 - 3 = -12: up to 21 bits left
+    with pytest.raises(AssertionError, match="up projection"):
+        LF.mlp_fx(activation_x16(rng, 256), qm, rs_f=7)
+    assert all("dev" not in v for v in qm.values())
+
+
 def test_mlp_async_rejects_mismatched_shapes(engine):
     rng = np.random.default_rng(2)
     q = _mats(rng, 256, 512)

@@ -313,6 +313,26 @@ def test_swiglu_chain_from_scripts(scripts):
     assert n == 8
 
 
+def test_emul32_of_clipped_up_equals_unclipped():
+    # ref/layer_fixed.py:1597-1602 multiplies the unclipped int64 up value
+    # u; the engine's SHIFT32W keeps clip32(u).  clip16(rshift_round(sg * u,
+    # 12)) is the same for both whenever |u| < 2^48 (the reference's int64
+    # product exact): beyond int32 both saturate to the rail of sg * u.
+    # Brute force over every sg and rail-adjacent, random and extreme u.
+    sg = np.arange(-32768, 32768, dtype=np.int64)
+    rng = np.random.default_rng(11)
+    us = [0, 1, -1, 2 ** 31 - 1, -2 ** 31, 2 ** 31, -2 ** 31 - 1, 2 ** 47, -2 ** 47,
+          2 ** 48 - 1, -(2 ** 48 - 1)]
+    us += list(rng.integers(-2 ** 48 + 1, 2 ** 48, 40))
+    us += list(rng.integers(-2 ** 33, 2 ** 33, 40))
+    us += list(rng.integers(-2 ** 20, 2 ** 20, 20))
+    for u in us:
+        u = np.int64(u)
+        ref = law.clip16(law.rshift_round(sg * u, 12))
+        eng = law.alu_emul32(np.full(sg.shape, law.clip32(np.array([u]))[0]), sg, 12)
+        assert np.array_equal(ref, eng), int(u)
+
+
 # ----------------------------------------------------------- a12 AMAX32
 def test_amax32_a_records(scripts):
     n = 0
