@@ -386,11 +386,19 @@ def head_leg(st, ctx, steps, warmup):
     x, nw = st.inputs[-1]
     res = torch.zeros(2, dtype=torch.int32, device=dev)
     tk = torch.zeros(66, dtype=torch.int32, device=dev)
+    from fable5_llm_amd import _native as N
+    from fable5_llm_amd.engine import Plan
+    tkp = torch.zeros(66, dtype=torch.int32, device=dev)
+    plan = Plan(ctx)
+    plan.add_head_topk32(w, x, tkp, prologue=s.prologue, norm_w=nw, in_f=s.in_f,
+                         one_plus=s.one_plus)
+    plan.set_mode(N.PLAN_PERSISTENT)
     calls = {
         "argmax": lambda: ctx.head_argmax_async(w, x, res, prologue=s.prologue, norm_w=nw,
                                                 in_f=s.in_f, one_plus=s.one_plus),
         "topk32": lambda: ctx.head_topk32_async(w, x, tk, prologue=s.prologue, norm_w=nw,
                                                 in_f=s.in_f, one_plus=s.one_plus),
+        "topk32_in_plan": plan.run,
     }
     out = {"rows": s.mats[0].nrows, "bytes": s.mats[0].bytes}
     for name, fn in calls.items():
@@ -408,7 +416,12 @@ def head_leg(st, ctx, steps, warmup):
         us = e0.elapsed_time(e1) * 1e3 / steps
         out[name] = {"us_per_call": round(us, 2),
                      "value": round(s.mats[0].bytes / (us * 1e-6) / 1e9, 1), "unit": "GB/s"}
-    keep = (res.cpu().numpy(), tk.cpu().numpy())
+    out["topk32"]["how"] = "w4a8_head_topk32_async: the head's y32, then the TOPK-32 kernel"
+    out["topk32_in_plan"]["how"] = ("a persistent plan of the head alone "
+                                    "(w4a8_plan_add_head_topk32): one launch, the scan "
+                                    "inside it, chunk by chunk as the rows are stored")
+    keep = (res.cpu().numpy(), tk.cpu().numpy(), tkp.cpu().numpy())
+    plan.close()
     return out, keep
 
 
@@ -416,12 +429,13 @@ def head_check(ys, keep):
     """The head leg's argmax and TOPK-32 against the oracle's head y32."""
     import numpy as np
     from oracle import law
-    res, tk = keep
+    res, tk, tkp = keep
     y = ys[-1][0]
     vals, rows, count, ovf = law.topk32(y)
     ok = tuple(int(v) for v in res) == tuple(int(v) for v in law.amax32(y))
-    ok = ok and int(tk[64]) == count and bool(tk[65]) == ovf
-    ok = ok and np.array_equal(tk[:count], vals) and np.array_equal(tk[32:32 + count], rows)
+    for t in (tk, tkp):
+        ok = ok and int(t[64]) == count and bool(t[65]) == ovf
+        ok = ok and np.array_equal(t[:count], vals) and np.array_equal(t[32:32 + count], rows)
     return "bit-exact" if ok else "MISMATCH"
 
 
@@ -466,6 +480,25 @@ def batched_check(st, keep):
             ref = cfast.matvec_y32_img(img, m.nrows, m.K, sh_for_k(m.K), x8[b], 0)
             bad += int(not np.array_equal(ref, y[b]))
     return "bit-exact" if bad == 0 else f"MISMATCH in {bad} token rows"
+
+
+def topk_step_leg(st, ctx, stream, args, ms_argmax):
+    """The headline step with its LM head ending in TOPK-32 instead of the
+    argmax (a sampling step): the same resident weights and inputs, one
+    persistent launch whose TOPK-32 scan runs as the head's rows are
+    stored.  Returns the stream (for the checker) and its figures."""
+    from fable5_llm_amd import _native as N
+    from fable5_llm_amd import stream9b
+    stt = stream9b.Stream9B(ctx, seed=args.seed, mode=N.PLAN_PERSISTENT, fences=N.FENCE_AUTO,
+                            weights_from=st, head_topk=True)
+    ctx.sync()
+    tm = time_steps(stt, ctx, stream, args.steps, args.warmup)
+    gbs = stt.bytes / (tm["ms_per_step"] * 1e-3) / 1e9
+    return stt, {"ms_per_step": round(tm["ms_per_step"], 4), "value": round(gbs, 1),
+                 "unit": "GB/s", "pct_of_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 1),
+                 "kernel_us": round(tm["kernel_ms"] * 1e3, 2),
+                 "us_over_argmax_step": round((tm["ms_per_step"] - ms_argmax) * 1e3, 2),
+                 "how": "the headline plan with w4a8_plan_add_head_topk32 as its head"}
 
 
 def chained_leg(ctx, stream, args):
@@ -961,6 +994,8 @@ def main():
         c0, keep_c0 = c0_leg(ctx, stream, args)
         log("read ceiling")
         line_ceiling = read_ceiling_leg(ctx)
+    log("step ending in TOPK-32")
+    stt, topk_step = topk_step_leg(st, ctx, stream, args, ms_step)
     chained = stc = None
     if not args.no_chain:
         log("chained step")
@@ -1035,6 +1070,7 @@ def main():
     }
     if ordered:
         line["ordered"] = ordered
+    line["topk_step"] = topk_step
     if c0:
         line["c0"] = c0
         line["read_ceiling"] = line_ceiling
@@ -1070,6 +1106,8 @@ def main():
         log("cpu baseline and parity")
         line["cpu_baseline"] = cpu_baseline(st, args.cpu_seconds, keep, keep_ffn, keep_head,
                                             imgs=imgs)
+        log("TOPK-32 step parity")
+        topk_step["parity"] = chain_check(stt, imgs)
         if stc is not None:
             log("chained parity")
             imgs_c = sc.images(stc)
@@ -1103,6 +1141,7 @@ def main():
                 [p["ms_per_step"] for p in perc])
     if stc is not None:
         stc.close()
+    stt.close()
     st.close()
     ctx.close()
     print(json.dumps(line, default=_plain), flush=True)

@@ -77,6 +77,7 @@ SIGNATURES = {
     "w4a8_plan_add_site_emul_res": [_P, _P, _I32, _P, _P, _P, _P, _P],
     "w4a8_plan_add_mlp": [_P, _P, _P, _P, _I32, _I32, _I32, _P, _P, _I32, _I32, _P, _P],
     "w4a8_plan_add_head": [_P, _P, _I32, _P, _P, _I32, _I32, _I32, _P],
+    "w4a8_plan_add_head_topk32": [_P, _P, _I32, _P, _P, _I32, _I32, _I32, _P],
     "w4a8_plan_set_mode": [_P, _I32],
     "w4a8_plan_set_fences": [_P, _I32],
     "w4a8_plan_fences": [_P, _I32, _P],

@@ -184,7 +184,8 @@ int take_err(w4a8_ctx *c) {
   HIP_TRY(hipMemcpy(&h, c->d_err, sizeof(h), hipMemcpyDeviceToHost));
   if (h) {
     HIP_TRY(hipMemset(c->d_err, 0, sizeof(int32_t)));
-    if (h & 1) return fail(W4A8_E_Y32_OVF, "y32 overflow — sh miscomputed");
+    // a wait that gave up leaves the launch's results undefined (an
+    // overflow found after it is one of them), so it is reported first
     if (h & 2)
       return fail(W4A8_E_HIP, "a persistent plan's wait for other workgroups timed out "
                             "(are all of its workgroups resident? another long-running "
@@ -194,6 +195,7 @@ int take_err(w4a8_ctx *c) {
       return fail(W4A8_E_HIP, "a wait between wavefronts of one workgroup timed out");
     if (h & 8)
       return fail(W4A8_E_HIP, "TOPK-32's wait for the lists of earlier chunks timed out");
+    if (h & 1) return fail(W4A8_E_Y32_OVF, "y32 overflow — sh miscomputed");
     if (h & 16) return fail(W4A8_E_RANGE, "MOVX source is not int8-packed");
   }
   return W4A8_OK;
@@ -1163,6 +1165,7 @@ struct w4a8_plan {
     GemvParams P;
     int grid;
     bool head;
+    bool topk;          // a head ending in TOPK-32 (result: 66 int32) instead of the argmax
     int32_t *result;
   };
   std::vector<Step> steps;
@@ -1183,6 +1186,11 @@ struct w4a8_plan {
   // words, head partials): a graph the caller captured from an earlier run
   // still points at them, so they are freed only by destroy
   std::vector<void *> retired;
+  // a TOPK-32 head: its rows' y32 (graph mode: int32; persistent: 8-byte
+  // stamped words), the scan's lists, and (persistent) the scan's flags
+  uint64_t *d_topk_y = nullptr;
+  uint8_t *d_topk_lists = nullptr;
+  int32_t *d_topk_flags = nullptr;
   bool dependent = false;           // some site waits for, or forms, others' results
   int G = 0;
   int head_site = -1;
@@ -1237,7 +1245,7 @@ static void step_ranges(const w4a8_plan::Step &st, std::vector<ByteRange> &rd,
   add(wr, P.x8_out, P.K);
   add(wr, P.e_x_out, 4);
   add(wr, P.xn_out, 2 * (int64_t)P.K);
-  if (st.head) add(wr, st.result, 2 * sizeof(int32_t));
+  if (st.head) add(wr, st.result, (st.topk ? 66 : 2) * (int64_t)sizeof(int32_t));
 }
 static bool ranges_meet(const std::vector<ByteRange> &a, const std::vector<ByteRange> &b) {
   for (const auto &x : a)
@@ -1372,6 +1380,7 @@ static int plan_build_persistent(w4a8_plan *p) {
       p->head_result = p->steps[i].result;
     }
   p->G = plan_grid(p);
+  const bool topk = p->head_site >= 0 && p->steps[p->head_site].topk;
   std::vector<GemvParams> sites(n);
   // tile t of site s goes to workgroup (off_s + t) mod G: the tiles of
   // consecutive sites continue one round-robin, so every workgroup's share
@@ -1425,6 +1434,12 @@ static int plan_build_persistent(w4a8_plan *p) {
                                           : nullptr;
     // a site reading a product formed by its producer is a DYNQ8 site of it
     if (src[i].job == kProduct) sites[i].pro = PRO_DYNQ8;
+    // the TOPK-32 head's rows go out as stamped words, for the scan that runs
+    // in the same launch
+    if (topk && i == p->head_site) {
+      sites[i].job[0].epi = EPI_TOPK;
+      sites[i].job[0].out = p->d_topk_y;
+    }
     // stream_kernel's residual ADD: an EPI_MOVY_I16 job with res_out set
     for (int k = 0; k < sites[i].njobs; ++k) {
       GemvJob &J = sites[i].job[k];
@@ -1432,6 +1447,8 @@ static int plan_build_persistent(w4a8_plan *p) {
       else J.res_out = nullptr;
     }
   }
+  if (topk && !p->d_topk_flags)
+    HIP_TRY(hipMalloc(&p->d_topk_flags, sizeof(int32_t) * kTopkFlagWords));
   p->epoch = 0;
   HIP_TRY(hipMemcpy(p->d_sites, sites.data(), sizeof(GemvParams) * (size_t)n,
                     hipMemcpyHostToDevice));
@@ -1448,17 +1465,32 @@ static int plan_launch_persistent(w4a8_plan *p, hipStream_t s, hipEvent_t e0,
   // captures (each replay of the graph stores the same values).
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   HIP_TRY(hipStreamIsCapturing(s, &cs));
+  const bool topk = p->head_site >= 0 && p->steps[p->head_site].topk;
+  const int64_t topk_rows = topk ? p->steps[p->head_site].P.job[0].nrows : 0;
+  // (the TOPK-32 scan's flags hold 2 epoch + 1 in an int32)
   if (p->epoch == 0 || cs != hipStreamCaptureStatusNone ||
-      (uint64_t)(p->epoch + 1) * (uint64_t)(n + 1) > 0xFFFFFFFFull) {
+      (uint64_t)(p->epoch + 1) * (uint64_t)(n + 1) > 0xFFFFFFFFull ||
+      (topk && p->epoch + 1 >= (uint32_t)kTopkEpochMax)) {
     HIP_TRY(launch_fill_i32((int32_t *)p->d_done, 0, (int64_t)stream_counter_words(p->G, n), s));
     if (p->stamped_words > 0)
       HIP_TRY(launch_fill_i32((int32_t *)p->d_stamped, 0, 2 * p->stamped_words, s));
+    if (topk) {
+      HIP_TRY(launch_fill_i32(p->d_topk_flags, 0, kTopkFlagWords, s));
+      HIP_TRY(launch_fill_i32((int32_t *)p->d_topk_y, 0, 2 * topk_rows, s));
+    }
     p->epoch = 0;
   }
   StreamParams sp{};
   sp.sites = p->d_sites;
   sp.nsites = (int32_t)n;
-  sp.head_site = p->head_site;
+  sp.head_site = topk ? -1 : p->head_site;
+  if (topk) {
+    sp.topk_y = p->d_topk_y;
+    sp.topk_lists = (uint64_t *)p->d_topk_lists;
+    sp.topk_flags = p->d_topk_flags;
+    sp.topk_out = p->head_result;
+    sp.topk_rows = (int32_t)topk_rows;
+  }
   sp.done = p->d_done;
   sp.epoch = ++p->epoch;
   sp.stage = p->d_stage;
@@ -1485,6 +1517,17 @@ static void plan_drop_graph(w4a8_plan *p) {
 
 static int plan_enqueue(w4a8_plan *p, hipStream_t s) {
   for (auto &st : p->steps) {
+    if (st.topk) {
+      // the head's raw y32 (shift 0, seq_format.py:2225-2226), then the scan
+      GemvParams P = st.P;
+      P.job[0].epi = EPI_Y32;
+      P.job[0].out = p->d_topk_y;
+      HIP_TRY(launch_gemv(P, st.grid, s));
+      int rc = topk_launch(p->ctx, (const int32_t *)p->d_topk_y, P.job[0].nrows,
+                           p->d_topk_lists, st.result);
+      if (rc) return rc;
+      continue;
+    }
     HIP_TRY(launch_gemv(st.P, st.grid, s));
     if (st.head) HIP_TRY(launch_argmax_final(st.P.partials, st.grid, st.result, s));
   }
@@ -1639,6 +1682,37 @@ int w4a8_plan_add_head(w4a8_plan *p, const w4a8_weights *w, int32_t prologue,
   return W4A8_OK;
 }
 
+int w4a8_plan_add_head_topk32(w4a8_plan *p, const w4a8_weights *w, int32_t prologue,
+                              const void *d_x, const int16_t *d_norm_w, int32_t in_f,
+                              int32_t one_plus, int32_t e_x, int32_t *d_out) {
+  if (!p || !d_out) return fail(W4A8_E_ARG, "null argument");
+  for (auto &o : p->steps)
+    if (o.topk) return fail(W4A8_E_ARG, "a plan takes one TOPK-32 head");
+  w4a8_plan::Step st{};
+  int rc = head_params(p->ctx, st.P, w, prologue, d_x, d_norm_w, in_f, one_plus, e_x);
+  if (rc) return rc;
+  DeviceGuard g(p->ctx->device);
+  // y32 of every row: int32 in graph mode, 8-byte stamped words in a
+  // persistent launch; the scan's lists (the plan's own, so that graphs of
+  // it hold them)
+  const size_t yb = ((size_t)w->nrows * 8 + 255) & ~(size_t)255;
+  uint8_t *buf = nullptr;
+  HIP_TRY(hipMalloc(&buf, yb + topk_scratch_bytes(w->nrows)));
+  HIP_TRY(hipMemset(buf, 0, yb));
+  if (p->d_topk_y) p->retired.push_back(p->d_topk_y);
+  p->d_topk_y = (uint64_t *)buf;
+  p->d_topk_lists = buf + yb;
+  st.P.job[0].epi = EPI_Y32;
+  st.P.job[0].out = p->d_topk_y;
+  st.grid = grid_for(p->ctx, st.P.total_tiles);
+  st.head = true;
+  st.topk = true;
+  st.result = d_out;
+  p->steps.push_back(st);
+  plan_drop_graph(p);
+  return W4A8_OK;
+}
+
 int w4a8_plan_set_mode(w4a8_plan *p, int32_t mode) {
   if (!p || (mode != W4A8_PLAN_GRAPH && mode != W4A8_PLAN_PERSISTENT &&
              mode != W4A8_PLAN_PERSISTENT_COOP))
@@ -1747,6 +1821,20 @@ int w4a8_plan_profile(w4a8_plan *p, int32_t n, float *ms) {
     if (hipEventCreate(&e) != hipSuccess) rc = fail(W4A8_E_HIP, "hipEventCreate");
   for (size_t i = 0; !rc && i < p->steps.size(); ++i) {
     auto &st = p->steps[i];
+    if (st.topk) {
+      // the head's y32 (st.P: EPI_Y32 into the plan's buffer), then its scan;
+      // the step's time covers both
+      hipError_t e = launch_gemv_timed(st.P, st.grid, c->stream, ev[2 * i], nullptr);
+      if (e != hipSuccess) {
+        rc = fail(W4A8_E_HIP, hipGetErrorString(e));
+        break;
+      }
+      rc = topk_launch(c, (const int32_t *)p->d_topk_y, st.P.job[0].nrows, p->d_topk_lists,
+                       st.result);
+      if (!rc && hipEventRecord(ev[2 * i + 1], c->stream) != hipSuccess)
+        rc = fail(W4A8_E_HIP, "hipEventRecord");
+      continue;
+    }
     hipError_t e = launch_gemv_timed(st.P, st.grid, c->stream, ev[2 * i], ev[2 * i + 1]);
     if (e == hipSuccess && st.head)
       e = launch_argmax_final(st.P.partials, st.grid, st.result, c->stream);
@@ -1798,6 +1886,8 @@ int w4a8_plan_destroy(w4a8_plan *p) {
   if (p->d_partials) (void)hipFree(p->d_partials);
   for (void *t : p->temps) (void)hipFree(t);
   for (void *q : p->retired) (void)hipFree(q);
+  if (p->d_topk_y) (void)hipFree(p->d_topk_y);
+  if (p->d_topk_flags) (void)hipFree(p->d_topk_flags);
   delete p;
   return W4A8_OK;
 }

@@ -50,9 +50,12 @@ constexpr int kWaves = kWG / 64;
 enum Prologue { PRO_X8 = 0, PRO_DYNQ8 = 1, PRO_RMSNORM_DYNQ8 = 2, PRO_EMUL_DYNQ8 = 3 };
 // EPI_MOVY_I16_ADD: EPI_MOVY_I16 into out (when set), and
 // clip16(res[row] + that) into res_out (ALU ADD, the block's residual).
+// EPI_TOPK (persistent plans' TOPK-32 head): the raw y32 of each row as an
+// 8-byte word {y32, the site's stamp} at (uint64_t *)out + row, for the
+// TOPK-32 scan that runs in the same launch.
 enum Epilogue {
   EPI_Y32 = 0, EPI_MOVY_I16 = 1, EPI_MOVY_P32 = 2, EPI_SILU32 = 3,
-  EPI_SHIFT_I64 = 4, EPI_ARGMAX = 5, EPI_MOVY_I16_ADD = 6
+  EPI_SHIFT_I64 = 4, EPI_ARGMAX = 5, EPI_MOVY_I16_ADD = 6, EPI_TOPK = 7
 };
 constexpr int kEmulP0 = 12;   // EMUL32's shift in the SwiGLU block
 
@@ -189,6 +192,16 @@ struct StreamParams {
   uint32_t grid_spin;       // polls before a wait for other workgroups gives up
                             // (err bit 1); 0: the kernel's default
   uint32_t lds_spin;        // ... a wait within the workgroup (err bit 2); 0: default
+  // A TOPK-32 head (the last site, EPI_TOPK; head_site is then -1): its rows'
+  // stamped words (topk_rows of them), the chunk and super-chunk lists
+  // (topk_scratch_bytes), the scan's flags (kTopkFlagWords, compared with
+  // epoch, which stays below kTopkEpochMax) and the result vals[32],
+  // rows[32], count, overflow; topk_out null: no TOPK-32 head
+  const uint64_t *topk_y;
+  uint64_t *topk_lists;
+  int32_t *topk_flags;
+  int32_t *topk_out;
+  int32_t topk_rows;
 };
 // one workgroup per CU; `cooperative`: through the cooperative launch API.
 // `dependent`: the kernel built for plans with dependent sites (any site
@@ -230,6 +243,7 @@ constexpr int kTopkMaxChunks = 17 * kTopkSuper;   // 2^18 rows: 256 + 1 chunks
 constexpr int kTopkFlagWords = 2 * kTopkMaxChunks + kTopkMaxChunks / kTopkSuper;
 constexpr int32_t kTopkEpochMax = 1 << 29;
 size_t topk_scratch_bytes(int64_t n);
+int topk_chunks(int64_t n);   // chunks of the scan over n rows
 hipError_t launch_topk32(const int32_t *y, int64_t n, void *scratch, int32_t *flags,
                          int32_t epoch, int32_t *out, int32_t *err, hipStream_t s,
                          uint32_t spin = 0);   // polls before a wait gives up; 0: default

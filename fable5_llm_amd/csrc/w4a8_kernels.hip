@@ -759,6 +759,7 @@ hipError_t launch_gemv_timed(const GemvParams &p, int grid, hipStream_t s,
 
 hipError_t launch_argmax_final(const uint64_t *partials, int n, int32_t *result,
                                hipStream_t s) {
+  if (!partials || !result || n < 1) return hipErrorInvalidValue;
   hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kWG), 0, s, partials, n,
                      result);
   return hipGetLastError();

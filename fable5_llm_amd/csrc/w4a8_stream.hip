@@ -41,6 +41,7 @@
 #include <hip/hip_ext.h>
 
 #include "w4a8_device.h"
+#include "w4a8_topk_device.h"
 
 namespace w4a8 {
 
@@ -96,6 +97,8 @@ struct __align__(16) Lds {
   int64_t pss[kPW];                 // prologue partial sums of squares
   int32_t pmx[kPW];                 // prologue partial maxima
   uint64_t best;                    // argmax key of the head's rows seen here (0: none)
+  uint64_t tkbuf[128];              // TOPK-32 head: the scan's key buffer ...
+  int32_t tkrows[tk::kTkRows];      // ... and its chunk's values (prologue wavefront 0)
 };
 
 // The workgroup's LDS block.
@@ -284,6 +287,7 @@ __device__ __forceinline__ void tile_epilogue(Lds &L, int kt, CJob &J, int tl, i
           break;
         case EPI_SILU32: outv = silu32(y, shift, L.sig); break;
         case EPI_SHIFT_I64: outv = movy_shift(y, shift); break;
+        case EPI_TOPK: outv = y; break;   // raw y32, as for the argmax
         default:   // EPI_ARGMAX: raw y32, seq_format.py:2225-2226
           lds_max_u64(&L.best, argmax_key((int32_t)y, (uint32_t)row));
 
@@ -363,6 +367,12 @@ __device__ void ctrl_serve(CSite &P, Lds &L, int kt0, int r, int G, int lane, ui
           case EPI_MOVY_I16:
           case EPI_SILU32: store_coherent((int16_t *)J.out + row, (int16_t)v); break;
           case EPI_SHIFT_I64: store_coherent((int64_t *)J.out + row, v); break;
+          case EPI_TOPK:
+            // {y32, stamp}: an 8-byte store lands whole, so the scan, seeing
+            // this launch's stamp, sees the value
+            store_coherent((uint64_t *)J.out + row,
+                           (uint64_t)(uint32_t)(int32_t)v | ((uint64_t)stamp << 32));
+            break;
           default: store_coherent((int32_t *)J.out + row, (int32_t)v); break;
         }
       }
@@ -951,6 +961,75 @@ __device__ __forceinline__ void prologue_role(const GemvParams *sites_arg, int n
   if (!(ok && ps.ok) && lane == 0) lds_or_i32(&L.err, 4);
 }
 
+// The TOPK-32 head's scan, by prologue wavefront 0 of workgroup r once the
+// plan's last prologue is done: chunks c = r, r + G, ... of the scan of
+// w4a8_topk_device.h, each as soon as its rows' stamped words all carry
+// this launch's stamp -- while the head still streams its later tiles.  A
+// chunk's rows are stored by other workgroups' control wavefronts, which
+// never wait for a prologue wavefront once the head's activations are
+// ready; a chunk waits only for the lists of lower-numbered chunks, so
+// every wait ends as long as every workgroup is resident (bounded: err bit
+// 3).  Only in the kernel instances for plans with a TOPK-32 head.
+__device__ __forceinline__ void topk_role(const uint64_t *ys, uint64_t *lists, int32_t *flags,
+                                       int32_t *out, int32_t n, uint32_t stamp, uint32_t epoch,
+                                       int32_t *err, uint32_t spin, int r, int G) {
+  Lds &L = g_lds;
+  ys = (const uint64_t *)uniform_ptr(ys);
+  lists = (uint64_t *)uniform_ptr(lists);
+  flags = (int32_t *)uniform_ptr(flags);
+  out = (int32_t *)uniform_ptr(out);
+  err = (int32_t *)uniform_ptr(err);
+  n = __builtin_amdgcn_readfirstlane(n);
+  stamp = __builtin_amdgcn_readfirstlane(stamp);
+  epoch = __builtin_amdgcn_readfirstlane(epoch);
+  spin = __builtin_amdgcn_readfirstlane(spin);
+  r = __builtin_amdgcn_readfirstlane(r);
+  G = __builtin_amdgcn_readfirstlane(G);
+  const int lane = threadIdx.x & 63;
+  const bool up = tk::tk_ror4_up();
+  const int nchunks = n <= tk::kTkFirst ? 1 : 1 + (n - tk::kTkFirst + tk::kTkRows - 1) / tk::kTkRows;
+  uint64_t *part = lists, *sup = lists + (size_t)nchunks * tk::kTk;
+  bool ok = true;
+  for (int c = r; c < nchunks; c += G) {
+    const int64_t s0 = tk::chunk_first(c), end = tk::chunk_end(c, n);
+    // the chunk's words through a buffer whose range ends with them: lanes
+    // past the end read zero and count as arrived
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(ys + s0), (short)0, (int)((end - s0) * 8), kBufDword3);
+    int32_t yv[tk::kTkPerLane];
+    // First a light poll, one word per tile (lane l: the first row of the
+    // chunk's tile l; a tile's rows are stored by one instruction), so that
+    // the wait for a chunk whose rows come late -- the last chunks wait for
+    // most of the head -- takes 512 bytes a poll instead of 8 KB from the
+    // weight stream's bandwidth.
+    bool all = false;
+    for (uint32_t it = 0; it < spin && !all; ++it) {
+      if (it > 0) __builtin_amdgcn_s_sleep(8);
+      typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+      const u2 w = __builtin_amdgcn_raw_buffer_load_b64(rs, lane * kTileRows * 8, 0, kAuxSc1);
+      all = __all(s0 + lane * kTileRows >= end || w.y == stamp);
+    }
+    all = false;
+    for (uint32_t it = 0; it < spin && !all; ++it) {
+      if (it > 0) __builtin_amdgcn_s_sleep(2);
+      bool mine = true;
+#pragma unroll
+      for (int t = 0; t < tk::kTkPerLane; ++t) {
+        const int i = lane + 64 * t;
+        typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+        const u2 w = __builtin_amdgcn_raw_buffer_load_b64(rs, i * 8, 0, kAuxSc1);
+        yv[t] = (int32_t)w.x;
+        mine = mine && (s0 + i >= end || w.y == stamp);
+      }
+      all = __all(mine);
+    }
+    ok = ok && all;
+    ok = tk::chunk_run(yv, L.tkrows, L.tkbuf, n, nchunks, c, (int32_t)epoch, part, sup, flags,
+                       out, spin, up, lane) && ok;
+  }
+  if (!ok && lane == 0) atomicOr(err, 8);
+}
+
 // The weight wavefronts' program.  (As a function of its own, with a
 // register allocation apart from the other roles', it ran 1-2 % slower on
 // the independent-input stream and 2.5 % slower on the chained one than
@@ -1036,8 +1115,9 @@ __device__ __forceinline__ void weight_role(const GemvParams *sites_arg, int nsi
 // kSpin: the context set its own spin limits (a test of the give-up paths);
 // otherwise the limits are the compile-time defaults, which the waits fold
 // in (runtime limits everywhere cost 1 % on the independent-input stream and
-// 5 % on the chained one)
-template <bool kDep, bool kSpin>
+// 5 % on the chained one).  kTopk: the plan ends in a TOPK-32 head (the scan
+// code stays out of the other instances)
+template <bool kDep, bool kSpin, bool kTopk>
 __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
                                                           const GemvParams *__restrict__ sites_arg) {
   CSite *sites = (CSite *)sites_arg;
@@ -1102,6 +1182,10 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
   } else if (wave >= kPW0) {
     prologue_role<kDep>(sites_arg, S.nsites, r, G, wave, S.done, S.stage, S.epoch, S.err,
                         gspin, lspin);
+    // the TOPK-32 head is the last site: its stamp is that of site nsites - 1
+    if (kTopk && wave == kPW0)
+      topk_role(S.topk_y, S.topk_lists, S.topk_flags, S.topk_out, S.topk_rows,
+                fbase + (uint32_t)nsites, S.epoch, S.err, gspin, r, G);
   } else {
     weight_role<kDep>(sites_arg, nsites, r, G, wave, lspin);
   }
@@ -1124,8 +1208,15 @@ hipError_t launch_stream(const StreamParams &sp, int grid, hipStream_t s, bool c
                          bool dependent, hipEvent_t start, hipEvent_t stop) {
   const GemvParams *sites = sp.sites;
   const bool spin = sp.grid_spin || sp.lds_spin;
-  auto kernel = dependent ? (spin ? stream_kernel<true, true> : stream_kernel<true, false>)
-                          : (spin ? stream_kernel<false, true> : stream_kernel<false, false>);
+  auto kernel =
+      sp.topk_out
+          ? (dependent ? (spin ? stream_kernel<true, true, true> : stream_kernel<true, false, true>)
+                       : (spin ? stream_kernel<false, true, true>
+                               : stream_kernel<false, false, true>))
+          : (dependent ? (spin ? stream_kernel<true, true, false>
+                               : stream_kernel<true, false, false>)
+                       : (spin ? stream_kernel<false, true, false>
+                               : stream_kernel<false, false, false>));
   if (cooperative) {
     void *args[] = {(void *)&sp, (void *)&sites};
     hipError_t e = start ? hipEventRecord(start, s) : hipSuccess;
@@ -1142,8 +1233,10 @@ hipError_t launch_stream(const StreamParams &sp, int grid, hipStream_t s, bool c
 
 int stream_max_blocks_per_cu() {
   int n = 1 << 30;
-  for (auto k : {stream_kernel<false, false>, stream_kernel<true, false>,
-                 stream_kernel<false, true>, stream_kernel<true, true>}) {
+  for (auto k : {stream_kernel<false, false, false>, stream_kernel<true, false, false>,
+                 stream_kernel<false, true, false>, stream_kernel<true, true, false>,
+                 stream_kernel<false, false, true>, stream_kernel<true, false, true>,
+                 stream_kernel<false, true, true>, stream_kernel<true, true, true>}) {
     int m = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&m, k, kThreads, 0) != hipSuccess) return 1;
     n = m < n ? m : n;

@@ -523,6 +523,22 @@ class Plan:
         self.nsites += 1
         self.nmats += 1
 
+    def add_head_topk32(self, w, x, out, prologue=N.PRO_DYNQ8, e_x=0, norm_w=None,
+                        in_f=0, one_plus=False):
+        """The LM head ending in TOPK-32 (docs/SEQ_ISA.md B8): out (66 int32)
+        gets vals[32], rows[32], count, overflow.  One per plan, its last
+        step in a persistent plan, where the scan runs in the same launch."""
+        _dev(x, _x_bytes(prologue, w.K), "x")
+        _dev(norm_w, 2 * w.K, "norm_w", required=False)
+        _dev(out, 66 * 4, "out")
+        N.check(N.lib().w4a8_plan_add_head_topk32(
+            self.h, w.h, int(prologue), _dptr(x), _dptr(norm_w), int(in_f),
+            1 if one_plus else 0, int(e_x), _dptr(out)), "plan_add_head_topk32")
+        self._keep += [w, x, out, norm_w]
+        self.bytes += w.wire_bytes
+        self.nsites += 1
+        self.nmats += 1
+
     def set_mode(self, mode):
         N.check(N.lib().w4a8_plan_set_mode(self.h, int(mode)), "plan_set_mode")
 

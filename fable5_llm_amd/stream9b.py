@@ -236,15 +236,18 @@ class Stream9B:
     step; only the first site's input (`x0`) is seeded, and the weights'
     scales are CHAIN_LOG2_LO's.
     weights_from: another Stream9B whose resident matrices this one uses
-    (same schedule) instead of uploading its own."""
+    (same schedule) instead of uploading its own.
+    head_topk: the head ends in TOPK-32 (its output: vals[32], rows[32],
+    count, overflow) instead of the argmax, as a sampling step's would."""
 
     def __init__(self, ctx, seed=0, sites=None, mode=N.PLAN_PERSISTENT, fences=N.FENCE_ALL,
-                 chain=False, weights_from=None):
+                 chain=False, weights_from=None, head_topk=False):
         import torch
         from .engine import Plan
         self.ctx = ctx
         self.sites = sites or schedule()
         self.chain = chain
+        self.head_topk = head_topk
         self.src = chain_sources(self.sites) if chain else [None] * len(self.sites)
         self.emul = emul_sources(self.sites) if chain else [None] * len(self.sites)
         log2_lo = CHAIN_LOG2_LO if chain else -10.0
@@ -279,15 +282,17 @@ class Stream9B:
                 ws = list(weights_from.weights[si])
             for m in s.mats:
                 if s.head:
-                    outs.append(torch.zeros(2, dtype=torch.int32, device=dev))
+                    outs.append(torch.zeros(66 if head_topk else 2, dtype=torch.int32,
+                                            device=dev))
                 else:
                     dt = torch.int32 if m.epi == N.EPI_MOVY_P32 else torch.int16
                     outs.append(torch.zeros(m.nrows, dtype=dt, device=dev))
             ctx.sync()
             del imgs
             if s.head:
-                self.plan.add_head(ws[0], x, outs[0], prologue=s.prologue, norm_w=nw,
-                                   in_f=s.in_f, one_plus=s.one_plus)
+                add = self.plan.add_head_topk32 if head_topk else self.plan.add_head
+                add(ws[0], x, outs[0], prologue=s.prologue, norm_w=nw, in_f=s.in_f,
+                    one_plus=s.one_plus)
                 # the head's DYNQ8 input is not exported by the fused launch
                 x8 = None
             elif self.emul[si] is not None:

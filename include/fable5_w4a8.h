@@ -360,6 +360,18 @@ int w4a8_plan_add_head(w4a8_plan *plan, const w4a8_weights *w,
                        int32_t prologue, const void *d_x,
                        const int16_t *d_norm_w, int32_t in_f, int32_t one_plus,
                        int32_t e_x, int32_t *d_result);
+/* The LM head ending in TOPK-32 instead of the argmax: the layer_topk32
+ * block fed from the AMAX32 compare site in the same pass over the rows
+ * (docs/SEQ_ISA.md:582-610; the sampling loop reads it,
+ * sw/chat_seq.py:284-291).  d_out: vals[32], rows[32], count, overflow as
+ * w4a8_head_topk32_async.  One per plan; in a persistent plan it is the last
+ * step and its scan runs inside the same launch, chunk by chunk as the
+ * head's rows are stored; in graph mode the head's y32 is followed by the
+ * TOPK-32 kernel. */
+int w4a8_plan_add_head_topk32(w4a8_plan *plan, const w4a8_weights *w,
+                              int32_t prologue, const void *d_x,
+                              const int16_t *d_norm_w, int32_t in_f, int32_t one_plus,
+                              int32_t e_x, int32_t *d_out);
 int w4a8_plan_set_mode(w4a8_plan *plan, int32_t mode);
 /* no counterpart in the reference (its sequencer orders every record): how
    a persistent plan orders its sites, W4A8_FENCE_ALL or W4A8_FENCE_AUTO */

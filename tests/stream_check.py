@@ -47,8 +47,15 @@ def oracle_prologue(s, h, x16=None, x2=None):
     return law.dyn_quant_i8(x)
 
 
-def oracle_epilogue(s, m, y, e):
-    """The site's output for matrix m from its y32 and the site's e_x."""
+def oracle_epilogue(s, m, y, e, topk=False):
+    """The site's output for matrix m from its y32 and the site's e_x (a
+    TOPK-32 head: vals[32], rows[32], count, overflow)."""
+    if s.head and topk:
+        vals, rows, count, ovf = law.topk32(y)
+        out = np.zeros(66, dtype=np.int64)
+        out[:count], out[32:32 + count] = vals, rows
+        out[64], out[65] = count, int(ovf)
+        return out
     if s.head:
         return np.array(law.amax32(y), dtype=np.int64)
     shift = m.p0(s.in_f) - e
@@ -84,7 +91,7 @@ def run_cpu_stream(st, host, nthreads=0):
             y = cfast.matvec_y32_img(img, m.nrows, m.K, sh_for_k(m.K), x8, nthreads)
             t += time.perf_counter() - t0
             ys.append(y)
-            outs.append(oracle_epilogue(s, m, y, e))
+            outs.append(oracle_epilogue(s, m, y, e, getattr(st, "head_topk", False)))
         ref.append(dict(x8=x8, e=e, ys=ys, outs=outs))
     return ref, t
 

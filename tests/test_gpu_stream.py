@@ -33,14 +33,14 @@ def _mode_name(mode, fences):
         ("/auto" if fences == N.FENCE_AUTO else "/all")
 
 
-def _check_modes(engine, chain, weight_seed):
+def _check_modes(engine, chain, weight_seed, head_topk=False, seeds=SEEDS):
     base = stream9b.Stream9B(engine, seed=weight_seed, chain=chain, mode=MODES[0][0],
-                             fences=MODES[0][1])
+                             fences=MODES[0][1], head_topk=head_topk)
     views = [base] + [stream9b.Stream9B(engine, chain=chain, weights_from=base, mode=m,
-                                        fences=f) for m, f in MODES[1:]]
+                                        fences=f, head_topk=head_topk) for m, f in MODES[1:]]
     try:
         imgs = sc.images(base)
-        for seed in SEEDS:
+        for seed in seeds:
             ref = None
             for st, (m, f) in zip(views, MODES):
                 st.reseed(seed)
@@ -72,6 +72,16 @@ def test_full_stream_bit_exact(engine):
 
 def test_chained_stream_bit_exact(engine):
     _check_modes(engine, chain=True, weight_seed=11)
+
+
+# A sampling step: the same streams ending in a TOPK-32 head
+# (w4a8_plan_add_head_topk32), whose scan runs inside the persistent launch.
+def test_full_stream_topk_head_bit_exact(engine):
+    _check_modes(engine, chain=False, weight_seed=13, head_topk=True, seeds=SEEDS[:2])
+
+
+def test_chained_stream_topk_head_bit_exact(engine):
+    _check_modes(engine, chain=True, weight_seed=17, head_topk=True, seeds=SEEDS[:2])
 
 
 def test_chained_fences_derived(engine):
