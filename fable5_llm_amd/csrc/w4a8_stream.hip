@@ -52,7 +52,7 @@ constexpr int kCtrl = kCW;                  // the control wavefront
 constexpr int kPW = 3;                      // prologue wavefronts
 constexpr int kPW0 = kCW + 1;               // ... 9..11
 constexpr int kThreads = (kPW0 + kPW) * 64; // 768
-constexpr int kNB = 6;                      // activation buffers
+constexpr int kNB = 8;                      // activation buffers (a power of 2)
 constexpr int kXloOff = kKMax;              // int32 corrections after x8
 constexpr int kXB = kKMax + kKMax / 8;      // x8 + corrections of one site
 constexpr int kTSlots = 32;                 // tiles being reduced at once
@@ -785,16 +785,32 @@ __device__ PSync compute_publish(CSite &P, Lds &L, int8_t *stg, uint32_t *flag, 
   return ps;
 }
 
-// the wavefront waits until site s's activations are staged in this launch
-// (bounded; bit 1 of err, as for the grid-wide wait)
-__device__ __forceinline__ bool wait_staged(const uint32_t *flag, uint32_t epoch, int lane,
-                                            int32_t *err, uint32_t gspin) {
-  for (uint32_t n = 0; n < gspin; ++n) {
-    if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= epoch) return true;
+// The wavefront waits until the first `need` of sites s .. s + n - 1 (flags
+// flag[0 .. n), need <= n <= 64) have their activations staged in this
+// launch, and returns how many of the n, from the first, are (bounded; on
+// giving up it returns fewer than need, with bit 1 of err, as for the
+// grid-wide wait).
+constexpr int kStageBatch = 4;   // staged sites copied per round trip, at most ...
+constexpr int kStageBlocks = 2 * kCW;   // ... with this many weight blocks per CU in all
+static_assert(kStageBatch < kNB, "a batch's buffers are free together");
+// a site's weight blocks on one CU, at most
+__device__ __forceinline__ int site_blocks(CSite &P, int G) {
+  return (P.total_tiles + G - 1) / G * P.nblk;
+}
+__device__ __forceinline__ int wait_staged_n(const uint32_t *flag, int n, int need,
+                                             uint32_t epoch, int lane, int32_t *err,
+                                             uint32_t gspin) {
+  for (uint32_t it = 0; it < gspin; ++it) {
+    const bool mine = lane < n && __hip_atomic_load(flag + lane, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT) >= epoch;
+    // sites from the first on that are staged: the lowest lane that is not
+    const uint64_t notyet = ~__ballot(mine);
+    const int run = notyet ? __builtin_ctzll(notyet) : 64;
+    if (run >= need) return run < n ? run : n;
     __builtin_amdgcn_s_sleep(1);
   }
   if (lane == 0) atomicOr(err, 2);
-  return false;
+  return 0;
 }
 
 // copy a staged site (x8 [0, K), corrections [kXloOff, + K/8)) into LDS
@@ -944,19 +960,44 @@ __device__ __forceinline__ void prologue_role(const GemvParams *sites_arg, int n
       ps = compute_publish<kDep>(P, L, stage + (size_t)s * kStageBytes, sflag + s, epoch, pw,
                            lane, ps, lspin);
     }
-    if (s >= kNB) ok = wait_weights_past(L, s - kNB, lane, lspin) && ok;
-    ok = wait_staged(sflag + s, epoch, lane, err, gspin) && ok;
-    load_staged(stg, L.x[b], P.K, pw, lane);
-    const int e = __hip_atomic_load((const int32_t *)(stg + kXB), __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
-    wait_vm_all();
-    // this wavefront's copies into buffer b have landed (lds_write_i32
-    // waits for its LDS work first); the site is ready once all three
-    // have posted
-    if (lane == 0) {
-      if (pw == 0) lds_write_i32(&L.ex[b], e);
-      lds_write_i32(&L.ready[b][pw], s);
+    // Staged sites go in batches: the consecutive sites s .. e - 1 that wait
+    // for no other workgroup (their staging flags went up at launch start)
+    // are polled in one round trip, copied, and waited for once.  One site
+    // at a time, every site cost two dependent round trips behind the weight
+    // stream, about 2.5 us, which bounded runs of small sites.
+    // (only small sites go together: while the batch's blocks on this CU fit
+    // the weight wavefronts' registers; a large site's readiness would
+    // otherwise wait for the copies of the sites after it)
+    int e = s + 1;
+    if (P.fence_at == 0) {
+      int blocks = site_blocks(P, G);
+      while (e < nsites && e < s + kStageBatch && sites[e].fence_at == 0 &&
+             !(kDep && sites[e].local_pro) && blocks + site_blocks(sites[e], G) <= kStageBlocks) {
+        blocks += site_blocks(sites[e], G);
+        ++e;
+      }
     }
+    if (e - 1 >= kNB) ok = wait_weights_past(L, e - 1 - kNB, lane, lspin) && ok;
+    ok = wait_staged_n(sflag + s, e - s, e - s, epoch, lane, err, gspin) >= e - s && ok;
+    for (int t = s; t < e; ++t)
+      load_staged(stage + (size_t)t * kStageBytes, L.x[t % kNB], sites[t].K, pw, lane);
+    // lane j: e_x of site s + j
+    const int exj = lane < e - s ? __hip_atomic_load((const int32_t *)(stg + (size_t)lane *
+                                                                        kStageBytes + kXB),
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                 : 0;
+    wait_vm_all();
+    // this wavefront's copies into the batch's buffers have landed
+    // (lds_write_i32 waits for its LDS work first); a site is ready once all
+    // three have posted
+    for (int t = s; t < e; ++t) {
+      const int ex = __builtin_amdgcn_readlane(exj, t - s);
+      if (lane == 0) {
+        if (pw == 0) lds_write_i32(&L.ex[t % kNB], ex);
+        lds_write_i32(&L.ready[t % kNB][pw], t);
+      }
+    }
+    s = e - 1;
   }
   if (!(ok && ps.ok) && lane == 0) lds_or_i32(&L.err, 4);
 }
