@@ -275,7 +275,7 @@ int site_params(w4a8_ctx *c, GemvParams &P, int32_t nmat,
     P.job[i].w = w[i]->d;
     P.job[i].out = out[i];
     P.job[i].nrows = (int32_t)w[i]->nrows;
-    P.job[i].tile0 = (int32_t)tiles;
+    P.job[i].tile0 = P.tile0[i] = (int32_t)tiles;
     P.job[i].sh = w[i]->sh;
     P.job[i].epi = epi[i];
     P.job[i].p0 = p0[i];
@@ -317,7 +317,7 @@ int head_params(w4a8_ctx *c, GemvParams &P, const w4a8_weights *w, int32_t prolo
   P.job[0].w = w->d;
   P.job[0].out = nullptr;
   P.job[0].nrows = (int32_t)w->nrows;
-  P.job[0].tile0 = 0;
+  P.job[0].tile0 = P.tile0[0] = 0;
   P.job[0].sh = w->sh;
   P.job[0].epi = EPI_ARGMAX;
   P.job[0].p0 = 0;

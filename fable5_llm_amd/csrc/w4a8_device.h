@@ -146,10 +146,10 @@ __device__ __forceinline__ uint32_t scale_of(const uint4 &sc, int i) {
 
 template <typename PT>
 __device__ __forceinline__ int job_of(const PT &P, int tg) {
-  // unrolled over the fixed job table so every tile0 is loaded at once
+  // unrolled over the fixed table of first tiles, so they load at once
   int j = 0;
 #pragma unroll
-  for (int k = 1; k < kMaxJobs; ++k) j += (k < P.njobs && tg >= P.job[k].tile0) ? 1 : 0;
+  for (int k = 1; k < kMaxJobs; ++k) j += (k < P.njobs && tg >= P.tile0[k]) ? 1 : 0;
   return j;
 }
 

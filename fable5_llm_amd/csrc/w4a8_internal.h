@@ -112,17 +112,21 @@ struct GemvJob {
                         // bits) and the producing site's stamp (high 32 bits)
 };
 
+// A site.  The fields the weight loops read for every block come first,
+// in one 64-byte line (with each job's first tile, job_of's table), so that
+// a site's table entry costs its loops two scalar-cache lines, not seven.
 struct GemvParams {
-  GemvJob job[kMaxJobs];
   int32_t njobs;
   int32_t total_tiles;
   int32_t K, NG, nblk;
-  int32_t pro;
+  int32_t tile_rot;         // persistent stream: first tile of WG r is (r + tile_rot) % G
   int64_t tile_bytes;
+  int32_t tile0[kMaxJobs];  // job[j].tile0
+  int32_t pro;
+  GemvJob job[kMaxJobs];
   const void *x;            // int8[K] or int16[K]
   const int16_t *norm_w;    // int16[K] Q14 (RMSNorm)
   int32_t in_f, one_plus, e_x_given;
-  int32_t tile_rot;         // persistent stream: first tile of WG r is (r + tile_rot) % G
   int32_t fence;            // persistent stream: every earlier site completes on all
                             // workgroups before this one reads its activations
   int32_t fence_at;         // persistent stream: the last fenced site <= this one (0: none)
@@ -147,7 +151,10 @@ struct GemvParams {
   int32_t *err;             // bit 0: y32 overflow; bit 2: an LDS wait gave up
   uint64_t *partials;       // EPI_ARGMAX: one key per workgroup
   const int32_t *x2;        // PRO_EMUL_DYNQ8: int32[K]
+  int32_t pad_[2];          // (a whole number of 64-byte lines: in a site table, every
+                            // entry's first line is its own)
 };
+static_assert(sizeof(GemvParams) % 64 == 0, "site table entries start on a line");
 
 // launchers (all asynchronous on `s`)
 hipError_t launch_fill_i32(int32_t *p, int32_t v, int64_t n, hipStream_t s);

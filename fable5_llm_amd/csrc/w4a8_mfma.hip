@@ -1,7 +1,8 @@
 // Batched W4A8 (several tokens): int8 MFMA on gfx950 with the per-group
 // scale applied after accumulation.  Per token the result is bit-identical
 // to ref/w4a8_ref.py:254-289 matvec_y32: every group sum is exact in int32
-// (|16 * sum w*x| <= 2^21) and the scale products are summed in int64.
+// (|16 * sum w*x| <= 2^21) and the scale products are summed exactly (in
+// int64 or, below 2^53, in double precision).
 //
 // v_mfma_i32_16x16x64_i8: A = 16 weight rows x 64 k, B = 64 k x 16 tokens,
 // D = 16 x 16 int32.  Lane l feeds row/token (l % 16) and k-quarter l / 16
@@ -22,7 +23,7 @@
 //    of LDS slots, ahead of the group wavefronts, and flag each slot once its
 //    copies have landed.
 //  * 1 store wavefront: at the end of a round the 8 group wavefronts add
-//    their int64 sums into an LDS table (two tables, alternating by round);
+//    their sums into an LDS table (two tables, alternating by round);
 //    the store wavefront rounds, checks and stores the round's y32 and frees
 //    the table.  Group wavefronts thus issue no stores, which would make the
 //    compiler's count of their outstanding loads unknown.
@@ -36,6 +37,7 @@
 // job boundaries, so the weight stream does not drain between matrices.  Every wait between wavefronts is bounded: a wait that gives
 // up sets bit 2 of the error word and an abort word, after which no wait of
 // the workgroup polls again, so a launch always drains.
+#include <type_traits>
 #include <vector>
 
 #include "w4a8_device.h"
@@ -134,8 +136,27 @@ __device__ __forceinline__ int64_t rshr64_mm(int64_t v, int s) {
 __device__ __forceinline__ void mm_wait_vm_all() {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
-__device__ __forceinline__ void mm_lds_add_u64(int64_t *p, int64_t v) {
+__device__ __forceinline__ void mm_lds_add(double *p, double v) {
+  asm volatile("ds_add_f64 %0, %1" :: "v"(lds_off(p)), "v"(v) : "memory");
+}
+__device__ __forceinline__ void mm_lds_add(int64_t *p, int64_t v) {
   asm volatile("ds_add_u64 %0, %1" :: "v"(lds_off(p)), "v"(v) : "memory");
+}
+
+// The sums of scale x group products of a kernel instance: exact either
+// way (every product < 2^16 * 2^21, every partial sum < 96 groups * 2^37 <
+// 2^44: integers below 2^53), in double precision (full-rate FMAs) where two
+// or more column tiles give each scale several products, else in int64
+// (quarter-rate multiply-adds, but no conversions)
+template <int CTX>
+using MmAcc = typename std::conditional<(CTX >= 2), double, int64_t>::type;
+template <int CTX>
+__device__ __forceinline__ MmAcc<CTX> mm_scale(int32_t m) { return (MmAcc<CTX>)m; }
+__device__ __forceinline__ double mm_fma(double m, int32_t a, double p) {
+  return __builtin_fma(m, (double)a, p);
+}
+__device__ __forceinline__ int64_t mm_fma(int64_t m, int32_t a, int64_t p) {
+  return p + m * (int64_t)a;
 }
 __device__ __forceinline__ int32_t mm_lds_add_rtn(int32_t *p, int32_t v) {
   int32_t old;
@@ -311,7 +332,8 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
       return P.job[ju];
   };
   MmFlags &F = *(MmFlags *)smem;
-  int64_t *tables = (int64_t *)(smem + kFlagBytes);   // [2][TMX][CTX][4][64]
+  typedef MmAcc<CTX> Acc;
+  Acc *tables = (Acc *)(smem + kFlagBytes);   // [2][TMX][CTX][4][64]
   uint8_t *ring = smem + kFlagBytes + 2 * TMX * CTX * 4 * 64 * 8;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -376,7 +398,7 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
       const MmJob &J = JOB(jb);
       const int rho = RHO - F.rbase[jb];
       const int tb = RHO & 1, nt = round_tiles(J, F.nmine[jb], rho);
-      int64_t *tbl = tables + tb * (TMX * CTX * 4 * 64);
+      Acc *tbl = tables + tb * (TMX * CTX * 4 * 64);
       if (!mm_wait(F, [&] { return lds_read_i32(&F.tcnt[tb]) == kMW; })) {
         ok = false;
         break;
@@ -395,7 +417,7 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
         for (int ct = 0; ct < CTX; ++ct)
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            tot[jj][ct][e] = tbl[((jj * CTX + ct) * 4 + e) * 64 + lane];
+            tot[jj][ct][e] = (int64_t)tbl[((jj * CTX + ct) * 4 + e) * 64 + lane];
 #pragma unroll
       for (int jj = 0; jj < TMX; ++jj)
 #pragma unroll
@@ -492,7 +514,7 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
     const int w = wave;
     const int q = lane >> 4, c = lane & 15;
     constexpr int D = mm_depth<TMX, CTX>();
-    int64_t p[TMX][CTX][4];
+    Acc p[TMX][CTX][4];
 #pragma unroll
     for (int a = 0; a < TMX; ++a)
 #pragma unroll
@@ -531,28 +553,53 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
           bx[ct][0] = v4i{u0.x, u0.y, u0.z, u0.w};
           bx[ct][1] = v4i{u1.x, u1.y, u1.z, u1.w};
         }
+        // Two or more column tiles: every product of the step first, then
+        // the scales -- the MFMAs' results are read only after the last one
+        // is issued, so their latency passes under the others.  One column
+        // tile: tile by tile (measured faster there).
+        v4i acc[TMX][CTX];
+        auto products = [&](int j) {
+          const uint4 wp = wr[j][d];
+          const v4i a0 = {cvt_lo16(wp.x), cvt_hi16(wp.x), cvt_lo16(wp.y), cvt_hi16(wp.y)};
+          const v4i a1 = {cvt_lo16(wp.z), cvt_hi16(wp.z), cvt_lo16(wp.w), cvt_hi16(wp.w)};
 #pragma unroll
-        for (int j = 0; j < TMX; ++j) {
-          if (j < nt) {
-            const uint4 wp = wr[j][d];
-            const v4i a0 = {cvt_lo16(wp.x), cvt_hi16(wp.x), cvt_lo16(wp.y), cvt_hi16(wp.y)};
-            const v4i a1 = {cvt_lo16(wp.z), cvt_hi16(wp.z), cvt_lo16(wp.w), cvt_hi16(wp.w)};
-            // this group's scales of rows 4q .. 4q+3 (row rr's 16 bytes hold
-            // the block's 8 uint16 scales)
-            const uint8_t *scl = sb + 16 * P.CT * kXRow + 256 * j;
-            int32_t m[4];
+          for (int ct = 0; ct < CTX; ++ct) {
+            if (ct < P.CT) {
+              acc[j][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bx[ct][0], v4i{0, 0, 0, 0}, 0,
+                                                                 0, 0);
+              acc[j][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bx[ct][1], acc[j][ct], 0, 0, 0);
+            }
+          }
+        };
+        auto scales = [&](int j) {
+          // this group's scales of rows 4q .. 4q+3 (row rr's 16 bytes hold
+          // the block's 8 uint16 scales)
+          const uint8_t *scl = sb + 16 * P.CT * kXRow + 256 * j;
+          Acc m[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              m[e] = *(const uint16_t *)(scl + (4 * q + e) * 16 + 2 * w);
+          for (int e = 0; e < 4; ++e)
+            m[e] = mm_scale<CTX>(*(const uint16_t *)(scl + (4 * q + e) * 16 + 2 * w));
 #pragma unroll
-            for (int ct = 0; ct < CTX; ++ct) {
-              if (ct < P.CT) {
-                v4i acc = {0, 0, 0, 0};
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bx[ct][0], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bx[ct][1], acc, 0, 0, 0);
+          for (int ct = 0; ct < CTX; ++ct) {
+            if (ct < P.CT) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) p[j][ct][e] += (int64_t)m[e] * (int64_t)acc[e];
-              }
+              for (int e = 0; e < 4; ++e) p[j][ct][e] = mm_fma(m[e], acc[j][ct][e], p[j][ct][e]);
+            }
+          }
+        };
+        if constexpr (CTX >= 2) {
+#pragma unroll
+          for (int j = 0; j < TMX; ++j)
+            if (j < nt) products(j);
+#pragma unroll
+          for (int j = 0; j < TMX; ++j)
+            if (j < nt) scales(j);
+        } else {
+#pragma unroll
+          for (int j = 0; j < TMX; ++j) {
+            if (j < nt) {
+              products(j);
+              scales(j);
             }
           }
         }
@@ -569,7 +616,7 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
         if (cur.kb == cur.nblk - 1) {
           // end of round RHO: add this wavefront's sums into its table
           const int tb = cur.RHO & 1;
-          int64_t *tbl = tables + tb * (TMX * CTX * 4 * 64);
+          Acc *tbl = tables + tb * (TMX * CTX * 4 * 64);
           mm_wait_word<true>(F, &F.tgen[tb], cur.RHO, lane);
 #pragma unroll
           for (int jj = 0; jj < TMX; ++jj)
@@ -578,7 +625,7 @@ __global__ __launch_bounds__(kMThreads) void matmul_kernel(MmParams P) {
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
                 if (jj < nt && ct < P.CT)
-                  mm_lds_add_u64(&tbl[((jj * CTX + ct) * 4 + e) * 64 + lane], p[jj][ct][e]);
+                  mm_lds_add(&tbl[((jj * CTX + ct) * 4 + e) * 64 + lane], p[jj][ct][e]);
                 p[jj][ct][e] = 0;
               }
           // the count follows the adds in this wavefront's LDS order, so the
