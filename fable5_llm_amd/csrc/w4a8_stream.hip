@@ -112,6 +112,17 @@ __device__ __forceinline__ void *uniform_ptr(const void *p) {
   return (void *)(uintptr_t)(((uint64_t)hi << 32) | lo);
 }
 
+// This lane's index, computed afresh where it is needed (v_mbcnt, in an asm
+// statement the compiler can neither hoist nor merge), so that no register
+// holds the thread index across the roles' loops: held, it was spilled to
+// scratch in the dependent-site instances, and the reload sat in the weight
+// loop.
+__device__ __forceinline__ int lane_now() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 // ---------------------------------------------------------------------------
 // LDS synchronisation
 // ---------------------------------------------------------------------------
@@ -705,6 +716,7 @@ __device__ __forceinline__ int group_prologue(CSite &P, Lds &L, int8_t *out, boo
     const double dscale = s1 >= 0 ? __builtin_ldexp(1.0, -min(s1, 63))
                                   : __builtin_ldexp(1.0, min(-s1, 63));
     const double dhalf = s1 > 0 ? 0.5 : 0.0;
+    const double drs = dr * dscale;   // exact: a power-of-2 scaling
 #pragma unroll
     for (int c = 0; c < kPN; ++c) {
       const int base = (c * kPW + pw) * kChunk + lane * 8;
@@ -713,9 +725,9 @@ __device__ __forceinline__ int group_prologue(CSite &P, Lds &L, int8_t *out, boo
         for (int j = 0; j < 8; ++j) {
           const int32_t xv = piece_get(X.pc[c], j);
           const int32_t sc = (int32_t)piece_get(X.wv[c], j) + one;
-          const double m = __builtin_fabs((double)xv) * dr;
-          const double y = __builtin_fmin(__builtin_floor(__builtin_fma(m, dscale, dhalf)),
-                                          4294967295.0);
+          // |x| * r * 2^-s, rounded once, as fma(m, 2^-s, 1/2) of the exact m
+          const double y = __builtin_fmin(
+              __builtin_floor(__builtin_fma(__builtin_fabs((double)xv), drs, dhalf)), 4294967295.0);
           const double w14 = (double)abs(sc) * 0x1p-14;
           const double qd = __builtin_fmin(__builtin_floor(__builtin_fma(y, w14, 0.5)), 65535.0);
           const bool neg = (xv < 0) != (sc < 0);
@@ -826,7 +838,11 @@ __device__ __forceinline__ void load_staged(const int8_t *stg, int8_t *xb, int K
 }
 
 // the wavefront waits until all prologue wavefronts have written site s's
-// activations into buffer b (bounded, like lds_wait_eq)
+// activations into buffer b (bounded, like lds_wait_eq).  Polled at a long
+// interval (about 1,000 cycles): eight weight wavefronts waiting here share
+// their SIMDs with the prologue wavefronts that compute the activations, and
+// polling every 64 cycles slowed those (the chained step by 4 %, the
+// independent one by 2 %); 2,000 cycles was slower again on the chained step.
 __device__ __forceinline__ void wait_ready(Lds &L, int b, int s, int lane, uint32_t lspin) {
   for (uint32_t n = 0;; ++n) {
     if (__all(lds_read_i32(&L.ready[b][lane % kPW]) == s)) break;
@@ -838,7 +854,7 @@ __device__ __forceinline__ void wait_ready(Lds &L, int b, int s, int lane, uint3
       }
       break;
     }
-    __builtin_amdgcn_s_sleep(1);
+    __builtin_amdgcn_s_sleep(16);
   }
   wait_lds();
 }
@@ -902,7 +918,7 @@ __device__ __forceinline__ void prologue_role(const GemvParams *sites_arg, int n
   wave = __builtin_amdgcn_readfirstlane(wave);
   epoch = __builtin_amdgcn_readfirstlane(epoch);
   const uint32_t fbase = (epoch - 1u) * (uint32_t)(nsites + 1);
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int lane = lane_now();
   // Every site's prologue is computed once, by CU s % G, into the site's
   // staging area (a site behind no fence at once, a fenced one after its
   // grid-wide wait); every CU then copies the staged sites, in order, into
@@ -921,11 +937,9 @@ __device__ __forceinline__ void prologue_role(const GemvParams *sites_arg, int n
       ps = compute_publish<kDep>(sites[s], L, stage + (size_t)s * kStageBytes, sflag + s, epoch,
                            pw, lane, ps, lspin);
   for (int s = 0; s < nsites; ++s) {
-    // lane-derived addresses are recomputed per site from an opaque copy
-    // of the thread index, so the compiler does not keep them live
-    int tid_s = tid;
-    asm volatile("" : "+v"(tid_s));
-    const int lane = tid_s & 63;
+    // lane-derived addresses are recomputed per site, so the compiler does
+    // not keep them live
+    const int lane = lane_now();
     CSite &P = sites[s];
     const int8_t *stg = stage + (size_t)s * kStageBytes;
     const int b = s % kNB;
@@ -999,7 +1013,7 @@ __device__ __forceinline__ void prologue_role(const GemvParams *sites_arg, int n
     }
     s = e - 1;
   }
-  if (!(ok && ps.ok) && lane == 0) lds_or_i32(&L.err, 4);
+  if (!(ok && ps.ok) && lane_now() == 0) lds_or_i32(&L.err, 4);
 }
 
 // The TOPK-32 head's scan, by prologue wavefront 0 of workgroup r once the
@@ -1103,11 +1117,9 @@ __device__ __forceinline__ void weight_role(const GemvParams *sites_arg, int nsi
   // refill R with the item two ahead, and add into the tile after this
   // wavefront's last block of it
   auto step = [&](BlockRegs &R, Cursor &c, const Cursor &nx) {
-    // the lane-derived addresses are recomputed from an opaque copy of the
-    // thread index, so the compiler does not keep them all live
-    int tid_s = tid;
-    asm volatile("" : "+v"(tid_s));
-    const int lane_s = tid_s & 63;
+    // the lane-derived addresses are recomputed per step, so the compiler
+    // does not keep them all live
+    const int lane_s = lane_now();
     if (c.s != s_cur) {
       // done with every earlier site; wait for this one's activations
       s_cur = c.s;
@@ -1231,9 +1243,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
     weight_role<kDep>(sites_arg, nsites, r, G, wave, lspin);
   }
 
-  int tid_e = tid;
-  asm volatile("" : "+v"(tid_e));
-  const int lane_e = tid_e & 63;
+  const int lane_e = lane_now();
   lds_barrier();
   if (wave == kCtrl && lane_e == 0) {
     const int32_t e = lds_read_i32(&L.err);
