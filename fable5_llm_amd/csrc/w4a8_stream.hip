@@ -1144,17 +1144,20 @@ __device__ __forceinline__ void weight_role(const GemvParams *sites_arg, int nsi
       }
       p = 0;
     };
-    // At this wavefront's last block of a site, its tile is finished before
-    // the refill: the refill's cursor reads table entries of sites further
-    // ahead, and a scalar-cache miss there would delay the site's completion
-    // -- which a fenced site after it waits for.  Elsewhere the refill goes
-    // first, to keep the weight stream full.
-    const bool site_end = kDep && nx.s != c.s;
-    if (last && site_end) finish_tile();
+    // In the instances for plans with waits, a tile is finished before the
+    // refill: the refill's cursor reads table entries of sites further
+    // ahead, and its nine loads queue behind the other wavefronts' refills,
+    // and both would delay the tile's completion -- which a site waiting
+    // for this one's outputs needs (chained step 1.418 -> 1.401 ms, the FFN
+    // blocks in layer order 0.682 -> 0.650 ms; with each down projection
+    // after the next gate / up, where nothing waits, 0.498 -> 0.512 ms).
+    // Otherwise the refill goes first, to keep the weight stream full.
+    const bool finish_first = kDep;
+    if (last && finish_first) finish_tile();
     c = cn;
     cur_next(sites, nsites, r, G, cn);
     issue_block(R, sites, nsites, G, c, lane_s);
-    if (last && !site_end) finish_tile();
+    if (last && !finish_first) finish_tile();
   };
   for (;;) {
     if (ca.s >= nsites) break;
