@@ -533,6 +533,10 @@ def chained_leg(ctx, stream, args):
                                "kernel": "stream_kernel",
                                "avg_launch_us": round(tm["kernel_ms"] * 1e3, 3)}
             out["end_hash"] = st.digest()
+            # per site class, from workgroup 0's stamps (as for the headline)
+            import numpy as np
+            prof = np.median(np.array([st.profile() for _ in range(5)]), axis=0)
+            leg["per_class"] = per_class(st, prof)
         else:
             leg["end_hash_equal"] = st.digest() == out["end_hash"]
         out[name] = leg
@@ -593,6 +597,7 @@ def c0_leg(ctx, stream, args, copies=64):
                            "includes the launch gaps, kernel_us_* are the launches alone")
         else:
             leg["note"] = "all copies in one stream_kernel launch (no site waits)"
+            leg["site_trace_us"] = site_trace(plan)
         out[name] = leg
     ctx.sync()
     keep = (x.cpu().numpy(), [np.frombuffer(w.download(), dtype=np.uint8) for w in ws[:8]],
@@ -601,6 +606,23 @@ def c0_leg(ctx, stream, args, copies=64):
     for w in ws:
         w.free()
     return out, keep
+
+
+def site_trace(plan, reps=5):
+    """A persistent plan's per-site times from workgroup 0's wall-clock
+    stamps (w4a8_plan_profile: the control wavefront stamps each site as it
+    starts storing it; the intervals are scaled to the launch's event time),
+    medians over `reps` launches: the first site's (launch start-up
+    included), the last one's (the launch's tail) and the spread of the
+    others."""
+    import numpy as np
+    us = np.median(np.array([plan.profile() for _ in range(reps)]), axis=0) * 1e3
+    mid = us[1:-1]
+    return {"first": round(float(us[0]), 3), "last": round(float(us[-1]), 3),
+            "others_p10_p50_p90": [round(float(np.percentile(mid, q)), 3) for q in (10, 50, 90)],
+            "sum": round(float(us.sum()), 2),
+            "basis": "workgroup 0's per-site wall-clock stamps, scaled to the launch's event "
+                     "time; medians over %d launches" % reps}
 
 
 def c0_check(keep):
