@@ -53,6 +53,8 @@ constexpr int kPW = 3;                      // prologue wavefronts
 constexpr int kPW0 = kCW + 1;               // ... 9..11
 constexpr int kThreads = (kPW0 + kPW) * 64; // 768
 constexpr int kNB = 8;                      // activation buffers (a power of 2)
+constexpr int kExpX8 = 1;                   // a prologue's exports: x8 and e_x ...
+constexpr int kExpXn = 2;                   // ... the RMSNorm output
 constexpr int kXloOff = kKMax;              // int32 corrections after x8
 constexpr int kXB = kKMax + kKMax / 8;      // x8 + corrections of one site
 constexpr int kTSlots = 32;                 // tiles being reduced at once
@@ -87,6 +89,7 @@ struct __align__(16) Lds {
   int32_t wsite[kCW];               // site each weight wavefront works on (nsites: done)
   int32_t gridok;                   // last fenced site whose grid-wide wait has passed
   int32_t served;                   // last site whose outputs the control wavefront stored
+  int32_t xdone;                    // last site whose x8 / e_x the control wavefront exported
   int16_t pairv[kPairTiles][kTileRows];  // paired site: job 0's outputs of this CU's tiles
   int16_t prod[kTileRows];          // ... and one tile's EMUL32 products
   int32_t psync[kPW];               // prologue wavefronts' barrier phases
@@ -620,10 +623,11 @@ __device__ __forceinline__ uint32_t pack4(uint32_t a, uint32_t b) {
 
 // The prologue of site P by the 3 prologue wavefronts (pw = 0..2; ps is
 // their barrier) from the inputs in X: x8 and the offset corrections into
-// `out` (put_x8 / put_corr), and, when `exports`, the site's exports (x8, e_x, the RMSNorm
+// `out` (put_x8 / put_corr), and the site's exports named by `exports` (kExpX8: x8 and
+// e_x; kExpXn: the RMSNorm
 // output); returns e_x.  Chunks past K are skipped.
 template <bool kLds, bool kDep>
-__device__ __forceinline__ int group_prologue(CSite &P, Lds &L, int8_t *out, bool exports,
+__device__ __forceinline__ int group_prologue(CSite &P, Lds &L, int8_t *out, int exports,
                                               int pw, int lane, PSync &ps, ProX &X,
                                               uint32_t lspin) {
   const int K = P.K;
@@ -643,11 +647,11 @@ __device__ __forceinline__ int group_prologue(CSite &P, Lds &L, int8_t *out, boo
           put_x8<kLds>(out, off, (uint32_t)v.x, (uint32_t)v.y);
           put_x8<kLds>(out, off + 8, (uint32_t)v.z, (uint32_t)v.w);
           if ((lane & 1) == 0) put_corr<kLds>(out, off / 32, -8 * t);
-          if (exports && P.x8_out) *(int4 *)(P.x8_out + off) = v;
+          if ((exports & kExpX8) && P.x8_out) *(int4 *)(P.x8_out + off) = v;
         }
       }
     }
-    if (exports && P.e_x_out && pw == 0 && lane == 0) *P.e_x_out = P.e_x_given;
+    if ((exports & kExpX8) && P.e_x_out && pw == 0 && lane == 0) *P.e_x_out = P.e_x_given;
     return P.e_x_given;
   }
   if (kDep && P.pro == PRO_EMUL_DYNQ8) {
@@ -734,7 +738,7 @@ __device__ __forceinline__ int group_prologue(CSite &P, Lds &L, int8_t *out, boo
           const int32_t qm = min((int32_t)qd, 32767 + (int32_t)neg);
           piece_set(X.pc[c], j, (int16_t)(neg ? -qm : qm));
         }
-        if (exports && P.xn_out && base < K) *(int4 *)(P.xn_out + base) = X.pc[c];
+        if ((exports & kExpXn) && P.xn_out && base < K) *(int4 *)(P.xn_out + base) = X.pc[c];
       }
     }
   }
@@ -774,11 +778,11 @@ __device__ __forceinline__ int group_prologue(CSite &P, Lds &L, int8_t *out, boo
       if (base < K) {
         put_x8<kLds>(out, base, lo, hi);
         if ((lane & 3) == 0) put_corr<kLds>(out, base / 32, -8 * t4);
-        if (exports && P.x8_out) *(uint2 *)(P.x8_out + base) = make_uint2(lo, hi);
+        if ((exports & kExpX8) && P.x8_out) *(uint2 *)(P.x8_out + base) = make_uint2(lo, hi);
       }
     }
   }
-  if (exports && P.e_x_out && pw == 0 && lane == 0) *P.e_x_out = e;
+  if ((exports & kExpX8) && P.e_x_out && pw == 0 && lane == 0) *P.e_x_out = e;
   return e;
 }
 
@@ -789,12 +793,28 @@ __device__ PSync compute_publish(CSite &P, Lds &L, int8_t *stg, uint32_t *flag, 
                                  int pw, int lane, PSync ps, uint32_t lspin) {
   ProX X;
   pro_issue<kDep>(X, P, pw, lane);
-  const int e = group_prologue<false, kDep>(P, L, stg, true, pw, lane, ps, X, lspin);
+  const int e = group_prologue<false, kDep>(P, L, stg, kExpX8 | kExpXn, pw, lane, ps, X, lspin);
   if (pw == 0 && lane == 0) store_coherent((int32_t *)(stg + kXB), (int32_t)e);
   wait_vm_all();
   psync(L, ps, pw, lane, lspin);
   if (pw == 0 && lane == 0) store_coherent(flag, epoch);
   return ps;
+}
+
+// A site whose prologue every CU computes itself (local) has its x8 and e_x
+// exported by CU s % G's control wavefront, from the site's LDS buffer, and
+// not by its prologue wavefronts: their stores would count in the same
+// in-order counter as their polls for the next site's input, which then
+// waited for the stores to complete, and that CU became the slowest at
+// every site (chained step 1.402 -> 1.371 ms).  The buffer is not reused
+// before the export is done (L.xdone).
+__device__ __forceinline__ bool ctrl_exports(CSite &P, int s, int r, int G) {
+  return P.local_pro && s % G == r && (P.x8_out != nullptr || P.e_x_out != nullptr);
+}
+template <bool kDep>
+__device__ __forceinline__ void wait_exported(CSite *sites, Lds &L, int t, int r, int G, int lane,
+                                              uint32_t lspin, bool &ok) {
+  if (kDep && t >= 0 && ctrl_exports(sites[t], t, r, G)) ok = lds_wait_ge(&L.xdone, t, lspin) && ok;
 }
 
 // The wavefront waits until the first `need` of sites s .. s + n - 1 (flags
@@ -950,6 +970,7 @@ __device__ __forceinline__ void prologue_role(const GemvParams *sites_arg, int n
       // grid-wide wait, instead of a staged copy that would first have to
       // be computed, published and flagged by one CU
       if (s >= kNB) ok = wait_weights_past(L, s - kNB, lane, lspin) && ok;
+      wait_exported<kDep>(sites, L, s - kNB, r, G, lane, lspin, ok);
       ok = lds_wait_ge(&L.gridok, P.fence_at, lspin) && ok;
       ProX X;
       if (P.stamp_src >= 0) {
@@ -962,7 +983,8 @@ __device__ __forceinline__ void prologue_role(const GemvParams *sites_arg, int n
       } else {
         pro_issue<kDep>(X, P, pw, lane);
       }
-      const int e = group_prologue<true, kDep>(P, L, L.x[b], s % G == r, pw, lane, ps, X, lspin);
+      const int e = group_prologue<true, kDep>(P, L, L.x[b], s % G == r ? kExpXn : 0, pw, lane,
+                                               ps, X, lspin);
       if (lane == 0) {
         if (pw == 0) lds_write_i32(&L.ex[b], e);
         lds_write_i32(&L.ready[b][pw], s);
@@ -992,6 +1014,7 @@ __device__ __forceinline__ void prologue_role(const GemvParams *sites_arg, int n
       }
     }
     if (e - 1 >= kNB) ok = wait_weights_past(L, e - 1 - kNB, lane, lspin) && ok;
+    for (int t = s; kDep && t < e; ++t) wait_exported<kDep>(sites, L, t - kNB, r, G, lane, lspin, ok);
     ok = wait_staged_n(sflag + s, e - s, e - s, epoch, lane, err, gspin) >= e - s && ok;
     for (int t = s; t < e; ++t)
       load_staged(stage + (size_t)t * kStageBytes, L.x[t % kNB], sites[t].K, pw, lane);
@@ -1203,6 +1226,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
   if (tid < kPW) L.psync[tid] = 0;
   if (tid == 0) {
     L.served = -1;
+    L.xdone = -1;
     L.gridok = 0;
     L.abort = 0;
     L.err = 0;
@@ -1223,6 +1247,18 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
         for (int a = s + 1; a < nsites && a <= s + 3; ++a) touch_site(&sites[a]);
       ctrl_serve<kDep>(P, L, kt0, r, G, lane, fbase + (uint32_t)s + 1u, lspin);
       if (kDep && lane == 0) lds_write_i32(&L.served, s);
+      if (kDep && ctrl_exports(P, s, r, G)) {
+        // x8 and e_x from the site's LDS buffer, after the post that lets
+        // this CU poll for the next site's input; once the site's prologue
+        // is done here (a CU with no tile of the site has not waited for it)
+        const int b = s % kNB;
+        wait_ready(L, b, s, lane, lspin);
+        if (P.x8_out)
+          for (int off = 16 * lane; off < P.K; off += 1024)
+            *(int4 *)(P.x8_out + off) = *(const int4 *)(L.x[b] + off);
+        if (P.e_x_out && lane == 0) *P.e_x_out = lds_read_i32(&L.ex[b]);
+        if (lane == 0) lds_write_i32(&L.xdone, s);
+      }
       {
         const int first = (r + P.tile_rot) % G;
         kt0 += first < P.total_tiles ? (P.total_tiles - 1 - first) / G + 1 : 0;
