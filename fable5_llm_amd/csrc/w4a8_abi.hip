@@ -1395,6 +1395,8 @@ static int plan_build_persistent(w4a8_plan *p) {
                                   std::to_string(i) + " has K=" +
                                   std::to_string(sites[i].K) + ")");
     sites[i].tile_rot = (int32_t)((V - off % V) % V);
+    sites[i].tiles_q = (int32_t)(sites[i].total_tiles / V);
+    sites[i].tiles_r = (int32_t)(sites[i].total_tiles % V);
     off += sites[i].total_tiles;
   }
   std::vector<StampSrc> src;

@@ -123,6 +123,7 @@ struct GemvParams {
   int64_t tile_bytes;
   int32_t tile0[kMaxJobs];  // job[j].tile0
   int32_t pro;
+  int32_t tiles_q, tiles_r; // persistent stream: total_tiles = tiles_q * G + tiles_r
   GemvJob job[kMaxJobs];
   const void *x;            // int8[K] or int16[K]
   const int16_t *norm_w;    // int16[K] Q14 (RMSNorm)
@@ -151,8 +152,8 @@ struct GemvParams {
   int32_t *err;             // bit 0: y32 overflow; bit 2: an LDS wait gave up
   uint64_t *partials;       // EPI_ARGMAX: one key per workgroup
   const int32_t *x2;        // PRO_EMUL_DYNQ8: int32[K]
-  int32_t pad_[2];          // (a whole number of 64-byte lines: in a site table, every
-                            // entry's first line is its own)
+  // (a whole number of 64-byte lines: in a site table, every entry's first
+  // line is its own)
 };
 static_assert(sizeof(GemvParams) % 64 == 0, "site table entries start on a line");
 

@@ -192,28 +192,82 @@ __device__ __forceinline__ void store_coherent(T *p, T v) {
 struct Cursor {
   int s;      // site; nsites once the sequence is exhausted
   int j;      // block index among the site's blocks on this CU
+  int i, b;   // ... as tile and block: j = i * nblk + b (kept by additions: a
+              // division per block, in scalar code shared by the CU's
+              // wavefronts, cost a weight wavefront more time than its dot)
   int kt0;    // CU-local number of the site's first tile
   int nb;     // blocks of the site on this CU
   int ntl;    // tiles of the site on this CU
   int nblk;   // scale blocks per tile
   int first;  // first global tile of the site on this CU
+  int ng;     // scale groups per row (the site's NG)
+  int tbytes; // bytes per tile
+  int job;    // the job of tile i (a site's jobs are runs of tiles, and t only grows)
+  int jend;   // ... the first tile past it
+  uint64_t jbase;   // ... and its weights' address less its first tile's offset
 };
+
+// Workgroup r's first tile of site P and its number of tiles there, without
+// a division (r and tile_rot lie in [0, G))
+__device__ __forceinline__ int site_first(CSite &P, int r, int G) {
+  const int f = r + P.tile_rot;
+  return f >= G ? f - G : f;
+}
+__device__ __forceinline__ int site_ntl(CSite &P, int first) {
+  return P.tiles_q + (first < P.tiles_r ? 1 : 0);
+}
+// s % G for a site number (a plan has few more sites than workgroups)
+__device__ __forceinline__ int site_owner(int s, int G) {
+  while (s >= G) s -= G;
+  return s;
+}
 
 __device__ __forceinline__ void cur_load_site(CSite *sites, int r, int G, Cursor &c) {
   CSite &P = sites[c.s];
-  c.first = (r + P.tile_rot) % G;
-  c.ntl = c.first < P.total_tiles ? (P.total_tiles - 1 - c.first) / G + 1 : 0;
+  c.first = site_first(P, r, G);
+  c.ntl = site_ntl(P, c.first);
   c.nblk = P.nblk;
   c.nb = c.ntl * c.nblk;
+  c.ng = P.NG;
+  c.tbytes = (int)P.tile_bytes;
+}
+
+// The job of tile i (global tile first + i * G), found from the cursor's
+// job on (from job 0 when `fresh`): the table is read only when the tile
+// leaves the job, so the weight loop's block addresses take no table reads.
+__device__ __forceinline__ void cur_job(CSite *sites, int G, Cursor &c, bool fresh) {
+  CSite &P = sites[c.s];
+  const int t = c.first + c.i * G;
+  if (!fresh && t < c.jend) return;
+  int j = fresh ? 0 : c.job;
+  while (j + 1 < P.njobs && t >= P.tile0[j + 1]) ++j;
+  c.job = j;
+  c.jend = j + 1 < P.njobs ? P.tile0[j + 1] : 0x7fffffff;
+  CJob &J = P.job[j];
+  c.jbase = (uint64_t)(uintptr_t)J.w - (uint64_t)(int64_t)J.tile0 * (uint64_t)(int64_t)c.tbytes;
+}
+
+// (i, b) of block j, from i = 0 (j is below a few nblk here)
+__device__ __forceinline__ void cur_split(Cursor &c) {
+  c.i = 0;
+  c.b = c.j;
+  while (c.b >= c.nblk && c.nblk > 0) {
+    c.b -= c.nblk;
+    ++c.i;
+  }
 }
 
 // move forward until block j lies in site s (or past the last site)
 __device__ __forceinline__ void cur_settle(CSite *sites, int nsites, int r, int G, Cursor &c) {
-  while (c.s < nsites && c.j >= c.nb) {
-    c.j -= c.nb;
-    c.kt0 += c.ntl;
-    ++c.s;
-    if (c.s < nsites) cur_load_site(sites, r, G, c);
+  if (c.s < nsites && c.j >= c.nb) {
+    while (c.s < nsites && c.j >= c.nb) {
+      c.j -= c.nb;
+      c.kt0 += c.ntl;
+      ++c.s;
+      if (c.s < nsites) cur_load_site(sites, r, G, c);
+    }
+    cur_split(c);
+    if (c.s < nsites) cur_job(sites, G, c, true);
   }
 }
 
@@ -222,14 +276,23 @@ __device__ __forceinline__ void cur_init(CSite *sites, int nsites, int r, int G,
   c.s = 0;
   c.j = j0;
   c.kt0 = 0;
-  c.nb = c.ntl = c.nblk = c.first = 0;
+  c.nb = c.ntl = c.nblk = c.first = c.ng = c.tbytes = c.job = c.jend = 0;
+  c.jbase = 0;
   if (nsites > 0) cur_load_site(sites, r, G, c);
+  cur_split(c);
+  if (nsites > 0 && c.j < c.nb) cur_job(sites, G, c, true);
   cur_settle(sites, nsites, r, G, c);
 }
 
 __device__ __forceinline__ void cur_next(CSite *sites, int nsites, int r, int G, Cursor &c) {
   c.j += kCW;
-  cur_settle(sites, nsites, r, G, c);
+  c.b += kCW;
+  while (c.b >= c.nblk && c.nblk > 0) {
+    c.b -= c.nblk;
+    ++c.i;
+  }
+  if (c.s < nsites && c.j >= c.nb) cur_settle(sites, nsites, r, G, c);
+  else if (c.s < nsites) cur_job(sites, G, c, false);
 }
 
 // Put block c in flight into R: always the same 1 + kGroupsPerBlock buffer
@@ -242,12 +305,10 @@ __device__ __forceinline__ void issue_block(BlockRegs &R, CSite *sites, int nsit
   const uint8_t *bb = (const uint8_t *)sites[0].tables;   // any mapped address: range 0
   int len = 0;
   if (c.s < nsites) {
-    CSite &P = sites[c.s];
-    const int i = c.j / c.nblk, b = c.j - i * c.nblk;
-    const int t = c.first + i * G;
-    CJob &J = P.job[job_of(P, t)];
-    bb = J.w + (int64_t)(t - J.tile0) * P.tile_bytes + (int64_t)b * kBlockBytes;
-    len = kScaleChunk + groups_in(P.NG, b) * kGroupChunk;
+    const uint32_t t = (uint32_t)(c.first + c.i * G);
+    bb = (const uint8_t *)(uintptr_t)(c.jbase + (uint64_t)t * (uint32_t)c.tbytes +
+                                      (uint64_t)(uint32_t)(c.b * kBlockBytes));
+    len = kScaleChunk + groups_in(c.ng, c.b) * kGroupChunk;
   }
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc((void *)bb, (short)0, len, kBufDword3);
@@ -352,7 +413,7 @@ __device__ __noinline__ void serve_residual(Lds &L, CJob &J, int slot, int t, in
 template <bool kDep>
 __device__ void ctrl_serve(CSite &P, Lds &L, int kt0, int r, int G, int lane, uint32_t stamp,
                            uint32_t lspin) {
-  const int first = (r + P.tile_rot) % G;
+  const int first = site_first(P, r, G);
   for (int i = 0, t = first; t < P.total_tiles; ++i, t += G) {
     CJob &J = P.job[job_of(P, t)];
     const int kt = kt0 + i, slot = kt & (kTSlots - 1);
@@ -395,7 +456,7 @@ __device__ void ctrl_serve(CSite &P, Lds &L, int kt0, int r, int G, int lane, ui
         // a paired site: this CU's tiles of job 0 come first (npair of
         // them), then the same tiles of job 1; ALU EMUL32 at p0 = 12
         // (gen_layer_script.py:1414-1418) of the two, as job 1's are stored
-        const int npair = P.total_tiles / 2 / G;
+        const int npair = P.tiles_q >> 1;   // total_tiles = 2 * npair * G
         if (i < npair) {
           L.pairv[i][lane] = (int16_t)v;
         } else {
@@ -404,7 +465,7 @@ __device__ void ctrl_serve(CSite &P, Lds &L, int kt0, int r, int G, int lane, ui
         }
       }
     }
-    if (kDep && P.prod_stamped && i >= P.total_tiles / 2 / G && lane < kTileRows / 2) {
+    if (kDep && P.prod_stamped && i >= (P.tiles_q >> 1) && lane < kTileRows / 2) {
       wait_lds();
       const int row = (t - J.tile0) * kTileRows + 2 * lane;
       const uint32_t lo = (uint32_t)(uint16_t)L.prod[2 * lane];
@@ -809,7 +870,7 @@ __device__ PSync compute_publish(CSite &P, Lds &L, int8_t *stg, uint32_t *flag, 
 // every site (chained step 1.402 -> 1.371 ms).  The buffer is not reused
 // before the export is done (L.xdone).
 __device__ __forceinline__ bool ctrl_exports(CSite &P, int s, int r, int G) {
-  return P.local_pro && s % G == r && (P.x8_out != nullptr || P.e_x_out != nullptr);
+  return P.local_pro && site_owner(s, G) == r && (P.x8_out != nullptr || P.e_x_out != nullptr);
 }
 template <bool kDep>
 __device__ __forceinline__ void wait_exported(CSite *sites, Lds &L, int t, int r, int G, int lane,
@@ -827,7 +888,7 @@ constexpr int kStageBlocks = 2 * kCW;   // ... with this many weight blocks per 
 static_assert(kStageBatch < kNB, "a batch's buffers are free together");
 // a site's weight blocks on one CU, at most
 __device__ __forceinline__ int site_blocks(CSite &P, int G) {
-  return (P.total_tiles + G - 1) / G * P.nblk;
+  return (P.tiles_q + (P.tiles_r > 0 ? 1 : 0)) * P.nblk;
 }
 __device__ __forceinline__ int wait_staged_n(const uint32_t *flag, int n, int need,
                                              uint32_t epoch, int lane, int32_t *err,
@@ -983,7 +1044,7 @@ __device__ __forceinline__ void prologue_role(const GemvParams *sites_arg, int n
       } else {
         pro_issue<kDep>(X, P, pw, lane);
       }
-      const int e = group_prologue<true, kDep>(P, L, L.x[b], s % G == r ? kExpXn : 0, pw, lane,
+      const int e = group_prologue<true, kDep>(P, L, L.x[b], site_owner(s, G) == r ? kExpXn : 0, pw, lane,
                                                ps, X, lspin);
       if (lane == 0) {
         if (pw == 0) lds_write_i32(&L.ex[b], e);
@@ -991,7 +1052,7 @@ __device__ __forceinline__ void prologue_role(const GemvParams *sites_arg, int n
       }
       continue;
     }
-    if (s % G == r && P.fence_at > 0) {
+    if (site_owner(s, G) == r && P.fence_at > 0) {
       ok = lds_wait_ge(&L.gridok, P.fence_at, lspin) && ok;
       ps = compute_publish<kDep>(P, L, stage + (size_t)s * kStageBytes, sflag + s, epoch, pw,
                            lane, ps, lspin);
@@ -1149,20 +1210,20 @@ __device__ __forceinline__ void weight_role(const GemvParams *sites_arg, int nsi
       lds_write_i32(&L.wsite[wave], s_cur);
       wait_ready(L, s_cur % kNB, s_cur, lane_s, lspin);
       e_x = __builtin_amdgcn_readfirstlane(lds_read_i32(&L.ex[s_cur % kNB]));
-      contributors = min(sites[s_cur].nblk, kCW);
+      contributors = min(c.nblk, kCW);
     }
     CSite &P = sites[c.s];
-    const int i = c.j / c.nblk, b = c.j - i * c.nblk;
+    const int i = c.i, b = c.b;
     const int8_t *xb = L.x[c.s % kNB];
-    p = dot_block(R, groups_in(P.NG, b), b * kGroupsPerBlock, lane_s & 3, xb,
+    p = dot_block(R, groups_in(c.ng, b), b * kGroupsPerBlock, lane_s & 3, xb,
                   (const int32_t *)(xb + kXloOff), p);
-    const bool last = !(nx.s == c.s && nx.j / nx.nblk == i);
+    const bool last = !(nx.s == c.s && nx.i == i);
     const Cursor done = c;
     auto finish_tile = [&]() {
       const int kt = done.kt0 + i;
       if (tile_add(L, kt, p, contributors, lspin, lane_s)) {
         const int t = done.first + i * G;
-        CJob &J = P.job[job_of(P, t)];
+        CJob &J = P.job[done.job];
         tile_epilogue(L, kt, J, t - J.tile0, e_x, lane_s);
       }
       p = 0;
@@ -1259,10 +1320,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
         if (P.e_x_out && lane == 0) *P.e_x_out = lds_read_i32(&L.ex[b]);
         if (lane == 0) lds_write_i32(&L.xdone, s);
       }
-      {
-        const int first = (r + P.tile_rot) % G;
-        kt0 += first < P.total_tiles ? (P.total_tiles - 1 - first) / G + 1 : 0;
-      }
+      kt0 += site_ntl(P, site_first(P, r, G));
       if (s + 1 < nsites && sites[s + 1].fence) {
         const uint32_t v = fbase + (uint32_t)(s + 1);
         wait_vm_all();   // this workgroup's outputs of sites <= s are stored
