@@ -205,6 +205,10 @@ struct Cursor {
   int job;    // the job of tile i (a site's jobs are runs of tiles, and t only grows)
   int jend;   // ... the first tile past it
   uint64_t jbase;   // ... and its weights' address less its first tile's offset
+  int jtile0, jrows;   // ... its first tile and rows
+  int jepi;   // ... and its epilogue: epi | sh << 8 | p0 << 16 (kept here, so a
+              // tile's epilogue reads no table entry, which may have left the
+              // scalar cache since the tile's first block)
 };
 
 // Workgroup r's first tile of site P and its number of tiles there, without
@@ -245,6 +249,9 @@ __device__ __forceinline__ void cur_job(CSite *sites, int G, Cursor &c, bool fre
   c.jend = j + 1 < P.njobs ? P.tile0[j + 1] : 0x7fffffff;
   CJob &J = P.job[j];
   c.jbase = (uint64_t)(uintptr_t)J.w - (uint64_t)(int64_t)J.tile0 * (uint64_t)(int64_t)c.tbytes;
+  c.jtile0 = J.tile0;
+  c.jrows = J.nrows;
+  c.jepi = (J.epi & 0xFF) | ((J.sh & 0xFF) << 8) | (int)((uint32_t)J.p0 << 16);
 }
 
 // (i, b) of block j, from i = 0 (j is below a few nblk here)
@@ -277,6 +284,7 @@ __device__ __forceinline__ void cur_init(CSite *sites, int nsites, int r, int G,
   c.j = j0;
   c.kt0 = 0;
   c.nb = c.ntl = c.nblk = c.first = c.ng = c.tbytes = c.job = c.jend = 0;
+  c.jtile0 = c.jrows = c.jepi = 0;
   c.jbase = 0;
   if (nsites > 0) cur_load_site(sites, r, G, c);
   cur_split(c);
@@ -342,19 +350,21 @@ __device__ __forceinline__ bool tile_add(Lds &L, int kt, int64_t p, int contribu
 // rows of tile kt (tile tl of job J).  Argmax tiles fold their rows into the
 // workgroup's key in LDS and free the slot; the others are staged for the
 // control wavefront.
-__device__ __forceinline__ void tile_epilogue(Lds &L, int kt, CJob &J, int tl, int e_x,
-                                              int lane) {
+// (the job's epi, sh and p0 packed as in Cursor::jepi, and its rows)
+__device__ __forceinline__ void tile_epilogue(Lds &L, int kt, int jepi, int nrows, int tl,
+                                              int e_x, int lane) {
   const int slot = kt & (kTSlots - 1);
-  const bool argmax = J.epi == EPI_ARGMAX;
+  const int epi = jepi & 0xFF, sh = (jepi >> 8) & 0xFF, p0 = jepi >> 16;
+  const bool argmax = epi == EPI_ARGMAX;
   if (lane < kTileRows) {
     const int64_t tot = L.tv[slot][lane];
     const int row = tl * kTileRows + lane;
     int64_t outv = 0;
-    if (row < J.nrows) {
-      const int64_t y = rshr64(tot >> 4, J.sh);   // tot is 16 * p exactly
+    if (row < nrows) {
+      const int64_t y = rshr64(tot >> 4, sh);   // tot is 16 * p exactly
       if (y > 2147483647LL || y < -2147483647LL) lds_or_i32(&L.err, 1);
-      const int shift = J.p0 - e_x;
-      switch (J.epi) {
+      const int shift = p0 - e_x;
+      switch (epi) {
         case EPI_Y32: outv = y; break;
         case EPI_MOVY_I16: outv = clamp64(movy_shift(y, shift), -32768, 32767); break;
         case EPI_MOVY_P32:
@@ -414,41 +424,59 @@ template <bool kDep>
 __device__ void ctrl_serve(CSite &P, Lds &L, int kt0, int r, int G, int lane, uint32_t stamp,
                            uint32_t lspin) {
   const int first = site_first(P, r, G);
+  // the job of tile t, found from the last one on (t only grows), and the
+  // fields its tiles' stores need, read from the table only when the job
+  // changes: a table read on every tile put its latency before every store
+  int j = -1, jend = 0, epi = 0, jt0 = 0, nrows = 0;
+  void *out = nullptr;
+  uint64_t *stamped = nullptr;
+  bool add = false;
   for (int i = 0, t = first; t < P.total_tiles; ++i, t += G) {
-    CJob &J = P.job[job_of(P, t)];
+    if (t >= jend) {
+      if (j < 0) j = 0;
+      while (j + 1 < P.njobs && t >= P.tile0[j + 1]) ++j;
+      CJob &Jn = P.job[j];
+      jend = j + 1 < P.njobs ? P.tile0[j + 1] : 0x7fffffff;
+      epi = Jn.epi;
+      jt0 = Jn.tile0;
+      nrows = Jn.nrows;
+      out = Jn.out;
+      stamped = Jn.stamped;
+      // a residual-ADD job reaches this kernel as EPI_MOVY_I16 with res_out
+      add = Jn.res_out != nullptr;
+    }
+    CJob &J = P.job[j];
     const int kt = kt0 + i, slot = kt & (kTSlots - 1);
-    if (J.epi == EPI_ARGMAX) {
+    if (epi == EPI_ARGMAX) {
       // later argmax tiles may have reused and freed the slot since
       lds_wait_eq<true>(L, &L.tgen[slot], kt + kTSlots, lane, lspin);
       continue;
     }
     lds_wait_eq(L, &L.tready[slot], kt + 1, lane, lspin);
-    // a residual-ADD job reaches this kernel as EPI_MOVY_I16 with res_out
-    const bool add = J.res_out != nullptr;
     if (add) serve_residual(L, J, slot, t, lane);
-    if (kDep && J.stamped && lane < kTileRows / 2) {
+    if (kDep && stamped && lane < kTileRows / 2) {
       // rows 2l and 2l + 1 (int16 epilogues); nrows is even
-      const int row = (t - J.tile0) * kTileRows + 2 * lane;
+      const int row = (t - jt0) * kTileRows + 2 * lane;
       const uint32_t lo = (uint32_t)(uint16_t)(int16_t)L.tv[slot][2 * lane];
       const uint32_t hi = (uint32_t)(uint16_t)(int16_t)L.tv[slot][2 * lane + 1];
-      if (row < J.nrows)
-        store_coherent(J.stamped + row / 2, (uint64_t)(lo | (hi << 16)) | ((uint64_t)stamp << 32));
+      if (row < nrows)
+        store_coherent(stamped + row / 2, (uint64_t)(lo | (hi << 16)) | ((uint64_t)stamp << 32));
     }
     if (lane < kTileRows) {
       const int64_t v = L.tv[slot][lane];
-      const int row = (t - J.tile0) * kTileRows + lane;
-      if (row < J.nrows && !add) {
-        switch (J.epi) {
+      const int row = (t - jt0) * kTileRows + lane;
+      if (row < nrows && !add) {
+        switch (epi) {
           case EPI_MOVY_I16:
-          case EPI_SILU32: store_coherent((int16_t *)J.out + row, (int16_t)v); break;
-          case EPI_SHIFT_I64: store_coherent((int64_t *)J.out + row, v); break;
+          case EPI_SILU32: store_coherent((int16_t *)out + row, (int16_t)v); break;
+          case EPI_SHIFT_I64: store_coherent((int64_t *)out + row, v); break;
           case EPI_TOPK:
             // {y32, stamp}: an 8-byte store lands whole, so the scan, seeing
             // this launch's stamp, sees the value
-            store_coherent((uint64_t *)J.out + row,
+            store_coherent((uint64_t *)out + row,
                            (uint64_t)(uint32_t)(int32_t)v | ((uint64_t)stamp << 32));
             break;
-          default: store_coherent((int32_t *)J.out + row, (int32_t)v); break;
+          default: store_coherent((int32_t *)out + row, (int32_t)v); break;
         }
       }
       L.tv[slot][lane] = 0;
@@ -467,7 +495,7 @@ __device__ void ctrl_serve(CSite &P, Lds &L, int kt0, int r, int G, int lane, ui
     }
     if (kDep && P.prod_stamped && i >= (P.tiles_q >> 1) && lane < kTileRows / 2) {
       wait_lds();
-      const int row = (t - J.tile0) * kTileRows + 2 * lane;
+      const int row = (t - jt0) * kTileRows + 2 * lane;
       const uint32_t lo = (uint32_t)(uint16_t)L.prod[2 * lane];
       const uint32_t hi = (uint32_t)(uint16_t)L.prod[2 * lane + 1];
       store_coherent(P.prod_stamped + row / 2, (uint64_t)(lo | (hi << 16)) | ((uint64_t)stamp << 32));
@@ -1223,8 +1251,7 @@ __device__ __forceinline__ void weight_role(const GemvParams *sites_arg, int nsi
       const int kt = done.kt0 + i;
       if (tile_add(L, kt, p, contributors, lspin, lane_s)) {
         const int t = done.first + i * G;
-        CJob &J = P.job[done.job];
-        tile_epilogue(L, kt, J, t - J.tile0, e_x, lane_s);
+        tile_epilogue(L, kt, done.jepi, done.jrows, t - done.jtile0, e_x, lane_s);
       }
       p = 0;
     };
