@@ -622,10 +622,10 @@ __device__ __forceinline__ void pro_issue(ProX &X, CSite &P, int pw, int lane) {
 // word of the wavefront carries the stamp; then X.pc[c] holds the chunk's
 // 8 int16.  The RMSNorm weights are loaded first, as in pro_issue.
 // Bounded: false if the words never all arrived (err bit 1).
-__device__ __forceinline__ bool pro_issue_stamped(ProX &X, CSite &P, uint32_t stamp, int pw,
-                                                  int lane, int32_t *err, uint32_t gspin) {
-  const int K = P.K;
-  const int wlen = P.pro == PRO_RMSNORM_DYNQ8 ? 2 * K : 0;
+__device__ __forceinline__ bool pro_issue_stamped(ProX &X, CSite &P, int K, int pro,
+                                                  uint32_t stamp, int pw, int lane, int32_t *err,
+                                                  uint32_t gspin) {
+  const int wlen = pro == PRO_RMSNORM_DYNQ8 ? 2 * K : 0;
   const __amdgpu_buffer_rsrc_t rw =
       __builtin_amdgcn_make_buffer_rsrc((void *)P.norm_w, (short)0, wlen, kBufDword3);
 #pragma unroll
@@ -723,11 +723,10 @@ __device__ __forceinline__ uint32_t pack4(uint32_t a, uint32_t b) {
 // e_x; kExpXn: the RMSNorm
 // output); returns e_x.  Chunks past K are skipped.
 template <bool kLds, bool kDep>
-__device__ __forceinline__ int group_prologue(CSite &P, Lds &L, int8_t *out, int exports,
-                                              int pw, int lane, PSync &ps, ProX &X,
+__device__ __forceinline__ int group_prologue(CSite &P, int K, int pro, Lds &L, int8_t *out,
+                                              int exports, int pw, int lane, PSync &ps, ProX &X,
                                               uint32_t lspin) {
-  const int K = P.K;
-  if (P.pro == PRO_X8) {
+  if (pro == PRO_X8) {
 #pragma unroll
     for (int c = 0; c < kPX; ++c) {
       const int off = (c * kPW + pw) * 1024 + lane * 16;
@@ -750,7 +749,7 @@ __device__ __forceinline__ int group_prologue(CSite &P, Lds &L, int8_t *out, int
     if ((exports & kExpX8) && P.e_x_out && pw == 0 && lane == 0) *P.e_x_out = P.e_x_given;
     return P.e_x_given;
   }
-  if (kDep && P.pro == PRO_EMUL_DYNQ8) {
+  if (kDep && pro == PRO_EMUL_DYNQ8) {
     // ALU EMUL32 at p0 = 12 (gen_layer_script.py:1414-1418): clip16 of the
     // rounded product, then DYNQ8 below.  The second factor of the first
     // half of the chunks came with the inputs; the second half's is loaded
@@ -773,7 +772,7 @@ __device__ __forceinline__ int group_prologue(CSite &P, Lds &L, int8_t *out, int
       }
     }
   }
-  if (P.pro == PRO_RMSNORM_DYNQ8) {
+  if (pro == PRO_RMSNORM_DYNQ8) {
     // layer_fixed.py:1262-1278 in sign-magnitude form (rshift_round rounds
     // the magnitude); K <= kStreamNormKMax
     // sum of squares: a pair's a^2 + b^2 <= 2^31 is exact as a uint32
@@ -889,7 +888,8 @@ __device__ PSync compute_publish(CSite &P, Lds &L, int8_t *stg, uint32_t *flag, 
                                  int pw, int lane, PSync ps, uint32_t lspin) {
   ProX X;
   pro_issue<kDep>(X, P, pw, lane);
-  const int e = group_prologue<false, kDep>(P, L, stg, kExpX8 | kExpXn, pw, lane, ps, X, lspin);
+  const int e =
+      group_prologue<false, kDep>(P, P.K, P.pro, L, stg, kExpX8 | kExpXn, pw, lane, ps, X, lspin);
   if (pw == 0 && lane == 0) store_coherent((int32_t *)(stg + kXB), (int32_t)e);
   wait_vm_all();
   psync(L, ps, pw, lane, lspin);
@@ -1069,18 +1069,25 @@ __device__ __forceinline__ void prologue_role(const GemvParams *sites_arg, int n
       wait_exported<kDep>(sites, L, s - kNB, r, G, lane, lspin, ok);
       ok = lds_wait_ge(&L.gridok, P.fence_at, lspin) && ok;
       ProX X;
+      // the fields the prologue branches on, read before its waits
+      int pK = P.K, ppro = P.pro;
       if (P.stamp_src >= 0) {
         // no grid-wide wait: the input's own words say when it is whole.
         // Polled once this CU has stored its own share (a CU that polls
         // while others still stream would only add traffic).
         ok = lds_wait_ge(&L.served, P.stamp_src, lspin) && ok;
-        ok = pro_issue_stamped(X, P, fbase + (uint32_t)P.stamp_src + 1u, pw, lane, err, gspin) &&
+        ok = pro_issue_stamped(X, P, pK, ppro, fbase + (uint32_t)P.stamp_src + 1u, pw, lane, err,
+                               gspin) &&
              ok;
       } else {
         pro_issue<kDep>(X, P, pw, lane);
       }
-      const int e = group_prologue<true, kDep>(P, L, L.x[b], site_owner(s, G) == r ? kExpXn : 0, pw, lane,
-                                               ps, X, lspin);
+      // held in registers across the waits: read again after them, the
+      // fields' scalar loads could miss
+      asm volatile("" : "+s"(pK), "+s"(ppro));
+      const int e = group_prologue<true, kDep>(P, pK, ppro, L, L.x[b],
+                                               site_owner(s, G) == r ? kExpXn : 0, pw, lane, ps, X,
+                                               lspin);
       if (lane == 0) {
         if (pw == 0) lds_write_i32(&L.ex[b], e);
         lds_write_i32(&L.ready[b][pw], s);
