@@ -421,8 +421,8 @@ __device__ __noinline__ void serve_residual(Lds &L, CJob &J, int slot, int t, in
 // completes them, which is waited for here too, so that no wavefront still
 // reads this site's activations once this returns.
 template <bool kDep>
-__device__ void ctrl_serve(CSite &P, Lds &L, int kt0, int r, int G, int lane, uint32_t stamp,
-                           uint32_t lspin) {
+__device__ __forceinline__ void ctrl_serve(CSite &P, Lds &L, int kt0, int r, int G, int lane,
+                                           uint32_t stamp, uint32_t lspin) {
   const int first = site_first(P, r, G);
   // the job of tile t, found from the last one on (t only grows), and the
   // fields its tiles' stores need, read from the table only when the job
@@ -508,8 +508,8 @@ __device__ void ctrl_serve(CSite &P, Lds &L, int kt0, int r, int G, int lane, ui
 }
 
 // all G workgroups have stored flag value >= v (bounded; bit 1 of err)
-__device__ void grid_wait(uint32_t *flags, int G, uint32_t v, int lane, int32_t *err,
-                          uint32_t gspin) {
+__device__ __forceinline__ void grid_wait(uint32_t *flags, int G, uint32_t v, int lane,
+                                          int32_t *err, uint32_t gspin) {
   uint32_t n = 0;
   for (;;) {
     bool ok = true;
@@ -571,11 +571,17 @@ __device__ __forceinline__ int4 vec_load(__amdgpu_buffer_rsrc_t rs, int off) {
 // elements -- one (group, k-quarter) of the weight layout), the RMSNorm
 // weights and the int32 second factor of PRO_EMUL_DYNQ8 alike; for int8 x
 // (PRO_X8), 1 KiB chunks of 16 bytes per lane.
-struct ProX {
-  int4 pc[kPC];
+// NC chunks per wavefront: kPC for any K, or kPS for a site read through
+// stamped words with K <= kStampKSmall (see small_prologue).
+template <int NC>
+struct ProXN {
+  int4 pc[NC];
   int4 wv[kPN];
-  int4 x2[kPC];   // PRO_EMUL_DYNQ8: the second factor of half the chunks at a time
+  int4 x2[NC];   // PRO_EMUL_DYNQ8: the second factor of half the chunks at a time
 };
+typedef ProXN<kPC> ProX;
+constexpr int kPS = kPN;                        // chunks per wavefront for K <= ...
+constexpr int kStampKSmall = kPS * kPW * kChunk;   // ... 4608
 constexpr int kPC2 = kPC / 2;   // chunks per half of the second factor
 static_assert(kPC % 2 == 0, "the second factor is loaded in two halves");
 
@@ -622,7 +628,8 @@ __device__ __forceinline__ void pro_issue(ProX &X, CSite &P, int pw, int lane) {
 // word of the wavefront carries the stamp; then X.pc[c] holds the chunk's
 // 8 int16.  The RMSNorm weights are loaded first, as in pro_issue.
 // Bounded: false if the words never all arrived (err bit 1).
-__device__ __forceinline__ bool pro_issue_stamped(ProX &X, CSite &P, int K, int pro,
+template <int NC>
+__device__ __forceinline__ bool pro_issue_stamped(ProXN<NC> &X, CSite &P, int K, int pro,
                                                   uint32_t stamp, int pw, int lane, int32_t *err,
                                                   uint32_t gspin) {
   const int wlen = pro == PRO_RMSNORM_DYNQ8 ? 2 * K : 0;
@@ -639,7 +646,7 @@ __device__ __forceinline__ bool pro_issue_stamped(ProX &X, CSite &P, int K, int 
   for (uint32_t n = 0; n < gspin && !ok; ++n) {
     if (n > 0) __builtin_amdgcn_s_sleep(2);
 #pragma unroll
-    for (int c = 0; c < kPC; ++c) {
+    for (int c = 0; c < NC; ++c) {
       const int off = ((c * kPW + pw) * kChunk + lane * 8) * 4;
       X.pc[c] = vec_load(rx, off);
       X.x2[c] = vec_load(rx, off + 16);
@@ -650,7 +657,7 @@ __device__ __forceinline__ bool pro_issue_stamped(ProX &X, CSite &P, int K, int 
     // ms, FFN blocks in layer order 0.630 -> 0.623 ms)
     uint32_t bad = 0;
 #pragma unroll
-    for (int c = 0; c < kPC; ++c) {
+    for (int c = 0; c < NC; ++c) {
       const bool past = (c * kPW + pw) * kChunk + lane * 8 >= K;
       const uint32_t d = ((uint32_t)X.pc[c].y ^ stamp) | ((uint32_t)X.pc[c].w ^ stamp) |
                          ((uint32_t)X.x2[c].y ^ stamp) | ((uint32_t)X.x2[c].w ^ stamp);
@@ -663,7 +670,7 @@ __device__ __forceinline__ bool pro_issue_stamped(ProX &X, CSite &P, int K, int 
   // or RMSNorm site, never the EMUL32 one whose second factor X.x2 holds,
   // and clearing it took 32 moves per site: chained step 1.351 -> 1.344 ms)
 #pragma unroll
-  for (int c = 0; c < kPC; ++c) {
+  for (int c = 0; c < NC; ++c) {
     X.pc[c] = make_int4(X.pc[c].x, X.pc[c].z, X.x2[c].x, X.x2[c].z);
   }
   return ok;
@@ -722,11 +729,13 @@ __device__ __forceinline__ uint32_t pack4(uint32_t a, uint32_t b) {
 // `out` (put_x8 / put_corr), and the site's exports named by `exports` (kExpX8: x8 and
 // e_x; kExpXn: the RMSNorm
 // output); returns e_x.  Chunks past K are skipped.
-template <bool kLds, bool kDep>
+template <bool kLds, bool kDep, int NC = kPC>
 __device__ __forceinline__ int group_prologue(CSite &P, int K, int pro, Lds &L, int8_t *out,
-                                              int exports, int pw, int lane, PSync &ps, ProX &X,
-                                              uint32_t lspin) {
-  if (pro == PRO_X8) {
+                                              int exports, int pw, int lane, PSync &ps,
+                                              ProXN<NC> &X, uint32_t lspin) {
+  // (the int8-input and EMUL32 variants only with every chunk: a site read
+  // through stamped words is a DYNQ8 or RMSNorm site)
+  if constexpr (NC == kPC) if (pro == PRO_X8) {
 #pragma unroll
     for (int c = 0; c < kPX; ++c) {
       const int off = (c * kPW + pw) * 1024 + lane * 16;
@@ -749,7 +758,7 @@ __device__ __forceinline__ int group_prologue(CSite &P, int K, int pro, Lds &L, 
     if ((exports & kExpX8) && P.e_x_out && pw == 0 && lane == 0) *P.e_x_out = P.e_x_given;
     return P.e_x_given;
   }
-  if (kDep && pro == PRO_EMUL_DYNQ8) {
+  if constexpr (NC == kPC) if (kDep && pro == PRO_EMUL_DYNQ8) {
     // ALU EMUL32 at p0 = 12 (gen_layer_script.py:1414-1418): clip16 of the
     // rounded product, then DYNQ8 below.  The second factor of the first
     // half of the chunks came with the inputs; the second half's is loaded
@@ -839,7 +848,7 @@ __device__ __forceinline__ int group_prologue(CSite &P, int K, int pro, Lds &L, 
   }
   u16x2 mx2 = (u16x2)(0);
 #pragma unroll
-  for (int c = 0; c < kPC; ++c)
+  for (int c = 0; c < NC; ++c)
     if ((c * kPW + pw) * kChunk < K) {
       mx2 = __builtin_elementwise_max(mx2, abs2(X.pc[c].x));
       mx2 = __builtin_elementwise_max(mx2, abs2(X.pc[c].y));
@@ -860,7 +869,7 @@ __device__ __forceinline__ int group_prologue(CSite &P, int K, int pro, Lds &L, 
   const u16x2 half2 = (u16x2)((unsigned short)((1 << e) >> 1));
   const u16x2 e2 = (u16x2)((unsigned short)e);
 #pragma unroll
-  for (int c = 0; c < kPC; ++c) {
+  for (int c = 0; c < NC; ++c) {
     const int base = (c * kPW + pw) * kChunk + lane * 8;
     if ((c * kPW + pw) * kChunk < K) {
       const uint32_t lo = pack4(dynq2(X.pc[c].x, half2, e2), dynq2(X.pc[c].y, half2, e2));
@@ -879,6 +888,44 @@ __device__ __forceinline__ int group_prologue(CSite &P, int K, int pro, Lds &L, 
   }
   if ((exports & kExpX8) && P.e_x_out && pw == 0 && lane == 0) *P.e_x_out = e;
   return e;
+}
+
+// A stamped site's prologue for K <= 4608 (every site but the down
+// projections), into LDS buffer b: code for three chunks per wavefront, not
+// eight -- the prologue is a single wavefront's instruction stream, and the
+// eight-chunk code spends most of its instructions on chunks past K (chained
+// step 1.300 -> 1.272 ms, FFN blocks in layer order 0.623 -> 0.620 ms).  A
+// function of its own: inlined, it changed the register allocation of the
+// rest of the kernel (the FFN blocks interleaved 0.460 -> 0.494 ms, though
+// that plan never runs it; 0.467 ms as it is).  The eight-chunk variant
+// stays inlined: out of line it was slower everywhere (chained step 1.353
+// ms).
+struct SmallPro {
+  int e;
+  PSync ps;
+  bool ok;
+};
+template <bool kDep>
+__device__ __noinline__ SmallPro small_prologue(const GemvParams *Parg, int K, int pro,
+                                                uint32_t stamp, int b, int exports, int pw,
+                                                PSync ps, int32_t *err, uint32_t gspin,
+                                                uint32_t lspin) {
+  CSite &P = *(CSite *)uniform_ptr(Parg);
+  K = __builtin_amdgcn_readfirstlane(K);
+  pro = __builtin_amdgcn_readfirstlane(pro);
+  stamp = __builtin_amdgcn_readfirstlane(stamp);
+  b = __builtin_amdgcn_readfirstlane(b);
+  exports = __builtin_amdgcn_readfirstlane(exports);
+  pw = __builtin_amdgcn_readfirstlane(pw);
+  err = (int32_t *)uniform_ptr(err);
+  Lds &L = g_lds;
+  const int lane = lane_now();
+  ProXN<kPS> X;
+  SmallPro r;
+  r.ok = pro_issue_stamped(X, P, K, pro, stamp, pw, lane, err, gspin);
+  r.e = group_prologue<true, kDep, kPS>(P, K, pro, L, L.x[b], exports, pw, lane, ps, X, lspin);
+  r.ps = ps;
+  return r;
 }
 
 // Site s's prologue, by the CU that owns it: inputs, compute, then -- every
@@ -995,7 +1042,7 @@ __device__ __forceinline__ bool wait_weights_past(Lds &L, int t, int lane, uint3
 // an L2 write-back and invalidate to every workgroup's exit.
 // A key is (value ^ 2^31) << 32 | (2^32 - 1 - index): the unsigned maximum is
 // the largest value and, among equal values, the lowest index.
-__device__ void head_arrive(const StreamParams &S, int G, uint64_t best) {
+__device__ __forceinline__ void head_arrive(const StreamParams &S, int G, uint64_t best) {
   const size_t w0 = stream_head_word0(G, S.nsites);
   uint64_t *key = (uint64_t *)(S.done + w0);
   uint32_t *count = S.done + w0 + 2;
@@ -1068,26 +1115,36 @@ __device__ __forceinline__ void prologue_role(const GemvParams *sites_arg, int n
       if (s >= kNB) ok = wait_weights_past(L, s - kNB, lane, lspin) && ok;
       wait_exported<kDep>(sites, L, s - kNB, r, G, lane, lspin, ok);
       ok = lds_wait_ge(&L.gridok, P.fence_at, lspin) && ok;
-      ProX X;
       // the fields the prologue branches on, read before its waits
       int pK = P.K, ppro = P.pro;
+      const int exports = site_owner(s, G) == r ? kExpXn : 0;
+      int e;
       if (P.stamp_src >= 0) {
         // no grid-wide wait: the input's own words say when it is whole.
         // Polled once this CU has stored its own share (a CU that polls
         // while others still stream would only add traffic).
         ok = lds_wait_ge(&L.served, P.stamp_src, lspin) && ok;
-        ok = pro_issue_stamped(X, P, pK, ppro, fbase + (uint32_t)P.stamp_src + 1u, pw, lane, err,
-                               gspin) &&
-             ok;
-      } else {
-        pro_issue<kDep>(X, P, pw, lane);
       }
-      // held in registers across the waits: read again after them, the
-      // fields' scalar loads could miss
-      asm volatile("" : "+s"(pK), "+s"(ppro));
-      const int e = group_prologue<true, kDep>(P, pK, ppro, L, L.x[b],
-                                               site_owner(s, G) == r ? kExpXn : 0, pw, lane, ps, X,
-                                               lspin);
+      if (P.stamp_src >= 0 && pK <= kStampKSmall) {
+        const SmallPro sp = small_prologue<kDep>(sites_arg + s, pK, ppro,
+                                                 fbase + (uint32_t)P.stamp_src + 1u, b, exports,
+                                                 pw, ps, err, gspin, lspin);
+        e = sp.e;
+        ps = sp.ps;
+        ok = sp.ok && ok;
+      } else {
+        ProX X;
+        if (P.stamp_src >= 0)
+          ok = pro_issue_stamped(X, P, pK, ppro, fbase + (uint32_t)P.stamp_src + 1u, pw, lane,
+                                 err, gspin) &&
+               ok;
+        else
+          pro_issue<kDep>(X, P, pw, lane);
+        // held in registers across the waits: read again after them, the
+        // fields' scalar loads could miss
+        asm volatile("" : "+s"(pK), "+s"(ppro));
+        e = group_prologue<true, kDep>(P, pK, ppro, L, L.x[b], exports, pw, lane, ps, X, lspin);
+      }
       if (lane == 0) {
         if (pw == 0) lds_write_i32(&L.ex[b], e);
         lds_write_i32(&L.ready[b][pw], s);
