@@ -735,6 +735,11 @@ __device__ __forceinline__ int group_prologue(CSite &P, int K, int pro, Lds &L, 
                                               ProXN<NC> &X, uint32_t lspin) {
   // (the int8-input and EMUL32 variants only with every chunk: a site read
   // through stamped words is a DYNQ8 or RMSNorm site)
+  // kAll: every chunk is computed, without a branch (its inputs past K read
+  // as zero), so that the compiler interleaves the chunks' instructions; only
+  // in LDS, where chunks past K < 4608 land in the buffer's unused room, and
+  // never with x8 exports (kExpX8), which go to global memory
+  constexpr bool kAll = kLds && NC == kPS;
   if constexpr (NC == kPC) if (pro == PRO_X8) {
 #pragma unroll
     for (int c = 0; c < kPX; ++c) {
@@ -788,7 +793,7 @@ __device__ __forceinline__ int group_prologue(CSite &P, int K, int pro, Lds &L, 
     uint64_t ss = 0;
 #pragma unroll
     for (int c = 0; c < kPN; ++c)
-      if ((c * kPW + pw) * kChunk < K) {
+      if (kAll || (c * kPW + pw) * kChunk < K) {
         const int32_t wd[4] = {X.pc[c].x, X.pc[c].y, X.pc[c].z, X.pc[c].w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -828,7 +833,7 @@ __device__ __forceinline__ int group_prologue(CSite &P, int K, int pro, Lds &L, 
 #pragma unroll
     for (int c = 0; c < kPN; ++c) {
       const int base = (c * kPW + pw) * kChunk + lane * 8;
-      if ((c * kPW + pw) * kChunk < K) {
+      if (kAll || (c * kPW + pw) * kChunk < K) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int32_t xv = piece_get(X.pc[c], j);
@@ -849,7 +854,7 @@ __device__ __forceinline__ int group_prologue(CSite &P, int K, int pro, Lds &L, 
   u16x2 mx2 = (u16x2)(0);
 #pragma unroll
   for (int c = 0; c < NC; ++c)
-    if ((c * kPW + pw) * kChunk < K) {
+    if (kAll || (c * kPW + pw) * kChunk < K) {
       mx2 = __builtin_elementwise_max(mx2, abs2(X.pc[c].x));
       mx2 = __builtin_elementwise_max(mx2, abs2(X.pc[c].y));
       mx2 = __builtin_elementwise_max(mx2, abs2(X.pc[c].z));
@@ -871,7 +876,7 @@ __device__ __forceinline__ int group_prologue(CSite &P, int K, int pro, Lds &L, 
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int base = (c * kPW + pw) * kChunk + lane * 8;
-    if ((c * kPW + pw) * kChunk < K) {
+    if (kAll || (c * kPW + pw) * kChunk < K) {
       const uint32_t lo = pack4(dynq2(X.pc[c].x, half2, e2), dynq2(X.pc[c].y, half2, e2));
       const uint32_t hi = pack4(dynq2(X.pc[c].z, half2, e2), dynq2(X.pc[c].w, half2, e2));
       // -8 * sum of the x8 met by the offset-form low nibbles of one
@@ -879,7 +884,11 @@ __device__ __forceinline__ int group_prologue(CSite &P, int K, int pro, Lds &L, 
       int t4 = __builtin_amdgcn_sdot4((int)lo, 0x01010101, 0, false);
       t4 += __builtin_amdgcn_update_dpp(0, t4, 0xB1, 0xF, 0xF, false);
       t4 += __builtin_amdgcn_update_dpp(0, t4, 0x4E, 0xF, 0xF, false);
-      if (base < K) {
+      if (kAll) {
+        // (chunks past K write zeros into the buffer's unused room)
+        put_x8<kLds>(out, base, lo, hi);
+        if ((lane & 3) == 0) put_corr<kLds>(out, base / 32, -8 * t4);
+      } else if (base < K) {
         put_x8<kLds>(out, base, lo, hi);
         if ((lane & 3) == 0) put_corr<kLds>(out, base / 32, -8 * t4);
         if ((exports & kExpX8) && P.x8_out) *(uint2 *)(P.x8_out + base) = make_uint2(lo, hi);
