@@ -21,12 +21,14 @@
 //    (an LDS flag), never for the other wavefronts.
 //  * 3 prologue wavefronts compute each site's activations (RMSNorm, DYNQ8:
 //    x8, e_x and the offset corrections) ahead of the weight wavefronts,
-//    into a ring of 6 LDS buffers; a buffer is reused once every weight
+//    into a ring of 8 LDS buffers; a buffer is reused once every weight
 //    wavefront has moved past the site that used it.
 //  * 1 control wavefront stores the outputs, which the wavefront completing
 //    a tile stages in LDS, and at a fenced site waits until every workgroup
 //    has stored its outputs of all earlier sites (one flag per workgroup)
-//    before the prologue wavefronts may read that site's activations.
+//    before the prologue wavefronts may read that site's activations.  At a
+//    site whose input is the site it has just stored, it computes a fourth
+//    share of the prologue (ctrl_assists).
 //
 // A tile's 16 rows are complete when every weight wavefront holding one of
 // its blocks has added its partial sums into an LDS slot; the wavefront
@@ -52,6 +54,9 @@ constexpr int kCtrl = kCW;                  // the control wavefront
 constexpr int kPW = 3;                      // prologue wavefronts
 constexpr int kPW0 = kCW + 1;               // ... 9..11
 constexpr int kThreads = (kPW0 + kPW) * 64; // 768
+constexpr int kPR = kPW + 1;                // ready flags per buffer: the prologue
+                                            // wavefronts and the control wavefront
+static_assert((kPR & (kPR - 1)) == 0, "a lane picks its flag with a mask");
 constexpr int kNB = 8;                      // activation buffers (a power of 2)
 constexpr int kExpX8 = 1;                   // a prologue's exports: x8 and e_x ...
 constexpr int kExpXn = 2;                   // ... the RMSNorm output
@@ -83,8 +88,9 @@ struct __align__(16) Lds {
   int32_t tcnt[kTSlots];            // contributions added to the slot
   int32_t tgen[kTSlots];            // tile number the slot is open for
   int32_t tready[kTSlots];          // tile number + 1 once its outputs are staged
-  int32_t ready[kNB][kPW];          // per prologue wavefront: the site whose activations it
-                                    // has written into the buffer (-1: none)
+  int32_t ready[kNB][kPR];          // per prologue wavefront (and the control wavefront
+                                    // last): the site whose activations it has written
+                                    // into the buffer (-1: none)
   int32_t ex[kNB];                  // ... and its e_x
   int32_t wsite[kCW];               // site each weight wavefront works on (nsites: done)
   int32_t gridok;                   // last fenced site whose grid-wide wait has passed
@@ -93,12 +99,13 @@ struct __align__(16) Lds {
   int16_t pairv[kPairTiles][kTileRows];  // paired site: job 0's outputs of this CU's tiles
   int16_t prod[kTileRows];          // ... and one tile's EMUL32 products
   int32_t psync[kPW];               // prologue wavefronts' barrier phases
+  int32_t psync4[kPR];              // ... with the control wavefront (site-numbered phases)
   int32_t abort;                    // set by the first LDS wait that gives up
   int32_t err;                      // error bits found inside the workgroup
   uint16_t rsqrt[512];
   uint16_t sig[264];
-  int64_t pss[kPW];                 // prologue partial sums of squares
-  int32_t pmx[kPW];                 // prologue partial maxima
+  int64_t pss[kPR];                 // prologue partial sums of squares
+  int32_t pmx[kPR];                 // prologue partial maxima
   uint64_t best;                    // argmax key of the head's rows seen here (0: none)
   uint64_t tkbuf[128];              // TOPK-32 head: the scan's key buffer ...
   int32_t tkrows[tk::kTkRows];      // ... and its chunk's values (prologue wavefront 0)
@@ -534,14 +541,19 @@ struct PSync {
   int32_t ok;
 };
 
-// barrier of the 3 prologue wavefronts only (bounded), through L.psync
+// barrier of the 3 prologue wavefronts only (bounded), through L.psync;
+// with NP = kPR also the control wavefront, through L.psync4, whose phases
+// the caller numbers by site (the control wavefront takes part in some
+// sites' prologues only)
+template <int NP = kPW>
 __device__ __forceinline__ void psync(Lds &L, PSync &ps, int pw, int lane, uint32_t lspin) {
+  int32_t *f = NP == kPW ? L.psync : L.psync4;
   ++ps.phase;
   wait_lds();
-  if (lane == 0) lds_write_i32(&L.psync[pw], ps.phase);
+  if (lane == 0) lds_write_i32(&f[pw], ps.phase);
   bool done = false;
   for (uint32_t n = 0; n < lspin && !done; ++n)
-    done = __all(lds_read_i32(&L.psync[lane % kPW]) >= ps.phase);
+    done = __all(lds_read_i32(&f[lane % NP]) >= ps.phase);
   ps.ok = ps.ok && done;
 }
 
@@ -628,7 +640,7 @@ __device__ __forceinline__ void pro_issue(ProX &X, CSite &P, int pw, int lane) {
 // word of the wavefront carries the stamp; then X.pc[c] holds the chunk's
 // 8 int16.  The RMSNorm weights are loaded first, as in pro_issue.
 // Bounded: false if the words never all arrived (err bit 1).
-template <int NC>
+template <int NC, int NP = kPW>
 __device__ __forceinline__ bool pro_issue_stamped(ProXN<NC> &X, CSite &P, int K, int pro,
                                                   uint32_t stamp, int pw, int lane, int32_t *err,
                                                   uint32_t gspin) {
@@ -636,7 +648,7 @@ __device__ __forceinline__ bool pro_issue_stamped(ProXN<NC> &X, CSite &P, int K,
   const __amdgpu_buffer_rsrc_t rw =
       __builtin_amdgcn_make_buffer_rsrc((void *)P.norm_w, (short)0, wlen, kBufDword3);
 #pragma unroll
-  for (int c = 0; c < kPN; ++c) X.wv[c] = vec_load(rw, ((c * kPW + pw) * kChunk + lane * 8) * 2);
+  for (int c = 0; c < kPN; ++c) X.wv[c] = vec_load(rw, ((c * NP + pw) * kChunk + lane * 8) * 2);
   // words past K are out of the buffer's range: they read as zero, so a
   // lane whose 8 elements lie past K (K % 8 == 0) takes them as arrived --
   // per lane, since K need not fill a chunk
@@ -647,7 +659,7 @@ __device__ __forceinline__ bool pro_issue_stamped(ProXN<NC> &X, CSite &P, int K,
     if (n > 0) __builtin_amdgcn_s_sleep(2);
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const int off = ((c * kPW + pw) * kChunk + lane * 8) * 4;
+      const int off = ((c * NP + pw) * kChunk + lane * 8) * 4;
       X.pc[c] = vec_load(rx, off);
       X.x2[c] = vec_load(rx, off + 16);
     }
@@ -658,7 +670,7 @@ __device__ __forceinline__ bool pro_issue_stamped(ProXN<NC> &X, CSite &P, int K,
     uint32_t bad = 0;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const bool past = (c * kPW + pw) * kChunk + lane * 8 >= K;
+      const bool past = (c * NP + pw) * kChunk + lane * 8 >= K;
       const uint32_t d = ((uint32_t)X.pc[c].y ^ stamp) | ((uint32_t)X.pc[c].w ^ stamp) |
                          ((uint32_t)X.x2[c].y ^ stamp) | ((uint32_t)X.x2[c].w ^ stamp);
       bad |= past ? 0u : d;
@@ -729,7 +741,7 @@ __device__ __forceinline__ uint32_t pack4(uint32_t a, uint32_t b) {
 // `out` (put_x8 / put_corr), and the site's exports named by `exports` (kExpX8: x8 and
 // e_x; kExpXn: the RMSNorm
 // output); returns e_x.  Chunks past K are skipped.
-template <bool kLds, bool kDep, int NC = kPC>
+template <bool kLds, bool kDep, int NC = kPC, int NP = kPW>
 __device__ __forceinline__ int group_prologue(CSite &P, int K, int pro, Lds &L, int8_t *out,
                                               int exports, int pw, int lane, PSync &ps,
                                               ProXN<NC> &X, uint32_t lspin) {
@@ -739,12 +751,14 @@ __device__ __forceinline__ int group_prologue(CSite &P, int K, int pro, Lds &L, 
   // as zero), so that the compiler interleaves the chunks' instructions; only
   // in LDS, where chunks past K < 4608 land in the buffer's unused room, and
   // never with x8 exports (kExpX8), which go to global memory
-  constexpr bool kAll = kLds && NC == kPS;
+  static_assert(NC != kPC || NP == kPW, "every chunk: the prologue wavefronts only");
+  constexpr bool kAll = kLds && NC <= kPS;
+  constexpr int kRN = NC < kPN ? NC : kPN;   // RMSNorm chunks held
   if constexpr (NC == kPC) if (pro == PRO_X8) {
 #pragma unroll
     for (int c = 0; c < kPX; ++c) {
-      const int off = (c * kPW + pw) * 1024 + lane * 16;
-      if ((c * kPW + pw) * 1024 < K) {
+      const int off = (c * NP + pw) * 1024 + lane * 16;
+      if ((c * NP + pw) * 1024 < K) {
         const int4 v = X.pc[c];
         // -8 * sum of the x8 met by the offset-form low nibbles of a
         // 32-byte (group, quarter): bytes 0-3 and 8-11 of each lane's 16,
@@ -774,7 +788,7 @@ __device__ __forceinline__ int group_prologue(CSite &P, int K, int pro, Lds &L, 
 #pragma unroll
       for (int i = 0; i < kPC2; ++i) {
         const int c = h * kPC2 + i;
-        if ((c * kPW + pw) * kChunk < K) {
+        if ((c * NP + pw) * kChunk < K) {
           const int4 a = X.x2[2 * i], b = X.x2[2 * i + 1];
           const int32_t av[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
@@ -792,8 +806,8 @@ __device__ __forceinline__ int group_prologue(CSite &P, int K, int pro, Lds &L, 
     // sum of squares: a pair's a^2 + b^2 <= 2^31 is exact as a uint32
     uint64_t ss = 0;
 #pragma unroll
-    for (int c = 0; c < kPN; ++c)
-      if (kAll || (c * kPW + pw) * kChunk < K) {
+    for (int c = 0; c < kRN; ++c)
+      if (kAll || (c * NP + pw) * kChunk < K) {
         const int32_t wd[4] = {X.pc[c].x, X.pc[c].y, X.pc[c].z, X.pc[c].w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -803,10 +817,10 @@ __device__ __forceinline__ int group_prologue(CSite &P, int K, int pro, Lds &L, 
       }
     ss = wave_sum_u64(ss);
     if (lane == 0) L.pss[pw] = (int64_t)ss;
-    psync(L, ps, pw, lane, lspin);
+    psync<NP>(L, ps, pw, lane, lspin);
     ss = 0;
 #pragma unroll
-    for (int w = 0; w < kPW; ++w) ss += (uint64_t)L.pss[w];
+    for (int w = 0; w < NP; ++w) ss += (uint64_t)L.pss[w];
     if (ss == 0) ss = 1;
     int64_t r;
     int e;
@@ -831,9 +845,9 @@ __device__ __forceinline__ int group_prologue(CSite &P, int K, int pro, Lds &L, 
     const double dhalf = s1 > 0 ? 0.5 : 0.0;
     const double drs = dr * dscale;   // exact: a power-of-2 scaling
 #pragma unroll
-    for (int c = 0; c < kPN; ++c) {
-      const int base = (c * kPW + pw) * kChunk + lane * 8;
-      if (kAll || (c * kPW + pw) * kChunk < K) {
+    for (int c = 0; c < kRN; ++c) {
+      const int base = (c * NP + pw) * kChunk + lane * 8;
+      if (kAll || (c * NP + pw) * kChunk < K) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int32_t xv = piece_get(X.pc[c], j);
@@ -854,7 +868,7 @@ __device__ __forceinline__ int group_prologue(CSite &P, int K, int pro, Lds &L, 
   u16x2 mx2 = (u16x2)(0);
 #pragma unroll
   for (int c = 0; c < NC; ++c)
-    if (kAll || (c * kPW + pw) * kChunk < K) {
+    if (kAll || (c * NP + pw) * kChunk < K) {
       mx2 = __builtin_elementwise_max(mx2, abs2(X.pc[c].x));
       mx2 = __builtin_elementwise_max(mx2, abs2(X.pc[c].y));
       mx2 = __builtin_elementwise_max(mx2, abs2(X.pc[c].z));
@@ -863,10 +877,10 @@ __device__ __forceinline__ int group_prologue(CSite &P, int K, int pro, Lds &L, 
   int32_t mx = max((int32_t)mx2.x, (int32_t)mx2.y);
   mx = wave_max_i32(mx);
   if (lane == 0) L.pmx[pw] = mx;
-  psync(L, ps, pw, lane, lspin);
+  psync<NP>(L, ps, pw, lane, lspin);
   mx = 0;
 #pragma unroll
-  for (int w = 0; w < kPW; ++w) mx = max(mx, L.pmx[w]);
+  for (int w = 0; w < NP; ++w) mx = max(mx, L.pmx[w]);
   // fixedpoint.py:24-33: the least e with rshift_round(max, e) <= 127 is
   // bitlen(max) - 7, or one more when rounding carries past 127
   int e = mx > 127 ? 25 - __clz(mx) : 0;
@@ -875,8 +889,8 @@ __device__ __forceinline__ int group_prologue(CSite &P, int K, int pro, Lds &L, 
   const u16x2 e2 = (u16x2)((unsigned short)e);
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    const int base = (c * kPW + pw) * kChunk + lane * 8;
-    if (kAll || (c * kPW + pw) * kChunk < K) {
+    const int base = (c * NP + pw) * kChunk + lane * 8;
+    if (kAll || (c * NP + pw) * kChunk < K) {
       const uint32_t lo = pack4(dynq2(X.pc[c].x, half2, e2), dynq2(X.pc[c].y, half2, e2));
       const uint32_t hi = pack4(dynq2(X.pc[c].z, half2, e2), dynq2(X.pc[c].w, half2, e2));
       // -8 * sum of the x8 met by the offset-form low nibbles of one
@@ -914,11 +928,11 @@ struct SmallPro {
   PSync ps;
   bool ok;
 };
-template <bool kDep>
+template <bool kDep, int NC = kPS, int NP = kPW>
 __device__ __noinline__ SmallPro small_prologue(const GemvParams *Parg, int K, int pro,
                                                 uint32_t stamp, int b, int exports, int pw,
                                                 PSync ps, int32_t *err, uint32_t gspin,
-                                                uint32_t lspin) {
+                                                uint32_t lspin, int s) {
   CSite &P = *(CSite *)uniform_ptr(Parg);
   K = __builtin_amdgcn_readfirstlane(K);
   pro = __builtin_amdgcn_readfirstlane(pro);
@@ -927,14 +941,42 @@ __device__ __noinline__ SmallPro small_prologue(const GemvParams *Parg, int K, i
   exports = __builtin_amdgcn_readfirstlane(exports);
   pw = __builtin_amdgcn_readfirstlane(pw);
   err = (int32_t *)uniform_ptr(err);
+  s = __builtin_amdgcn_readfirstlane(s);
   Lds &L = g_lds;
   const int lane = lane_now();
-  ProXN<kPS> X;
+  ProXN<NC> X;
   SmallPro r;
-  r.ok = pro_issue_stamped(X, P, K, pro, stamp, pw, lane, err, gspin);
-  r.e = group_prologue<true, kDep, kPS>(P, K, pro, L, L.x[b], exports, pw, lane, ps, X, lspin);
-  r.ps = ps;
+  r.ok = pro_issue_stamped<NC, NP>(X, P, K, pro, stamp, pw, lane, err, gspin);
+  if (NP == kPW) {
+    r.e = group_prologue<true, kDep, NC, NP>(P, K, pro, L, L.x[b], exports, pw, lane, ps, X,
+                                             lspin);
+    r.ps = ps;
+  } else {
+    // with the control wavefront: barrier phases 2s + 1, 2s + 2 of site s
+    PSync p4{2 * s, 1};
+    r.e = group_prologue<true, kDep, NC, NP>(P, K, pro, L, L.x[b], exports, pw, lane, p4, X,
+                                             lspin);
+    r.ps = ps;
+    r.ok = r.ok && p4.ok;
+  }
   return r;
+}
+
+// The control wavefront computes a share of site s's prologue with the
+// three prologue wavefronts (two chunks of 512 elements each of the four,
+// for K <= 4096, instead of three chunks each of the three) when it is idle
+// then: in a dependent plan, at a site whose stamped input is the site just
+// before it, whose outputs this CU's control wavefront has then just stored
+// (and whose other CUs' outputs the prologue waits for anyway).  Chained
+// step 1.235 -> 1.202 ms, FFN blocks in layer order 0.617 -> 0.621 ms and
+// interleaved 0.467 -> 0.471 ms (plans that never run it: the code moved);
+// the weight wavefronts wait for the fourth flag at such sites only (the
+// prologue wavefronts posting it at every other site cost the FFN blocks
+// 0.617 -> 0.630 ms).
+constexpr int kAssistKMax = 2 * kPR * kChunk;   // 4096
+template <bool kDep>
+__device__ __forceinline__ bool ctrl_assists(CSite &P, int s) {
+  return kDep && P.local_pro && P.stamp_src >= 0 && P.stamp_src == s - 1 && P.K <= kAssistKMax;
 }
 
 // Site s's prologue, by the CU that owns it: inputs, compute, then -- every
@@ -1015,9 +1057,13 @@ __device__ __forceinline__ void load_staged(const int8_t *stg, int8_t *xb, int K
 // their SIMDs with the prologue wavefronts that compute the activations, and
 // polling every 64 cycles slowed those (the chained step by 4 %, the
 // independent one by 2 %); 2,000 cycles was slower again on the chained step.
-__device__ __forceinline__ void wait_ready(Lds &L, int b, int s, int lane, uint32_t lspin) {
+// (with_ctrl: the control wavefront has a share of the site's prologue, and
+// its flag counts too)
+__device__ __forceinline__ void wait_ready(Lds &L, int b, int s, int lane, uint32_t lspin,
+                                           bool with_ctrl) {
+  const int f = with_ctrl ? (lane & (kPR - 1)) : lane % kPW;
   for (uint32_t n = 0;; ++n) {
-    if (__all(lds_read_i32(&L.ready[b][lane % kPW]) == s)) break;
+    if (__all(lds_read_i32(&L.ready[b][f]) == s)) break;
     if (lds_read_i32(&L.abort) != 0) break;
     if (n > lspin) {
       if (lane == 0) {
@@ -1069,11 +1115,9 @@ __device__ __forceinline__ void head_arrive(const StreamParams &S, int G, uint64
 }
 
 // The prologue wavefronts' program: every site's activations, in order,
-// into the LDS ring.  A function of its own, not inlined: its code (the
-// RMSNorm, EMUL32 and DYNQ8 variants, staged and local) would otherwise share
-// one register allocation and layout with the weight wavefronts' loop, which
-// measured slower on the independent-input stream although none of it runs
-// there.  Arguments are made wavefront-uniform, so table reads stay scalar.
+// into the LDS ring.  Inlined into the kernel (the three-chunk stamped
+// prologue excepted, see small_prologue); the arguments are made
+// wavefront-uniform, so table reads stay scalar.
 template <bool kDep>
 __device__ __forceinline__ void prologue_role(const GemvParams *sites_arg, int nsites, int r,
                                            int G, int wave, uint32_t *done, int8_t *stage,
@@ -1134,10 +1178,14 @@ __device__ __forceinline__ void prologue_role(const GemvParams *sites_arg, int n
         // while others still stream would only add traffic).
         ok = lds_wait_ge(&L.served, P.stamp_src, lspin) && ok;
       }
+      const bool assisted = ctrl_assists<kDep>(P, s);
       if (P.stamp_src >= 0 && pK <= kStampKSmall) {
-        const SmallPro sp = small_prologue<kDep>(sites_arg + s, pK, ppro,
-                                                 fbase + (uint32_t)P.stamp_src + 1u, b, exports,
-                                                 pw, ps, err, gspin, lspin);
+        const uint32_t stamp = fbase + (uint32_t)P.stamp_src + 1u;
+        const SmallPro sp =
+            assisted ? small_prologue<kDep, 2, kPR>(sites_arg + s, pK, ppro, stamp, b, exports,
+                                                    pw, ps, err, gspin, lspin, s)
+                     : small_prologue<kDep>(sites_arg + s, pK, ppro, stamp, b, exports, pw, ps,
+                                            err, gspin, lspin, s);
         e = sp.e;
         ps = sp.ps;
         ok = sp.ok && ok;
@@ -1316,7 +1364,7 @@ __device__ __forceinline__ void weight_role(const GemvParams *sites_arg, int nsi
       // done with every earlier site; wait for this one's activations
       s_cur = c.s;
       lds_write_i32(&L.wsite[wave], s_cur);
-      wait_ready(L, s_cur % kNB, s_cur, lane_s, lspin);
+      wait_ready(L, s_cur % kNB, s_cur, lane_s, lspin, ctrl_assists<kDep>(sites[s_cur], s_cur));
       e_x = __builtin_amdgcn_readfirstlane(lds_read_i32(&L.ex[s_cur % kNB]));
       contributors = min(c.nblk, kCW);
     }
@@ -1389,9 +1437,10 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
     L.tgen[tid] = tid;
     L.tready[tid] = 0;
   }
-  if (tid < kNB * kPW) (&L.ready[0][0])[tid] = -1;
+  if (tid < kNB * kPR) (&L.ready[0][0])[tid] = -1;
   if (tid < kCW) L.wsite[tid] = 0;
   if (tid < kPW) L.psync[tid] = 0;
+  if (tid < kPR) L.psync4[tid] = 0;
   if (tid == 0) {
     L.served = -1;
     L.xdone = -1;
@@ -1420,7 +1469,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
         // this CU poll for the next site's input; once the site's prologue
         // is done here (a CU with no tile of the site has not waited for it)
         const int b = s % kNB;
-        wait_ready(L, b, s, lane, lspin);
+        wait_ready(L, b, s, lane, lspin, ctrl_assists<kDep>(P, s));
         if (P.x8_out)
           for (int off = 16 * lane; off < P.K; off += 1024)
             *(int4 *)(P.x8_out + off) = *(const int4 *)(L.x[b] + off);
@@ -1434,6 +1483,23 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(StreamParams S,
         if (lane == 0) store_coherent(S.done + r, v);
         grid_wait(S.done, G, v, lane, S.err, gspin);
         if (lane == 0) lds_write_i32(&L.gridok, s + 1);
+      }
+      if (s + 1 < nsites && ctrl_assists<kDep>(sites[s + 1], s + 1)) {
+        // this wavefront's share of the next site's prologue (its input is
+        // the site just stored); its buffer is free once every weight
+        // wavefront has left the site that used it last (this wavefront's
+        // own exports of that site are done)
+        const int t = s + 1, b = t % kNB;
+        CSite &Q = sites[t];
+        bool aok = t < kNB || wait_weights_past(L, t - kNB, lane, lspin);
+        const SmallPro sp = small_prologue<kDep, 2, kPR>(
+            sites_arg + t, Q.K, Q.pro, fbase + (uint32_t)t, b, site_owner(t, G) == r ? kExpXn : 0,
+            kPW, PSync{0, 1}, S.err, gspin, lspin, t);
+        aok = aok && sp.ok;
+        if (lane == 0) {
+          lds_write_i32(&L.ready[b][kPW], t);
+          if (!aok) lds_or_i32(&L.err, 4);
+        }
       }
     }
   } else if (wave >= kPW0) {
