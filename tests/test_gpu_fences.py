@@ -106,11 +106,16 @@ def test_dependent_sites(engine, mode, fences):
                                     (640, N.PRO_DYNQ8), (1152, N.PRO_DYNQ8),
                                     (2048, N.PRO_RMSNORM_DYNQ8)])
 @pytest.mark.parametrize("mode", [N.PLAN_PERSISTENT, N.PLAN_PERSISTENT_COOP])
-def test_stamped_sites_any_k(engine, kb, pro, mode):
+@pytest.mark.parametrize("gap", [False, True])
+def test_stamped_sites_any_k(engine, kb, pro, mode, gap):
     """Sites reading an earlier site's output through stamped words when
     that output (the reader's K) does not fill the prologue's 512-element
     chunks: A (kb rows) -> B (K = kb) -> LM head (K = 256), each waiting for
-    the words of the one before, bit-exact against the oracle."""
+    the words of the one before, bit-exact against the oracle.  Reading the
+    site just before it, a site's prologue is shared with the control
+    wavefront (four wavefronts); with `gap`, an independent site C sits
+    between A and B, and B's prologue runs on the three prologue wavefronts
+    alone."""
     from fable5_llm_amd.engine import Plan
     dev = torch.device("cuda", 0)
     gen = torch.Generator(device=dev)
@@ -136,11 +141,17 @@ def test_stamped_sites_any_k(engine, kb, pro, mode):
     nwB = S.synth_norm_w(gen, kb, True) if pro == N.PRO_RMSNORM_DYNQ8 else None
     outB = torch.full((256,), 0x5A5A, dtype=torch.int16, device=dev)
     wH, iH = mat(512, 256)
+    wC, iC = mat(256, 256)
+    xC = S.synth_x16(gen, 256, S.RS_F)
+    outC = torch.full((256,), 0x5A5A, dtype=torch.int16, device=dev)
     res = torch.zeros(2, dtype=torch.int32, device=dev)
     p0A = 15 - S.E_SCALE - S.sh_for_k(K)
     p0B = 15 - S.E_SCALE - S.sh_for_k(kb)
+    p0C = 15 - S.E_SCALE - S.sh_for_k(256)
     plan = Plan(engine)
     plan.add_site([wA], [I16], [p0A], [outA], xA, prologue=N.PRO_DYNQ8, in_f=S.RS_F)
+    if gap:
+        plan.add_site([wC], [I16], [p0C], [outC], xC, prologue=N.PRO_DYNQ8, in_f=S.RS_F)
     plan.add_site([wB], [I16], [p0B], [outB], outA, prologue=pro, norm_w=nwB, in_f=S.RS_F,
                   one_plus=True)
     plan.add_head(wH, outB, res, prologue=N.PRO_DYNQ8)
@@ -155,9 +166,12 @@ def test_stamped_sites_any_k(engine, kb, pro, mode):
         refB = law.movy(yB, p0B - eB, law.MOVY_INT16)
         yH, _ = ref(iH, 512, 256, np.asarray(refB, np.int16), N.PRO_DYNQ8)
         refH = tuple(int(v) for v in law.amax32(yH))
+        yC, eC = ref(iC, 256, 256, xC.cpu().numpy(), N.PRO_DYNQ8)
+        refC = law.movy(yC, p0C - eC, law.MOVY_INT16)
         for rep in range(2):
             outA.fill_(0x5A5A)
             outB.fill_(0x5A5A)
+            outC.fill_(0x5A5A)
             res.zero_()
             torch.cuda.synchronize()
             plan.run()
@@ -166,8 +180,11 @@ def test_stamped_sites_any_k(engine, kb, pro, mode):
                                   np.asarray(refA, np.int64)), rep
             assert np.array_equal(outB.cpu().numpy().astype(np.int64),
                                   np.asarray(refB, np.int64)), rep
+            if gap:
+                assert np.array_equal(outC.cpu().numpy().astype(np.int64),
+                                      np.asarray(refC, np.int64)), rep
             assert tuple(res.cpu().numpy().tolist()) == refH, rep
     finally:
         plan.close()
-        for w in (wA, wB, wH):
+        for w in (wA, wB, wC, wH):
             w.free()
