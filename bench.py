@@ -178,7 +178,7 @@ def batched_leg(st, ctx, batches, steps, warmup, seed):
       * one w4a8_matmul_y32_multi_async launch per site (a layer's gate and
         up share their tokens' x8 and one launch; its down takes another:
         64 launches per pass), for comparison.
-    Returns the timings and, for the checker, layer 0's inputs and the
+    Returns the timings and, for the oracle comparison, layer 0's inputs and the
     plan's outputs."""
     import numpy as np
     import torch
@@ -247,7 +247,7 @@ def batched_leg(st, ctx, batches, steps, warmup, seed):
                                           "value": round(gbs_site, 1), "timing": how_site,
                                           "pct_of_peak_hbm":
                                               round(100.0 * gbs_site / PEAK_HBM_GBS, 1)}})
-        # layer 0's gate, up and down from the plan's last run, for the checker
+        # layer 0's gate, up and down from the plan's last run, for the oracle comparison
         plan.run()
         ctx.sync()
         for si, mi in ffn[:3]:
@@ -269,7 +269,7 @@ def ffn_leg(st, ctx, steps, warmup):
         gate and up site (the product is complete before it is needed);
       * w4a8_mlp_async per layer (two launches each), as one HIP graph.
     Every layer's block output and residual must be identical across the
-    three.  Returns the timings and, for the checker, layer 0's input and
+    three.  Returns the timings and, for the oracle comparison, layer 0's input and
     outputs."""
     import torch
     from fable5_llm_amd import _native as N
@@ -486,7 +486,7 @@ def topk_step_leg(st, ctx, stream, args, ms_argmax):
     """The headline step with its LM head ending in TOPK-32 instead of the
     argmax (a sampling step): the same resident weights and inputs, one
     persistent launch whose TOPK-32 scan runs as the head's rows are
-    stored.  Returns the stream (for the checker) and its figures."""
+    stored.  Returns the stream (for the oracle comparison) and its figures."""
     from fable5_llm_amd import _native as N
     from fable5_llm_amd import stream9b
     stt = stream9b.Stream9B(ctx, seed=args.seed, mode=N.PLAN_PERSISTENT, fences=N.FENCE_AUTO,

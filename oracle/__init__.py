@@ -2,8 +2,8 @@
 
 Nothing in the product package (`fable5_llm_amd`) imports this package.  Only
 `tests/`, `__graft_entry__.smoke()` and the `cpu_baseline` leg of `bench.py`
-may use it, and only as the checker or as the timed CPU baseline, never as a
-fallback for the HIP path.
+may use it, and only to check results against or as the timed CPU
+baseline, never as a fallback for the HIP path.
 
 Contents
   law.py     numpy restatement of the reference's integer law (each function

@@ -1,5 +1,6 @@
-"""ctypes loader for oracle/law_c.c -- TEST INFRASTRUCTURE (the checker and
-the multi-threaded CPU baseline; never a product fallback)."""
+"""ctypes loader for oracle/law_c.c -- TEST INFRASTRUCTURE (expected
+results in tests and the multi-threaded CPU baseline; never a product
+fallback)."""
 import ctypes
 import os
 
