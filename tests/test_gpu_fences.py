@@ -104,7 +104,8 @@ def test_dependent_sites(engine, mode, fences):
 
 @pytest.mark.parametrize("kb,pro", [(128, N.PRO_RMSNORM_DYNQ8), (256, N.PRO_DYNQ8),
                                     (640, N.PRO_DYNQ8), (1152, N.PRO_DYNQ8),
-                                    (2048, N.PRO_RMSNORM_DYNQ8)])
+                                    (2048, N.PRO_RMSNORM_DYNQ8), (4224, N.PRO_DYNQ8),
+                                    (5248, N.PRO_DYNQ8)])
 @pytest.mark.parametrize("mode", [N.PLAN_PERSISTENT, N.PLAN_PERSISTENT_COOP])
 @pytest.mark.parametrize("gap", [False, True])
 def test_stamped_sites_any_k(engine, kb, pro, mode, gap):
@@ -115,7 +116,9 @@ def test_stamped_sites_any_k(engine, kb, pro, mode, gap):
     site just before it, a site's prologue is shared with the control
     wavefront (four wavefronts); with `gap`, an independent site C sits
     between A and B, and B's prologue runs on the three prologue wavefronts
-    alone."""
+    alone.  K = 4224 takes the three-chunk prologue past K = 4096 (the
+    control wavefront's share stops there), its ninth chunk a quarter full;
+    K = 5248 the eight-chunk prologue with its chunks past K skipped."""
     from fable5_llm_amd.engine import Plan
     dev = torch.device("cuda", 0)
     gen = torch.Generator(device=dev)
